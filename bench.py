@@ -1,0 +1,217 @@
+#!/usr/bin/env python3
+"""Benchmark of the PowerSparse hot path on one MI355X.
+
+One step = one pass of the hot path over the synthetic BASELINE graph (config
+C1 by default: Chung-Lu n = 1e6, gamma 2.1, mean degree 50, degree clip 5e4,
+values U(0,1); C2's SDDMM uses the same pattern): SpMM at N = 32, SpMM at
+N = 128 and SDDMM at N = 128, each one fused launch covering every workset,
+enqueued back to back on one stream with the operands resident in HBM. The
+outputs are not cleared between calls, as in the reference harness
+(benchmarks/benchmark.cu:179-187).
+
+Prints one JSON line: value = total FLOP of the timed steps (2 * nnz * N per
+operator, benchmark.cu:189) / wall time between two events, in GFLOPS; the
+`roofline` object is for the dominant kernel (algorithmic bytes per launch /
+its mean launch time, HIP events on its stream); `cpu_baseline` is the OpenMP
+double-precision restatement of the reference's check path (the oracle) timed
+on this host over the same graph and operators.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C1]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "SpMM/SDDMM GFLOPS + achieved HBM GB/s (% of roofline), N=32/128, 1 GPU"
+HBM_PEAK_GBPS = 8000.0
+WORKLOADS = {
+    "C1": "C1/C2 power-law graph (Chung-Lu n=1e6, gamma 2.1, mean 50, clip 5e4): "
+          "SpMM N=32 + SpMM N=128 + SDDMM N=128",
+    "C3": "C3 power-law graph (Chung-Lu n=1.6e6, gamma 1.8, mean 165, clip 1e5): "
+          "SpMM N=32 + SpMM N=128 + SDDMM N=128",
+    "C4": "C4 community graph (2048 x 1024 nodes, 2% intra, +8 inter, 5% empty, 5% singleton): "
+          "SpMM N=64 + SDDMM N=64",
+}
+OPS = {"C1": [("spmm", 32), ("spmm", 128), ("sddmm", 128)],
+       "C3": [("spmm", 32), ("spmm", 128), ("sddmm", 128)],
+       "C4": [("spmm", 64), ("sddmm", 64)]}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(op, nnz, rows, cols, n):
+    """Compulsory HBM traffic of one call: every array touched once."""
+    if op == "spmm":  # values + columns, row extents, B read, C written
+        return 8 * nnz + 4 * (rows + 1) + 4 * n * cols + 4 * n * rows
+    return 12 * nnz + 4 * (rows + 1) + 4 * n * rows + 4 * n * cols  # + outputs
+
+
+def cpu_baseline(csr, host_ops, reps=3):
+    """Times the oracle (OpenMP, double accumulation) on the same workload."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    threads = oracle.max_threads()
+    rows_as_groups = np.arange(csr.rows, dtype=np.int32)
+
+    def run():
+        for op, n, a, b in host_ops:
+            if op == "spmm":
+                oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, n, a)
+            else:
+                oracle.sddmm(rows_as_groups, csr.row_ptr, csr.col_ind, csr.values, n, a, b)
+
+    run()  # warm-up
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t)
+    return float(np.median(times)), threads
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C1", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only (the operators run on one device; "
+              "multi-GPU sharding is a design note, not part of this build). Use --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import powersparse_amd as ps
+
+    ps.set_device(0)
+    props = ps.device_props(0)
+    log(f"device: {props['name']} {props['arch']} CUs={props['cu_count']}")
+    t = time.perf_counter()
+    csr = ps.synth(args.config, seed=1)
+    gen_s = time.perf_counter() - t
+    nnz, rows, cols = csr.nnz, csr.rows, csr.cols
+    log(f"graph {args.config}: rows={rows} nnz={nnz} (generated in {gen_s:.1f} s)")
+
+    ps.synchronize()
+    t = time.perf_counter()
+    m = ps.PowerSparseMatrixGPU.from_csr(csr)
+    ps.synchronize()
+    preprocess_ms = (time.perf_counter() - t) * 1e3
+    S = m.GroupTypeNum()
+    log(f"preprocess {preprocess_ms:.1f} ms: S={S} groups={m.GroupNum()} L={m.SignatureLen()}")
+
+    stream = ps.Stream()
+    ops = []
+    seed = 100
+    sizes = m.sddmm_output_sizes()
+    for op, n in OPS[args.config]:
+        seed += 1
+        if op == "spmm":
+            B = ps.DeviceBuffer(cols * n * 4)
+            ps.fill_random(B, cols * n, seed, -1.0, 1.0, stream=stream)
+            C = ps.DeviceBuffer(rows * n * 4)
+            C.zero(stream)
+            ops.append(dict(op=op, N=n, bufs=(B, C),
+                            call=lambda n=n, B=B, C=C: ps.SpMMAsync(m, n, B, C, stream)))
+        else:
+            X = ps.DeviceBuffer(rows * n * 4)
+            Y = ps.DeviceBuffer(cols * n * 4)
+            ps.fill_random(X, rows * n, seed, 0.0, 1.0, normal=True, stream=stream)
+            ps.fill_random(Y, cols * n, seed + 50, 0.0, 1.0, normal=True, stream=stream)
+            outs = [ps.DeviceBuffer(max(sz, 1) * 4) for sz in sizes]
+            for o in outs:
+                o.zero(stream)
+            ops.append(dict(op=op, N=n, bufs=(X, Y, outs),
+                            call=lambda n=n, X=X, Y=Y, outs=outs: ps.SDDMMAsync(m, n, X, Y, outs,
+                                                                                stream)))
+    stream.synchronize()
+
+    for _ in range(args.warmup):
+        for o in ops:
+            o["call"]()
+    stream.synchronize()
+
+    K = args.steps
+    marks = [[ps.Event() for _ in range(len(ops) + 1)] for _ in range(K)]
+    start, stop = ps.Event(), ps.Event()
+    ps.synchronize()
+    start.record(stream)
+    for k in range(K):
+        marks[k][0].record(stream)
+        for i, o in enumerate(ops):
+            o["call"]()
+            marks[k][i + 1].record(stream)
+    stop.record(stream)
+    stop.synchronize()
+    ps.synchronize()
+    total_ms = start.elapsed_ms(stop)
+    flop_step = sum(2.0 * nnz * o["N"] for o in ops)
+    value = flop_step * K / (total_ms * 1e-3) / 1e9
+
+    detail = []
+    for i, o in enumerate(ops):
+        ms = float(np.mean([marks[k][i].elapsed_ms(marks[k][i + 1]) for k in range(K)]))
+        alg = algorithmic_bytes(o["op"], nnz, rows, cols, o["N"])
+        detail.append({"op": o["op"], "N": o["N"], "ms": ms,
+                       "gflops": 2.0 * nnz * o["N"] / (ms * 1e-3) / 1e9,
+                       "alg_bytes": alg, "alg_GBps": alg / (ms * 1e-3) / 1e9,
+                       "roofline_frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS})
+        log(f"{o['op']} N={o['N']}: {ms:.3f} ms  {detail[-1]['gflops']:.1f} GFLOPS  "
+            f"{detail[-1]['alg_GBps']:.0f} GB/s ({100 * detail[-1]['roofline_frac']:.1f}% of 8 TB/s)")
+    dom = max(detail, key=lambda d: d["ms"])
+    kernel = "ps::spmm_kernel" if dom["op"] == "spmm" else "ps::sddmm_kernel"
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        host_ops = []
+        for o in ops:
+            if o["op"] == "spmm":
+                B, _ = o["bufs"]
+                host_ops.append(("spmm", o["N"], B.download(np.float32).reshape(cols, o["N"]),
+                                 None))
+            else:
+                X, Y, _ = o["bufs"]
+                host_ops.append(("sddmm", o["N"], X.download(np.float32).reshape(rows, o["N"]),
+                                 Y.download(np.float32).reshape(cols, o["N"])))
+        cpu_s, threads = cpu_baseline(csr, host_ops)
+        cpu = {"value": flop_step / cpu_s / 1e9, "unit": "GFLOPS", "cores": threads,
+               "kind": "port",
+               "sample": f"full {args.config} graph, one step ("
+                         + ", ".join(f"{o['op']} N={o['N']}" for o in ops)
+                         + "), oracle/oracle.cpp OpenMP double accumulation, median of 3 "
+                           f"after 1 warm-up, {cpu_s:.2f} s per step"}
+        log(f"cpu baseline: {cpu['value']:.2f} GFLOPS on {threads} threads")
+
+    line = {
+        "metric": METRIC, "value": value, "unit": "GFLOPS", "n_gpus": 1, "steps": K,
+        "warmup": args.warmup, "ms_per_step": total_ms / K, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": WORKLOADS[args.config], "graph": args.config, "rows": rows,
+                   "nnz": nnz, "worksets": S, "group_num": m.GroupNum(),
+                   "preprocess_ms": preprocess_ms, "parallelism": "single GPU",
+                   "device": f"{props['name']} ({props['arch'].split(':')[0]}, "
+                             f"{props['cu_count']} CUs)"},
+        "ops": detail,
+        "roofline": {"bound": "hbm", "kernel": kernel, "op": f"{dom['op']} N={dom['N']}",
+                     "achieved": dom["alg_GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": dom["roofline_frac"], "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

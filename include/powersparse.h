@@ -1,0 +1,104 @@
+/*
+ * powersparse.h — C facade over the C++17 PowerSparse API, for FFI callers
+ * (Python ctypes, cgo, JNI, N-API) that cannot bind C++ classes.
+ *
+ * Each function wraps one C++ entry point of powersparse_amd/host, which keeps
+ * the reference's interface (ParCIS/PowerSparse); the citation names the
+ * reference declaration it stands for. Status codes and ps_stream_t come from
+ * powersparse_hip.h. C++ exceptions never cross this boundary: std::invalid_argument
+ * maps to PS_ERR_INVALID, every other exception to PS_ERR_RUNTIME, and the text
+ * is available from psx_last_error() on the calling thread.
+ *
+ * Device pointers (B, C, lhs, rhs, outputs, workset arrays) are raw device
+ * addresses, e.g. from ps_malloc.
+ */
+#ifndef POWERSPARSE_H
+#define POWERSPARSE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "powersparse_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct psx_matrix psx_matrix;
+typedef struct psx_csr psx_csr;
+
+const char* psx_last_error(void);
+
+/* Builds the worksets on the current device.
+ * Replaces: PowerSparseMatrixGPU::PowerSparseMatrixGPU (utils/matrix_utils.h:22-23).
+ * cu_count == 0 uses the device's multiProcessorCount (matrix_utils.cu:37-39);
+ * a positive value reproduces the partition the reference would compute on a
+ * device with that many SMs/CUs. timings_ms (optional) receives 9 stage times:
+ * upload, analyze, rank, groups, sigbit, signature, order, gather, total — the
+ * device is synchronised between stages only when it is non-null. */
+int psx_matrix_create(int rows, int cols, int nnz, const int* row_ptr, const int* col_ind,
+                      const float* sp_data, int cu_count, double* timings_ms,
+                      psx_matrix** out);
+/* Replaces: ~PowerSparseMatrixGPU (matrix_utils.h:24). */
+int psx_matrix_destroy(psx_matrix* m);
+/* Replaces: MatrixRow/MatrixCol/MatrixNNZ/GroupTypeNum/GroupFineSize (matrix_utils.h:30-34);
+ * any output may be NULL. */
+int psx_matrix_info(const psx_matrix* m, int* rows, int* cols, int* nnz, int* group_type_num,
+                    int* fine, int* signature_len, int* cu_count);
+/* Replaces: GroupNum() (matrix_utils.h:35); writes GroupTypeNum() ints. */
+int psx_matrix_group_num(const psx_matrix* m, int* group_num);
+/* Replaces: WorksetColInd()[s], WorksetSpData()[s], GroupDestination()[s]
+ * (matrix_utils.h:36-38); device pointers, NULL for an empty workset. */
+int psx_matrix_workset(const psx_matrix* m, int s, const int** col_ind, const float** sp_data,
+                       const int** group_des);
+/* Replaces: ResidueOffset(), ResidueAtomic() (matrix_utils.h:39-40). */
+int psx_matrix_residue(const psx_matrix* m, const int** offset, const uint8_t** atomic);
+
+/* Replaces: PowerSparse::SpMM (PowerSparse_SpMM/PowerSparse_SpMM.h:14-17). */
+int psx_spmm(const psx_matrix* m, int N, const float* B, float* C, int stream_count,
+             const ps_stream_t* streams);
+/* One launch on `stream`, no device synchronisation (no reference counterpart). */
+int psx_spmm_async(const psx_matrix* m, int N, const float* B, float* C, ps_stream_t stream);
+/* Replaces: PowerSparse::SDDMM (PowerSparse_SDDMM/PowerSparse_SDDMM.h:14-18). */
+int psx_sddmm(const psx_matrix* m, int N, const float* lhs, const float* rhs, float** out,
+              int stream_count, const ps_stream_t* streams);
+int psx_sddmm_async(const psx_matrix* m, int N, const float* lhs, const float* rhs,
+                    float* const* out, ps_stream_t stream);
+
+/* ------------------------------------------------------ host CSR inputs */
+/* Replaces: ReadMatrixMarket (benchmarks/matrix_market.cpp:97-134). */
+int psx_csr_read_mtx(const char* path, psx_csr** out);
+/* Binary CSR ("PSCSR001"); no reference counterpart. */
+int psx_csr_read_binary(const char* path, psx_csr** out);
+int psx_csr_write_binary(const psx_csr* csr, const char* path);
+/* Seeded synthetic graphs "C0".."C4" (no reference counterpart); scale >= 1
+ * divides the node count. */
+int psx_csr_synth(const char* config, uint64_t seed, int scale, psx_csr** out);
+int psx_csr_chung_lu(int n, double gamma, double mean_deg, double max_deg, float val_lo,
+                     float val_hi, uint64_t seed, psx_csr** out);
+int psx_csr_uniform_degree(int rows, int cols, int deg_lo, int deg_hi, float val_lo,
+                           float val_hi, uint64_t seed, psx_csr** out);
+int psx_csr_community(int communities, int block, double p_intra, double inter_mean,
+                      double empty_frac, double single_frac, float val_lo, float val_hi,
+                      uint64_t seed, psx_csr** out);
+int psx_csr_info(const psx_csr* csr, int* rows, int* cols, int* nnz);
+/* Host pointers owned by the csr handle. */
+int psx_csr_arrays(const psx_csr* csr, const int** row_ptr, const int** col_ind,
+                   const float** values);
+int psx_csr_free(psx_csr* csr);
+
+/* ------------------------------------------- host steps of preprocessing */
+/* Replaces: GenerateSigBit, FFC mode (utils/matrix_utils.cu:65-128). */
+int psx_generate_sigbit(int cols, const int* col_nnz, int ffc, int* sigbit, int* signature_len);
+/* Replaces: AnalyzeMatrix's workset count (utils/matrix_utils.cu:31-63) from
+ * degree_sums[s] = sum_r floor(deg_r / GROUP_SIZE(s)), s = 0..31 (entry 0 unused). */
+int psx_workset_count(const unsigned long long* degree_sums, int cu_count, int* group_type_num);
+/* Replaces: DenseInput (benchmarks/benchmark_utils.h:100-104): one std::mt19937(seed),
+ * n1 values then n2 values of (rng() % 3) / 10. */
+int psx_dense_input(unsigned seed, size_t n1, float* out1, size_t n2, float* out2);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POWERSPARSE_H */

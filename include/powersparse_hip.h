@@ -1,0 +1,254 @@
+/*
+ * powersparse_hip.h — the C ABI of the MI355X (gfx950) PowerSparse engine.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers and sizes, returns an
+ * int status (PS_OK == 0) and leaves a message for ps_last_error() on failure.
+ * No C++, HIP or CUDA type crosses this boundary: streams and events are opaque
+ * handles, device buffers are raw device pointers obtained from ps_malloc.
+ *
+ * The reference (ParCIS/PowerSparse) has no C ABI: its .cu files call the CUDA
+ * runtime and launch kernels directly. Each declaration below names the
+ * reference code whose role it takes over (file:line in the reference tree).
+ * The C++17 host library (powersparse_amd/host) is the only in-tree caller; its
+ * public headers keep the reference's C++ API (PowerSparse_SpMM.h,
+ * PowerSparse_SDDMM.h, matrix_utils.h).
+ *
+ * Threading: calls are thread-compatible, not thread-safe on the same output.
+ * All launches are asynchronous on the given stream unless stated otherwise.
+ */
+#ifndef POWERSPARSE_HIP_H
+#define POWERSPARSE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PS_OK 0
+#define PS_ERR_INVALID 1  /* bad argument; the reference throws std::invalid_argument */
+#define PS_ERR_RUNTIME 2  /* HIP runtime failure; the reference's CUDA_CALL throws std::runtime_error */
+
+/* A null stream means the device's default (null) stream. */
+typedef struct ps_stream_s* ps_stream_t;
+typedef struct ps_event_s* ps_event_t;
+
+/* Message of the last failed call on this thread ("" if none).
+ * Replaces: CheckCuda's exception text (utils/cuda_utils.h:7-12). */
+const char* ps_last_error(void);
+
+/* ---------------------------------------------------------------- device */
+typedef struct ps_device_props {
+  char name[256];       /* marketing name */
+  char arch[64];        /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+  int cu_count;         /* multiProcessorCount */
+  int major, minor;
+  int lds_per_block;    /* sharedMemPerBlock, bytes */
+  int l2_bytes;
+  int clock_khz;
+  int mem_clock_khz;
+  int mem_bus_width;
+  size_t global_mem;
+} ps_device_props;
+
+/* Replaces: cudaSetDevice / cudaFree(nullptr) (benchmarks/benchmark.cu:116-117). */
+int ps_set_device(int device);
+int ps_get_device(int* device);
+int ps_device_count(int* count);
+/* Replaces: cudaGetDeviceProperties (benchmark.cu:118-120, matrix_utils.cu:37-39). */
+int ps_get_device_props(int device, ps_device_props* props);
+/* Replaces: cudaRuntimeGetVersion / cudaDriverGetVersion (benchmark.cu:121-123). */
+int ps_runtime_version(int* version);
+int ps_driver_version(int* version);
+/* Replaces: cudaDeviceSynchronize (spmm_solution.cu:33, sddmm_solution.cu:49). */
+int ps_device_synchronize(void);
+
+/* ---------------------------------------------------------------- memory */
+/* Replaces: cudaMalloc / cudaFree (matrix_utils.cu:628-633, matrix_utils.h:43-55,
+ * benchmark_utils.h:13-37). ps_free(NULL) is a no-op. */
+int ps_malloc(void** ptr, size_t bytes);
+int ps_free(void* ptr);
+/* Replaces: thrust::copy / cudaMemcpy H2D and D2H (matrix_utils.cu:495-497, 637;
+ * benchmark_utils.h:30-46). Synchronous with respect to the host. */
+int ps_memcpy_htod(void* dst, const void* src, size_t bytes);
+int ps_memcpy_dtoh(void* dst, const void* src, size_t bytes);
+int ps_memcpy_dtod_async(void* dst, const void* src, size_t bytes, ps_stream_t stream);
+/* Replaces: cudaMemset (benchmark_utils.h:29). */
+int ps_memset_async(void* dst, int value, size_t bytes, ps_stream_t stream);
+/* Fills count floats with a counter-based hash of (seed, index): uniform in
+ * [lo, hi) when normal == 0, N(lo, hi^2) (mean lo, std hi) when normal != 0.
+ * No counterpart in the reference, whose inputs come from the host
+ * (benchmark_utils.h:100-104); used for the synthetic BASELINE configs. */
+int ps_fill_random_async(float* dst, size_t count, uint64_t seed, float lo, float hi,
+                         int normal, ps_stream_t stream);
+
+/* ------------------------------------------------------- streams, events */
+/* Replaces: cudaStreamCreate / cudaStreamDestroy (benchmark_utils.h:48-66). */
+int ps_stream_create(ps_stream_t* stream);
+int ps_stream_destroy(ps_stream_t stream);
+int ps_stream_synchronize(ps_stream_t stream);
+/* Replaces: cudaEventCreate/Record/Synchronize/ElapsedTime (benchmark_utils.h:68-88). */
+int ps_event_create(ps_event_t* event);
+int ps_event_destroy(ps_event_t event);
+int ps_event_record(ps_event_t event, ps_stream_t stream);
+int ps_event_synchronize(ps_event_t event);
+int ps_event_elapsed_ms(float* ms, ps_event_t start, ps_event_t stop);
+/* Makes `stream` wait for `event` (used to join per-workset streams). */
+int ps_stream_wait_event(ps_stream_t stream, ps_event_t event);
+
+/* ------------------------------------------------------------- operators */
+/* Maximum number of worksets (GroupTypeNum) one call accepts. */
+#define PS_MAX_WORKSETS 32
+
+/* One workset as the kernels read it. For s == 0 (residue) group_size is 0 and
+ * the group extents come from residue_offset; for s > 0 every group holds
+ * group_size = 32 * 2^(s-1) nonzeros (utils/matrix_utils.h:8). */
+typedef struct ps_workset {
+  const int* col_ind;     /* WorksetColInd()[s]  (matrix_utils.h:36) */
+  const float* sp_data;   /* WorksetSpData()[s]  (matrix_utils.h:37) */
+  const int* group_des;   /* GroupDestination()[s] (matrix_utils.h:38) */
+  int group_num;          /* GroupNum()[s] (matrix_utils.h:35) */
+  int group_size;
+} ps_workset;
+
+/* SpMM C += A * B over all worksets in ONE launch on `stream`, FP32, B (cols x N)
+ * and C (rows x N) row-major. Block groups and residue groups with
+ * residue_atomic[g] != 0 add atomically into C; other residue groups store
+ * (overwrite) their row. N must be a positive multiple of 32; cols * N and
+ * rows * N must fit in int32.
+ * Replaces: the launch loop of PowerSparse::SpMM (PowerSparse_SpMM/spmm_solution.cu:16-31)
+ * and the kernels spmm_kernel_block (spmm_kernel_block.cu:60-162) and
+ * spmm_kernel_residue (spmm_kernel_residue.cu:5-82). */
+int ps_spmm_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
+                   const uint8_t* residue_atomic, int rows, int cols, int N, const float* B,
+                   float* C, ps_stream_t stream);
+
+/* Same operator for a single workset s (s == 0: residue), so callers may keep
+ * the reference's one-stream-per-workset schedule (spmm_solution.cu:16-31). */
+int ps_spmm_workset_launch(int s, const ps_workset* workset, const int* residue_offset,
+                           const uint8_t* residue_atomic, int rows, int cols, int N,
+                           const float* B, float* C, ps_stream_t stream);
+
+/* SDDMM over all worksets in ONE launch: for every stored nonzero p of workset
+ * s in group g, out[s][p] = sp_data[p] * dot(lhs[group_des[g], :], rhs[col_ind[p], :])
+ * with K = N features, lhs (rows x N) and rhs (cols x N) row-major. Block
+ * worksets store their outputs; the residue workset adds into out[0] (the
+ * reference uses atomicAdd into a caller-zeroed buffer). N must be a positive
+ * multiple of 32 and at most 512 (the reference accepts 32 and 128 only,
+ * sddmm_solution.cu:10-11).
+ * Replaces: PowerSparse::SDDMM's launch loop (sddmm_solution.cu:23-48) and
+ * sddmm_kernel_block_reduce{32,128} (sddmm_kernel_block.cu:92-240),
+ * sddmm_kernel_residue_reduce{32,128} (sddmm_kernel_residue.cu:69-545). */
+int ps_sddmm_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
+                    int rows, int cols, int N, const float* lhs, const float* rhs,
+                    float* const* out, ps_stream_t stream);
+int ps_sddmm_workset_launch(int s, const ps_workset* workset, const int* residue_offset,
+                            int rows, int cols, int N, const float* lhs, const float* rhs,
+                            float* out, ps_stream_t stream);
+
+/* ---------------------------------------------------------- primitives */
+/* Device-wide exclusive prefix sum of n uint32 values (out may alias in).
+ * workspace: ps_scan_workspace_bytes(n) bytes of device memory.
+ * Replaces: the host prefix loops of GetGroupMetaInfo and GetResidueOffset
+ * (utils/matrix_utils.cu:158-208, 451-464). */
+size_t ps_scan_workspace_bytes(size_t n);
+int ps_exclusive_scan_u32(const uint32_t* in, uint32_t* out, size_t n, void* workspace,
+                          ps_stream_t stream);
+
+/* Stable LSD radix sort of (key, value) pairs by key bits [begin_bit, end_bit).
+ * Keys and values ping-pong between the two buffer pairs; *result_in_alt is set
+ * to 1 when the sorted data ended in the *_alt buffers. workspace:
+ * ps_radix_workspace_bytes(n) bytes.
+ * Replaces: thrust::sort of NNZPoint (matrix_utils.cu:522-524) and
+ * thrust::stable_sort of group indices (matrix_utils.cu:590-592). */
+size_t ps_radix_workspace_bytes(size_t n);
+int ps_radix_sort_pairs_u64(uint64_t* keys, uint64_t* keys_alt, uint32_t* vals,
+                            uint32_t* vals_alt, size_t n, int begin_bit, int end_bit,
+                            void* workspace, int* result_in_alt, ps_stream_t stream);
+int ps_radix_sort_pairs_u32(uint32_t* keys, uint32_t* keys_alt, uint32_t* vals,
+                            uint32_t* vals_alt, size_t n, int begin_bit, int end_bit,
+                            void* workspace, int* result_in_alt, ps_stream_t stream);
+
+/* out[i] = i for i < n. Replaces: thrust::sequence (matrix_utils.cu:562-566). */
+int ps_iota_u32(uint32_t* out, int n, ps_stream_t stream);
+
+/* -------------------------------------------------------- preprocessing */
+/* sums[s] = sum over rows of floor(deg / (32 * 2^(s-1))) for s = 1..31 (sums[0] = 0),
+ * written to host memory (synchronous).
+ * Replaces: the row loop of AnalyzeMatrix (utils/matrix_utils.cu:44-53). */
+int ps_pre_degree_sums(const int* row_ptr, int rows, unsigned long long* sums_host,
+                       ps_stream_t stream);
+
+/* col_nnz[c] += number of nonzeros in column c (col_nnz pre-zeroed).
+ * Replaces: the OpenMP histogram (matrix_utils.cu:508-514). */
+int ps_pre_col_histogram(const int* col_ind, int nnz, int* col_nnz, ps_stream_t stream);
+
+/* keys[p] = (row(p) << count_bits) | (max_count - col_nnz[col_ind[p]]), vals[p] = p:
+ * the stable sort of these pairs gives each row's nonzeros by column count
+ * descending, ties in CSR order.
+ * Replaces: CopyCSRToNNZ + NNZPoint::operator< (matrix_utils.cu:210-223, 239-257). */
+int ps_pre_rank_keys(const int* row_ptr, int rows, const int* col_ind, int nnz,
+                     const int* col_nnz, int max_count, int count_bits, uint64_t* keys,
+                     uint32_t* vals, ps_stream_t stream);
+
+/* Per-row group counts: counts[s * rows + r] = groups of row r in workset s
+ * (s = 0 residue). Replaces: GetGroupNumArray (matrix_utils.cu:132-156). */
+int ps_pre_group_counts(const int* row_ptr, int rows, int group_type_num, int fine,
+                        uint32_t* counts, ps_stream_t stream);
+
+/* Per-group metadata in initial (row) order from the exclusive prefix of the
+ * counts (prefix[s * rows + r]): destination row, first ranked index, and for
+ * the residue workset its length and atomic flag.
+ * Replaces: GetGroupMetaInfo (matrix_utils.cu:158-208). */
+int ps_pre_group_meta(const int* row_ptr, int rows, int group_type_num, int fine,
+                      const uint32_t* prefix, int* const* group_des,
+                      int* const* group_start, int* residue_len, uint8_t* residue_atomic,
+                      ps_stream_t stream);
+
+/* Signature bitmaps, word-major per workset: sig[s][w * G_s + g] gets bit
+ * 31 - b % 32 of word b / 32 for b = sigbit[col] of every member (sig zeroed).
+ * ranked_keys are the sorted keys of ps_pre_rank_keys (row in the high bits),
+ * ranked_vals the CSR positions in ranked order.
+ * Replaces: GetResidueSignature / GetBlockSignature (matrix_utils.cu:261-327). */
+int ps_pre_signatures(const int* row_ptr, int rows, int group_type_num, int fine,
+                      const uint64_t* ranked_keys, int count_bits,
+                      const uint32_t* ranked_vals, int nnz, const int* col_ind,
+                      const int* sigbit, const uint32_t* prefix, const int* group_num,
+                      uint32_t* const* sig, ps_stream_t stream);
+
+/* keys[k] = ~sig_word[perm[k]] (descending signature order as an ascending key).
+ * Replaces: CompareDescending (matrix_utils.cu:394-401). */
+int ps_pre_signature_keys(const uint32_t* sig_word, const uint32_t* perm, int n,
+                          uint32_t* keys, ps_stream_t stream);
+
+/* OR and AND of each signature word over all groups (host arrays of `words`),
+ * to skip digits that cannot reorder the groups. */
+int ps_pre_signature_span(const uint32_t* sig, int groups, int words, uint32_t* or_host,
+                          uint32_t* and_host, ps_stream_t stream);
+
+/* Final metadata in sorted order: des[k] = src_des[perm[k]]; for the residue
+ * workset also len[k] = src_len[perm[k]] and atomic[k] = src_atomic[perm[k]].
+ * Replaces: the metadata half of GetResidueWorkset / GetBlockWorkset
+ * (matrix_utils.cu:403-449). */
+int ps_pre_permute_meta(const uint32_t* perm, int groups, const int* src_des, int* des,
+                        const int* src_len, uint32_t* len, const uint8_t* src_atomic,
+                        uint8_t* atomic, ps_stream_t stream);
+
+/* Final nonzeros of one workset: group k (in sorted order) takes the members
+ * of initial group perm[k] (ranked_vals[group_start[perm[k]] ...]) sorted by
+ * column ascending, ties in ranked order, written at offset[k] (residue) or
+ * k * group_size (blocks).
+ * Replaces: GetSrc{Residue,Block}Workset + thrust::sort of NNZPoint2 +
+ * Get{Residue,Block}Workset (matrix_utils.cu:329-392, 596-617, 639-656). */
+int ps_pre_gather_workset(int group_size, const uint32_t* perm, int groups,
+                          const int* group_start, const int* residue_offset,
+                          const uint32_t* ranked_vals, const int* col_ind,
+                          const float* sp_data, int* out_col, float* out_val,
+                          ps_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POWERSPARSE_HIP_H */

@@ -1,0 +1,246 @@
+// SDDMM (edge messaging), out[p] = a_p * <X[row], Y[col_p]>, FP32, on gfx950.
+//
+// One launch covers every workset. Wave tasks:
+//   block workset: 64 consecutive stored nonzeros (one group when GS >= 64, two
+//     groups of 32 when GS == 32);
+//   residue workset: 64 / RCAP groups per wave, RCAP lanes per group.
+// Lanes form slots of 8; slot q owns 8 consecutive nonzeros and each lane of the
+// slot holds K / 8 features of X (float4 pieces 32 floats apart, so a slot reads
+// a 128-byte line per piece). After the 8 partial dots per lane the slot does a
+// transposing butterfly (xor 4, 2, 1 via swizzle / DPP): each exchange halves the
+// number of partials a lane keeps, and at the end lane `sub` of slot `q` holds
+// the full dot of nonzero 8q + sub, so the wave's 64 results are stored with
+// one coalesced write.
+//
+// Reference behaviour kept (PowerSparse_SDDMM/sddmm_solution.cu:7-50,
+// sddmm_kernel_block.cu:155-164, sddmm_kernel_residue.cu:295-305): block
+// outputs are stored, residue outputs are added atomically into out[0], the
+// output is in workset order.
+#include "ps_common.hpp"
+
+namespace ps {
+namespace {
+
+constexpr int kWavesPerBlock = 4;
+
+struct SddmmArgs {
+  ps_workset ws[PS_MAX_WORKSETS];
+  float* out[PS_MAX_WORKSETS];
+  uint32_t task_begin[PS_MAX_WORKSETS + 1];
+  int32_t count;
+  int32_t N;
+  int32_t rcap;
+  uint32_t total_tasks;
+  const int* residue_offset;
+  const float* lhs;
+  const float* rhs;
+};
+
+template <int KQ>
+__device__ __forceinline__ float partial_dot(const float4 (&x)[KQ], const float* y) {
+  float s = 0.f;
+#pragma unroll
+  for (int q = 0; q < KQ; ++q) {
+    const float4 v = *reinterpret_cast<const float4*>(y + 32 * q);
+    s = fmaf(x[q].x, v.x, s);
+    s = fmaf(x[q].y, v.y, s);
+    s = fmaf(x[q].z, v.z, s);
+    s = fmaf(x[q].w, v.w, s);
+  }
+  return s;
+}
+
+// Transposing reduction over the 8 lanes of a slot: in p[j] each lane holds
+// its partial for nonzero j of the slot; returns the full sum for j == sub.
+__device__ __forceinline__ float slot_transpose_sum(const float (&p)[8], int sub) {
+  const bool b2 = sub & 4, b1 = sub & 2, b0 = sub & 1;
+  float q[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float keep = b2 ? p[i + 4] : p[i];
+    const float send = b2 ? p[i] : p[i + 4];
+    q[i] = keep + xor_shfl<4>(send);
+  }
+  float r[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float keep = b1 ? q[i + 2] : q[i];
+    const float send = b1 ? q[i] : q[i + 2];
+    r[i] = keep + xor_shfl<2>(send);
+  }
+  const float keep = b0 ? r[1] : r[0];
+  const float send = b0 ? r[0] : r[1];
+  return keep + xor_shfl<1>(send);
+}
+
+template <int KQ>
+__global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs args) {
+  constexpr int K = 32 * KQ;
+  const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t task =
+      __builtin_amdgcn_readfirstlane(blk * kWavesPerBlock + threadIdx.x / kWave);
+  if (task >= args.total_tasks) return;
+  int i = 0;
+  while (i + 1 < args.count && task >= args.task_begin[i + 1]) ++i;
+  const ps_workset ws = args.ws[i];
+  float* __restrict__ out = args.out[i];
+  const int local = int(task - args.task_begin[i]);
+
+  const int lane = lane_id();
+  const int slot = lane / 8, sub = lane % 8;
+  const float* __restrict__ Y = args.rhs + sub * 4;
+  float4 x[KQ];
+  float p[8];
+
+  if (ws.group_size > 0) {
+    const int total = ws.group_num * ws.group_size;
+    const int p0 = local * 64 + slot * 8;
+    const bool valid = p0 < total;
+    const int g = valid ? p0 / ws.group_size : 0;
+    const int row = valid ? ws.group_des[g] : 0;
+    const float* xr = args.lhs + row * K + sub * 4;
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) x[q] = *reinterpret_cast<const float4*>(xr + 32 * q);
+    int4 c0 = make_int4(0, 0, 0, 0), c1 = make_int4(0, 0, 0, 0);
+    if (valid) {
+      c0 = *reinterpret_cast<const int4*>(ws.col_ind + p0);
+      c1 = *reinterpret_cast<const int4*>(ws.col_ind + p0 + 4);
+    }
+    const int c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) p[j] = partial_dot<KQ>(x, Y + c[j] * K);
+    const float dot = slot_transpose_sum(p, sub);
+    const int pos = local * 64 + lane;
+    if (valid) out[pos] = dot * ws.sp_data[pos];
+  } else {
+    const int rcap = args.rcap;
+    const int h = lane / rcap, q = lane % rcap;
+    const int g = local * (64 / rcap) + h;
+    const bool has = g < ws.group_num;
+    const int beg = has ? args.residue_offset[g] : 0;
+    const int len = has ? args.residue_offset[g + 1] - beg : 0;
+    const int row = has ? ws.group_des[g] : 0;
+    const float* xr = args.lhs + row * K + sub * 4;
+#pragma unroll
+    for (int qq = 0; qq < KQ; ++qq) x[qq] = *reinterpret_cast<const float4*>(xr + 32 * qq);
+    const int first = (q / 8) * 8;  // first nonzero of this lane's slot in a chunk
+    for (int c0 = 0; __any(c0 < len); c0 += rcap) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int k = c0 + first + j;
+        const int col = k < len ? ws.col_ind[beg + k] : -1;
+        p[j] = col >= 0 ? partial_dot<KQ>(x, Y + col * K) : 0.f;
+      }
+      const float dot = slot_transpose_sum(p, sub);
+      const int k = c0 + q;
+      if (k < len) unsafeAtomicAdd(out + beg + k, dot * ws.sp_data[beg + k]);
+    }
+  }
+}
+
+template <int KQ>
+void launch_kq(const SddmmArgs& a, unsigned grid, hipStream_t stream) {
+  sddmm_kernel<KQ><<<grid, kWave * kWavesPerBlock, 0, stream>>>(a);
+}
+
+int launch(int count, const int* order, const ps_workset* worksets, float* const* outs,
+           const int* residue_offset, int rows, int cols, int N, const float* lhs,
+           const float* rhs, int rcap, hipStream_t stream) {
+  PS_CHECK_ARG(N > 0 && N % 32 == 0 && N <= 512,
+               "SDDMM requires N to be a multiple of 32 between 32 and 512");
+  PS_CHECK_ARG(int64_t(rows) * N <= INT32_MAX && int64_t(cols) * N <= INT32_MAX,
+               "Dense dimensions exceed the 32-bit kernel indexing range");
+  PS_CHECK_ARG(lhs && rhs && outs, "Invalid SDDMM buffers");
+  SddmmArgs a{};
+  a.N = N;
+  a.rcap = rcap;
+  a.lhs = lhs;
+  a.rhs = rhs;
+  a.residue_offset = residue_offset;
+  uint64_t tasks = 0;
+  int n = 0;
+  // Validate every workset before submitting any work (sddmm_solution.cu:16-22).
+  for (int q = 0; q < count; ++q) {
+    const ps_workset& w = worksets[q];
+    if (w.group_num <= 0) continue;
+    PS_CHECK_ARG(outs[q], "Missing SDDMM output workset");
+    PS_CHECK_ARG(w.col_ind && w.sp_data && w.group_des, "Invalid SDDMM workset buffers");
+    const int s = order[q];
+    uint64_t t;
+    if (s > 0) {
+      PS_CHECK_ARG(w.group_size >= 32 && (w.group_size & (w.group_size - 1)) == 0,
+                   "Block workset group size must be a power of two >= 32");
+      t = (uint64_t(w.group_num) * w.group_size + 63) / 64;
+    } else {
+      PS_CHECK_ARG(residue_offset, "Missing residue offsets");
+      t = (uint64_t(w.group_num) + (64 / rcap) - 1) / (64 / rcap);
+    }
+    a.ws[n] = w;
+    if (s == 0) a.ws[n].group_size = 0;
+    a.out[n] = outs[q];
+    a.task_begin[n] = uint32_t(tasks);
+    tasks += t;
+    ++n;
+  }
+  if (n == 0) return PS_OK;
+  PS_CHECK_ARG(tasks < (1ull << 31), "SDDMM task count exceeds the launch range");
+  a.count = n;
+  a.task_begin[n] = uint32_t(tasks);
+  a.total_tasks = uint32_t(tasks);
+  const unsigned grid = unsigned((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
+  switch (N / 32) {
+    case 1: launch_kq<1>(a, grid, stream); break;
+    case 2: launch_kq<2>(a, grid, stream); break;
+    case 3: launch_kq<3>(a, grid, stream); break;
+    case 4: launch_kq<4>(a, grid, stream); break;
+    case 5: launch_kq<5>(a, grid, stream); break;
+    case 6: launch_kq<6>(a, grid, stream); break;
+    case 7: launch_kq<7>(a, grid, stream); break;
+    case 8: launch_kq<8>(a, grid, stream); break;
+    case 9: launch_kq<9>(a, grid, stream); break;
+    case 10: launch_kq<10>(a, grid, stream); break;
+    case 11: launch_kq<11>(a, grid, stream); break;
+    case 12: launch_kq<12>(a, grid, stream); break;
+    case 13: launch_kq<13>(a, grid, stream); break;
+    case 14: launch_kq<14>(a, grid, stream); break;
+    case 15: launch_kq<15>(a, grid, stream); break;
+    default: launch_kq<16>(a, grid, stream); break;
+  }
+  PS_LAUNCHED();
+  return PS_OK;
+}
+
+}  // namespace
+}  // namespace ps
+
+extern "C" {
+
+int ps_sddmm_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
+                    int rows, int cols, int N, const float* lhs, const float* rhs,
+                    float* const* out, ps_stream_t stream) {
+  PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets && out,
+               "Invalid SDDMM workset count");
+  int order[PS_MAX_WORKSETS];
+  ps_workset ordered[PS_MAX_WORKSETS];
+  float* outs[PS_MAX_WORKSETS];
+  for (int q = 0; q < workset_count; ++q) {
+    order[q] = workset_count - 1 - q;
+    ordered[q] = worksets[workset_count - 1 - q];
+    outs[q] = out[workset_count - 1 - q];
+  }
+  // A single workset means fine mode (residue groups of at most 16 nonzeros,
+  // utils/matrix_utils.cu:137-141); otherwise residue groups hold at most 31.
+  const int rcap = workset_count == 1 ? 16 : 32;
+  return ps::launch(workset_count, order, ordered, outs, residue_offset, rows, cols, N, lhs,
+                    rhs, rcap, ps::to_hip(stream));
+}
+
+int ps_sddmm_workset_launch(int s, const ps_workset* workset, const int* residue_offset,
+                            int rows, int cols, int N, const float* lhs, const float* rhs,
+                            float* out, ps_stream_t stream) {
+  PS_CHECK_ARG(s >= 0 && s < PS_MAX_WORKSETS && workset, "Invalid SDDMM workset");
+  return ps::launch(1, &s, workset, &out, residue_offset, rows, cols, N, lhs, rhs, 32,
+                    ps::to_hip(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,378 @@
+// PowerSparseMatrixGPU: host orchestration of the GPU preprocessing.
+//
+// Follows ParCIS/PowerSparse utils/matrix_utils.cu:470-663 step by step, with
+// every per-nonzero and per-row loop moved to HIP kernels behind the C ABI:
+//   validation (host, as :475-488) -> CSR upload -> worksets S (:31-63, device
+//   degree sums) -> column histogram (:508-514, device) -> each row's nonzeros
+//   ranked by column count descending, ties in CSR order (:518-524, stable
+//   radix sort) -> group counts, scans and metadata (:132-208, device) ->
+//   column signature bits (:65-128, host std::sort as in the reference) ->
+//   signatures and the stable per-word group sort (:261-327, :562-594) ->
+//   final worksets (:596-656).
+// The host signature-bit step overlaps the device rank sort.
+#include "matrix_utils.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <numeric>
+#include <string>
+#include <vector>
+
+#include "device_buffer.h"
+#include "preprocess_host.h"
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+namespace PowerSparse {
+
+void ThrowOnError(int status) {
+  if (status == PS_OK) return;
+  const std::string msg = ps_last_error();
+  if (status == PS_ERR_INVALID) throw std::invalid_argument(msg);
+  throw std::runtime_error(msg);
+}
+
+int GenerateSigBitFFC(int cols, const int* col_nnz, int ffc, int* sigbit) {
+  // The reference sorts iota by col_nnz descending with libstdc++ std::sort
+  // (unstable, matrix_utils.cu:70-75). Sorting (count, column) records with a
+  // comparator that reads only the count makes the same comparisons and moves
+  // as sorting column ids through an indirect comparator, so the resulting
+  // order (ties included) is identical, without the indirect loads.
+  struct Rec {
+    int count;
+    int col;
+  };
+  std::vector<Rec> order(static_cast<size_t>(cols));
+  for (int c = 0; c < cols; ++c) order[size_t(c)] = Rec{col_nnz[c], c};
+  std::sort(order.begin(), order.end(),
+            [](const Rec& a, const Rec& b) { return a.count > b.count; });
+  // FFC buckets (matrix_utils.cu:91-118): the ffc most frequent columns take
+  // bit 0 and define the bucket mass; each later bucket takes at least one
+  // column and keeps taking columns while its running mass stays below it.
+  int i = 0, bit = 0, mass0 = 0;
+  const int head = std::min(ffc, cols);
+  for (; i < head; ++i) {
+    sigbit[order[size_t(i)].col] = 0;
+    mass0 += order[size_t(i)].count;
+  }
+  bit = 1;
+  while (i < cols) {
+    int mass = order[size_t(i)].count;
+    sigbit[order[size_t(i)].col] = bit;
+    ++i;
+    while (i < cols) {
+      mass += order[size_t(i)].count;
+      if (mass >= mass0) break;
+      sigbit[order[size_t(i)].col] = bit;
+      ++i;
+    }
+    ++bit;
+  }
+  // Length rounded to whole 32-bit words (:120-122), bits clamped (:123-127).
+  int len = bit;
+  if (len < 32) len = 32;
+  else if (len % 32 < 16) len = len / 32 * 32;
+  else len = (len + 31) / 32 * 32;
+  for (int c = 0; c < cols; ++c)
+    if (sigbit[c] >= len) sigbit[c] = len - 1;
+  return len;
+}
+
+int WorksetCount(const unsigned long long* degree_sums, int cu_count) {
+  // matrix_utils.cu:40-53: threshold = 8 blocks per SM * SMs * 4; the number
+  // of worksets is one more than the count of leading sizes whose groups reach it.
+  const long long threshold = 8LL * cu_count * 4;
+  int S = 0;
+  long long groups = threshold + 1;
+  while (groups >= threshold) {
+    groups = S + 1 < 32 ? (long long)degree_sums[S + 1] : 0;
+    ++S;
+  }
+  return S;
+}
+
+namespace {
+
+int BitsFor(uint64_t v) {
+  int b = 0;
+  while (b < 64 && (v >> b) != 0) ++b;
+  return b;
+}
+
+class StageClock {
+ public:
+  explicit StageClock(PreprocessTimings* t) : t_(t), last_(Now()), first_(last_) {}
+  // Records the time since the previous mark into `slot` (synchronising the
+  // device first) when timings were requested.
+  void Mark(double PreprocessTimings::*slot) {
+    if (!t_) return;
+    ThrowOnError(ps_device_synchronize());
+    const auto now = Now();
+    t_->*slot += std::chrono::duration<double, std::milli>(now - last_).count();
+    last_ = now;
+  }
+  void Finish() {
+    if (t_) t_->total_ms = std::chrono::duration<double, std::milli>(Now() - first_).count();
+  }
+
+ private:
+  static std::chrono::steady_clock::time_point Now() { return std::chrono::steady_clock::now(); }
+  PreprocessTimings* t_;
+  std::chrono::steady_clock::time_point last_, first_;
+};
+
+}  // namespace
+
+PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num,
+                                           const int* row_ptr, const int* col_ind,
+                                           const float* sp_data)
+    : PowerSparseMatrixGPU(row_num, col_num, nnz_num, row_ptr, col_ind, sp_data,
+                           PartitionPolicy{}) {}
+
+PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num,
+                                           const int* row_ptr, const int* col_ind,
+                                           const float* sp_data, const PartitionPolicy& policy,
+                                           PreprocessTimings* timings)
+    : _matrix_row(row_num), _matrix_col(col_num), _matrix_nnz(nnz_num) {
+  // Same checks and messages as the reference constructor (matrix_utils.cu:475-488).
+  if (row_num <= 0 || col_num <= 0 || nnz_num <= 0 ||
+      row_num > std::numeric_limits<int>::max() - 32 ||
+      nnz_num > std::numeric_limits<int>::max() - 32 || !row_ptr || !col_ind || !sp_data) {
+    throw std::invalid_argument("Expected a nonempty CSR matrix with 32-bit indices");
+  }
+  if (row_ptr[0] != 0 || row_ptr[row_num] != nnz_num)
+    throw std::invalid_argument("Invalid CSR row-pointer endpoints");
+  int bad = 0;
+#pragma omp parallel for reduction(| : bad) schedule(static)
+  for (int r = 0; r < row_num; ++r) bad |= (row_ptr[r] < 0 || row_ptr[r] > row_ptr[r + 1]);
+  if (bad) throw std::invalid_argument("CSR row pointers must be nondecreasing");
+#pragma omp parallel for reduction(| : bad) schedule(static)
+  for (int p = 0; p < nnz_num; ++p)
+    bad |= (col_ind[p] < 0 || col_ind[p] >= col_num || !std::isfinite(sp_data[p]));
+  if (bad) throw std::invalid_argument("Invalid CSR column index or sparse value");
+  if (policy.cu_count < 0) throw std::invalid_argument("PartitionPolicy::cu_count must be >= 0");
+  _cu_count = policy.cu_count;
+  if (_cu_count == 0) {
+    int dev = 0;
+    ThrowOnError(ps_get_device(&dev));
+    ps_device_props props;
+    ThrowOnError(ps_get_device_props(dev, &props));
+    _cu_count = props.cu_count;
+  }
+  try {
+    Build(row_ptr, col_ind, sp_data, timings);
+  } catch (...) {
+    Release();
+    throw;
+  }
+}
+
+void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const float* sp_data,
+                                 PreprocessTimings* timings) {
+  const int rows = _matrix_row, cols = _matrix_col, nnz = _matrix_nnz;
+  const int fine = _group_fine_size;
+  ps_stream_t st = nullptr;
+  StageClock clock(timings);
+
+  DeviceArray<int> d_rp(static_cast<size_t>(rows) + 1), d_ci(static_cast<size_t>(nnz));
+  DeviceArray<float> d_sv(static_cast<size_t>(nnz));
+  d_rp.Upload(row_ptr, size_t(rows) + 1);
+  d_ci.Upload(col_ind, size_t(nnz));
+  d_sv.Upload(sp_data, size_t(nnz));
+  clock.Mark(&PreprocessTimings::upload_ms);
+
+  // Worksets S (AnalyzeMatrix) and the column histogram.
+  unsigned long long sums[32];
+  ThrowOnError(ps_pre_degree_sums(d_rp.data(), rows, sums, st));
+  const int S = WorksetCount(sums, _cu_count);
+  if (S > PS_MAX_WORKSETS) throw std::runtime_error("Too many worksets");
+  _group_type_num = S;
+  DeviceArray<int> d_cn(static_cast<size_t>(cols));
+  d_cn.Zero(st);
+  ThrowOnError(ps_pre_col_histogram(d_ci.data(), nnz, d_cn.data(), st));
+  std::vector<int> col_nnz(static_cast<size_t>(cols));
+  d_cn.Download(col_nnz.data(), size_t(cols));
+  const int max_count = *std::max_element(col_nnz.begin(), col_nnz.end());
+  clock.Mark(&PreprocessTimings::analyze_ms);
+
+  // Rank every row's nonzeros by column count (descending, ties in CSR order).
+  const int count_bits = BitsFor(uint64_t(max_count));
+  const int row_bits = BitsFor(uint64_t(rows - 1));
+  DeviceArray<uint64_t> keys(static_cast<size_t>(nnz)), keys_alt(static_cast<size_t>(nnz));
+  DeviceArray<uint32_t> vals(static_cast<size_t>(nnz)), vals_alt(static_cast<size_t>(nnz));
+  {
+    DeviceArray<char> ws(ps_radix_workspace_bytes(size_t(nnz)));
+    ThrowOnError(ps_pre_rank_keys(d_rp.data(), rows, d_ci.data(), nnz, d_cn.data(), max_count,
+                                  count_bits, keys.data(), vals.data(), st));
+    int alt = 0;
+    ThrowOnError(ps_radix_sort_pairs_u64(keys.data(), keys_alt.data(), vals.data(),
+                                         vals_alt.data(), size_t(nnz), 0,
+                                         count_bits + row_bits, ws.data(), &alt, st));
+    if (alt) {
+      std::swap(keys, keys_alt);
+      std::swap(vals, vals_alt);
+    }
+    // The workspace is released when it leaves scope; ps_free synchronises.
+  }
+  keys_alt.Reset();
+  vals_alt.Reset();
+  clock.Mark(&PreprocessTimings::rank_ms);
+
+  // Per-row group counts and their exclusive scans (group ids in row order).
+  const size_t stride = size_t(rows) + 1;
+  DeviceArray<uint32_t> prefix(static_cast<size_t>(S) * stride);
+  ThrowOnError(ps_pre_group_counts(d_rp.data(), rows, S, fine, prefix.data(), st));
+  {
+    DeviceArray<char> ws(ps_scan_workspace_bytes(stride));
+    for (int s = 0; s < S; ++s)
+      ThrowOnError(ps_exclusive_scan_u32(prefix.data() + s * stride, prefix.data() + s * stride,
+                                         stride, ws.data(), st));
+  }
+
+  // Host: column signature bits, while the device works.
+  std::vector<int> sigbit(static_cast<size_t>(cols));
+  _signature_len = GenerateSigBitFFC(cols, col_nnz.data(), 2, sigbit.data());
+  clock.Mark(&PreprocessTimings::sigbit_ms);
+
+  _group_num = new int[S]();
+  for (int s = 0; s < S; ++s) {
+    uint32_t total = 0;
+    ThrowOnError(ps_memcpy_dtoh(&total, prefix.data() + s * stride + rows, sizeof(uint32_t)));
+    _group_num[s] = int(total);
+  }
+  const int G0 = _group_num[0];
+
+  std::vector<DeviceArray<int>> des0(static_cast<size_t>(S)), start(static_cast<size_t>(S));
+  std::vector<int*> des_ptr(static_cast<size_t>(S), nullptr), start_ptr(static_cast<size_t>(S), nullptr);
+  for (int s = 0; s < S; ++s) {
+    des0[size_t(s)].Allocate(size_t(_group_num[s]));
+    start[size_t(s)].Allocate(size_t(_group_num[s]));
+    des_ptr[size_t(s)] = des0[size_t(s)].data();
+    start_ptr[size_t(s)] = start[size_t(s)].data();
+  }
+  DeviceArray<int> res_len(static_cast<size_t>(G0));
+  DeviceArray<uint8_t> res_atomic0(static_cast<size_t>(G0));
+  ThrowOnError(ps_pre_group_meta(d_rp.data(), rows, S, fine, prefix.data(), des_ptr.data(),
+                                 start_ptr.data(), res_len.data(), res_atomic0.data(), st));
+  clock.Mark(&PreprocessTimings::groups_ms);
+
+  // Signatures, word-major per workset.
+  const int words = _signature_len / 32;
+  DeviceArray<int> d_sigbit(static_cast<size_t>(cols));
+  d_sigbit.Upload(sigbit.data(), size_t(cols));
+  std::vector<DeviceArray<uint32_t>> sig(static_cast<size_t>(S));
+  std::vector<uint32_t*> sig_ptr(static_cast<size_t>(S), nullptr);
+  for (int s = 0; s < S; ++s) {
+    sig[size_t(s)].Allocate(size_t(_group_num[s]) * words);
+    sig[size_t(s)].Zero(st);
+    sig_ptr[size_t(s)] = sig[size_t(s)].data();
+  }
+  ThrowOnError(ps_pre_signatures(d_rp.data(), rows, S, fine, keys.data(), count_bits,
+                                 vals.data(), nnz, d_ci.data(), d_sigbit.data(), prefix.data(),
+                                 _group_num, sig_ptr.data(), st));
+  keys.Reset();
+  clock.Mark(&PreprocessTimings::signature_ms);
+
+  // Stable sort of each workset's groups by signature, descending, word 0
+  // most significant: one stable pass per word from the last word to the first
+  // (matrix_utils.cu:590-592), skipping words and digits that do not vary.
+  std::vector<DeviceArray<uint32_t>> perm(static_cast<size_t>(S));
+  for (int s = 0; s < S; ++s) {
+    const int G = _group_num[s];
+    if (G == 0) continue;
+    perm[size_t(s)].Allocate(size_t(G));
+    ThrowOnError(ps_iota_u32(perm[size_t(s)].data(), G, st));
+    if (G == 1) continue;
+    std::vector<uint32_t> w_or(static_cast<size_t>(words)), w_and(static_cast<size_t>(words));
+    ThrowOnError(ps_pre_signature_span(sig[size_t(s)].data(), G, words, w_or.data(),
+                                       w_and.data(), st));
+    DeviceArray<uint32_t> k1(static_cast<size_t>(G)), k2(static_cast<size_t>(G)), p2(static_cast<size_t>(G));
+    DeviceArray<char> ws(ps_radix_workspace_bytes(size_t(G)));
+    for (int w = words - 1; w >= 0; --w) {
+      const uint32_t diff = w_or[size_t(w)] ^ w_and[size_t(w)];
+      if (diff == 0) continue;
+      const int lo = __builtin_ctz(diff) / 8 * 8;
+      const int hi = 32 - __builtin_clz(diff);
+      ThrowOnError(ps_pre_signature_keys(sig[size_t(s)].data() + size_t(w) * G,
+                                         perm[size_t(s)].data(), G, k1.data(), st));
+      int alt = 0;
+      ThrowOnError(ps_radix_sort_pairs_u32(k1.data(), k2.data(), perm[size_t(s)].data(),
+                                           p2.data(), size_t(G), lo, hi, ws.data(), &alt, st));
+      if (alt) std::swap(perm[size_t(s)], p2);
+    }
+    sig[size_t(s)].Reset();
+  }
+  clock.Mark(&PreprocessTimings::order_ms);
+
+  // Final metadata and worksets in signature order.
+  _workset_col_ind = new int*[S]();
+  _workset_sp_data = new float*[S]();
+  _group_des = new int*[S]();
+  ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_residue_offset), sizeof(int) * (size_t(G0) + 1)));
+  ThrowOnError(ps_memset_async(_residue_offset, 0, sizeof(int) * (size_t(G0) + 1), st));
+  if (G0 > 0) {
+    ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_residue_atomic), sizeof(bool) * size_t(G0)));
+    ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_group_des[0]), sizeof(int) * size_t(G0)));
+    DeviceArray<uint32_t> len(static_cast<size_t>(G0) + 1);
+    ThrowOnError(ps_pre_permute_meta(perm[0].data(), G0, des0[0].data(), _group_des[0],
+                                     res_len.data(), len.data(), res_atomic0.data(),
+                                     reinterpret_cast<uint8_t*>(_residue_atomic), st));
+    DeviceArray<char> ws(ps_scan_workspace_bytes(size_t(G0) + 1));
+    ThrowOnError(ps_exclusive_scan_u32(len.data(), reinterpret_cast<uint32_t*>(_residue_offset),
+                                       size_t(G0) + 1, ws.data(), st));
+  }
+  for (int s = 1; s < S; ++s) {
+    const int G = _group_num[s];
+    if (G == 0) continue;
+    ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_group_des[s]), sizeof(int) * size_t(G)));
+    ThrowOnError(ps_pre_permute_meta(perm[size_t(s)].data(), G, des0[size_t(s)].data(),
+                                     _group_des[s], nullptr, nullptr, nullptr, nullptr, st));
+  }
+  for (int s = 0; s < S; ++s) {
+    const int G = _group_num[s];
+    if (G == 0) continue;
+    size_t size;
+    if (s == 0) {
+      int total = 0;
+      ThrowOnError(ps_memcpy_dtoh(&total, _residue_offset + G0, sizeof(int)));
+      size = size_t(total);
+    } else {
+      size = size_t(G) * size_t(GROUP_SIZE(s));
+    }
+    ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_workset_col_ind[s]), sizeof(int) * size));
+    ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_workset_sp_data[s]), sizeof(float) * size));
+    ThrowOnError(ps_pre_gather_workset(s == 0 ? 0 : GROUP_SIZE(s), perm[size_t(s)].data(), G,
+                                       start[size_t(s)].data(), s == 0 ? _residue_offset : nullptr,
+                                       vals.data(), d_ci.data(), d_sv.data(), _workset_col_ind[s],
+                                       _workset_sp_data[s], st));
+  }
+  ThrowOnError(ps_device_synchronize());
+  clock.Mark(&PreprocessTimings::gather_ms);
+  clock.Finish();
+}
+
+void PowerSparseMatrixGPU::Release() noexcept {
+  for (int s = 0; s < _group_type_num; ++s) {
+    if (_workset_col_ind) ps_free(_workset_col_ind[s]);
+    if (_workset_sp_data) ps_free(_workset_sp_data[s]);
+    if (_group_des) ps_free(_group_des[s]);
+  }
+  delete[] _group_num;
+  delete[] _workset_col_ind;
+  delete[] _workset_sp_data;
+  delete[] _group_des;
+  ps_free(_residue_offset);
+  ps_free(_residue_atomic);
+  _group_num = nullptr;
+  _workset_col_ind = nullptr;
+  _workset_sp_data = nullptr;
+  _group_des = nullptr;
+  _residue_offset = nullptr;
+  _residue_atomic = nullptr;
+}
+
+}  // namespace PowerSparse

@@ -1,0 +1,103 @@
+// PowerSparseMatrixGPU: owns the device worksets of a CSR matrix.
+//
+// Same public interface as the reference (ParCIS/PowerSparse
+// utils/matrix_utils.h:8-76): constructor from host CSR arrays, the accessors
+// returning device pointers, ValidateDenseShape and the GROUP_SIZE / CEIL /
+// FLOOR macros. The worksets are built on the GPU (HIP kernels reached through
+// the C ABI in include/powersparse_hip.h) and are bit-identical to what the
+// reference's preprocessing produces for the same CU count.
+//
+// No HIP or CUDA header is included here: device work goes through the C ABI.
+#pragma once
+
+#include <cstdint>
+#include <limits>
+#include <stdexcept>
+
+#include "powersparse_hip.h"
+
+#define GROUP_SIZE(I) (32 * (1 << ((I) - 1)))
+#define CEIL(X, Y) ((X) / (Y) + ((X) % (Y) != 0))
+#define FLOOR(X, Y) ((X) / (Y))
+
+namespace PowerSparse {
+
+enum SigBitMode { PPL = 0, FFC = 1 };
+enum FreqSort { FreqNoSort = 0, FreqDoSort = 1 };
+enum GroupSort { GroupNoSort = 0, GroupDoSort = 1 };
+
+// Partition settings. The reference hard-codes all of them except the CU
+// count, which it reads from the current device (utils/matrix_utils.cu:31-63);
+// cu_count == 0 means "the current device's multiProcessorCount".
+struct PartitionPolicy {
+  int cu_count = 0;
+};
+
+// Wall-clock milliseconds of the preprocessing stages (host timer, the stream
+// synchronised at each stage boundary only when timing was requested).
+struct PreprocessTimings {
+  double upload_ms = 0, analyze_ms = 0, rank_ms = 0, groups_ms = 0, sigbit_ms = 0,
+         signature_ms = 0, order_ms = 0, gather_ms = 0, total_ms = 0;
+};
+
+// Owns the GPU worksets built from host CSR arrays. Construct and destroy on
+// the same device; complete outstanding operator calls before destruction.
+class PowerSparseMatrixGPU {
+ public:
+  PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num, const int* row_ptr,
+                       const int* col_ind, const float* sp_data);
+  PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num, const int* row_ptr,
+                       const int* col_ind, const float* sp_data, const PartitionPolicy& policy,
+                       PreprocessTimings* timings = nullptr);
+  ~PowerSparseMatrixGPU() { Release(); }
+  PowerSparseMatrixGPU(const PowerSparseMatrixGPU&) = delete;
+  PowerSparseMatrixGPU& operator=(const PowerSparseMatrixGPU&) = delete;
+  PowerSparseMatrixGPU(PowerSparseMatrixGPU&&) = delete;
+  PowerSparseMatrixGPU& operator=(PowerSparseMatrixGPU&&) = delete;
+
+  int MatrixRow() const { return _matrix_row; }
+  int MatrixCol() const { return _matrix_col; }
+  int MatrixNNZ() const { return _matrix_nnz; }
+  int GroupTypeNum() const { return _group_type_num; }
+  int GroupFineSize() const { return _group_fine_size; }
+  const int* GroupNum() const { return _group_num; }
+  const int* const* WorksetColInd() const { return _workset_col_ind; }
+  const float* const* WorksetSpData() const { return _workset_sp_data; }
+  const int* const* GroupDestination() const { return _group_des; }
+  const int* ResidueOffset() const { return _residue_offset; }
+  const bool* ResidueAtomic() const { return _residue_atomic; }
+
+  // Not in the reference: the signature length L (bits) and the CU count the
+  // partition was computed for.
+  int SignatureLen() const { return _signature_len; }
+  int PartitionCuCount() const { return _cu_count; }
+
+ private:
+  void Build(const int* row_ptr, const int* col_ind, const float* sp_data,
+             PreprocessTimings* timings);
+  void Release() noexcept;
+
+  int _matrix_row, _matrix_col, _matrix_nnz;
+  int _group_type_num = 0, _group_fine_size = 16;
+  int _signature_len = 32;
+  int _cu_count = 0;
+  int* _group_num = nullptr;
+  int** _workset_col_ind = nullptr;
+  float** _workset_sp_data = nullptr;
+  int** _group_des = nullptr;
+  int* _residue_offset = nullptr;
+  bool* _residue_atomic = nullptr;
+};
+
+// The kernels use signed 32-bit dense element offsets (matrix_utils.h:71-76).
+inline void ValidateDenseShape(int rows, int cols, int n) {
+  if (n <= 0 || int64_t(rows) * n > std::numeric_limits<int>::max() ||
+      int64_t(cols) * n > std::numeric_limits<int>::max())
+    throw std::invalid_argument("Dense dimensions exceed the 32-bit kernel indexing range");
+}
+
+// Converts a C ABI status into the reference's exception types:
+// PS_ERR_INVALID -> std::invalid_argument, anything else -> std::runtime_error.
+void ThrowOnError(int status);
+
+}  // namespace PowerSparse

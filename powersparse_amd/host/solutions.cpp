@@ -1,0 +1,86 @@
+// Operator dispatchers: argument checks of the reference, then one fused
+// launch over every workset through the C ABI.
+//
+// The reference launches one kernel per workset on its own stream and then
+// synchronises the device when there is more than one workset
+// (PowerSparse_SpMM/spmm_solution.cu:7-34, PowerSparse_SDDMM/sddmm_solution.cu:7-50).
+// Here every workset is covered by a single launch (ps_spmm_launch /
+// ps_sddmm_launch), enqueued on the first supplied stream; the synchronisation
+// contract is kept: asynchronous for one workset, device-synchronising for more.
+#include <stdexcept>
+#include <vector>
+
+#include "PowerSparse_SDDMM.h"
+#include "PowerSparse_SpMM.h"
+
+namespace PowerSparse {
+namespace {
+
+std::vector<ps_workset> Worksets(const PowerSparseMatrixGPU& m) {
+  std::vector<ps_workset> ws(static_cast<size_t>(m.GroupTypeNum()));
+  for (int s = 0; s < m.GroupTypeNum(); ++s) {
+    ws[size_t(s)].col_ind = m.WorksetColInd()[s];
+    ws[size_t(s)].sp_data = m.WorksetSpData()[s];
+    ws[size_t(s)].group_des = m.GroupDestination()[s];
+    ws[size_t(s)].group_num = m.GroupNum()[s];
+    ws[size_t(s)].group_size = s == 0 ? 0 : GROUP_SIZE(s);
+  }
+  return ws;
+}
+
+void CheckSpmmArgs(const PowerSparseMatrixGPU& m, int N, const float* B, float* C) {
+  if (N <= 0 || N % 32 != 0 || N / 32 > 65535)
+    throw std::invalid_argument("SpMM requires N to be a positive multiple of 32, with N/32 <= 65535");
+  ValidateDenseShape(m.MatrixRow(), m.MatrixCol(), N);
+  if (!B || !C) throw std::invalid_argument("Invalid SpMM buffers or stream count");
+}
+
+void CheckSddmmArgs(const PowerSparseMatrixGPU& m, int N, const float* lhs, const float* rhs,
+                    const void* out) {
+  if (N <= 0 || N % 32 != 0 || N > 512)
+    throw std::invalid_argument(
+        "SDDMM dispatcher expects a width N that is a multiple of 32 between 32 and 512");
+  ValidateDenseShape(m.MatrixRow(), m.MatrixCol(), N);
+  if (!lhs || !rhs || !out) throw std::invalid_argument("Invalid SDDMM buffers or stream count");
+}
+
+}  // namespace
+
+void SpMMAsync(const PowerSparseMatrixGPU& m, int N, const float* B, float* C,
+               ps_stream_t stream) {
+  CheckSpmmArgs(m, N, B, C);
+  const auto ws = Worksets(m);
+  ThrowOnError(ps_spmm_launch(m.GroupTypeNum(), ws.data(), m.ResidueOffset(),
+                              reinterpret_cast<const uint8_t*>(m.ResidueAtomic()),
+                              m.MatrixRow(), m.MatrixCol(), N, B, C, stream));
+}
+
+void SpMM(const PowerSparseMatrixGPU& m, int N, const float* B, float* C, int stream_count,
+          const ps_stream_t* streams) {
+  CheckSpmmArgs(m, N, B, C);
+  if (stream_count != m.GroupTypeNum() || (stream_count > 1 && !streams))
+    throw std::invalid_argument("Invalid SpMM buffers or stream count");
+  SpMMAsync(m, N, B, C, stream_count == 1 ? nullptr : streams[0]);
+  if (stream_count > 1) ThrowOnError(ps_device_synchronize());
+}
+
+void SDDMMAsync(const PowerSparseMatrixGPU& m, int N, const float* lhs, const float* rhs,
+                float* const* out, ps_stream_t stream) {
+  CheckSddmmArgs(m, N, lhs, rhs, out);
+  for (int s = 0; s < m.GroupTypeNum(); ++s)
+    if (m.GroupNum()[s] != 0 && !out[s]) throw std::invalid_argument("Missing SDDMM output workset");
+  const auto ws = Worksets(m);
+  ThrowOnError(ps_sddmm_launch(m.GroupTypeNum(), ws.data(), m.ResidueOffset(), m.MatrixRow(),
+                               m.MatrixCol(), N, lhs, rhs, out, stream));
+}
+
+void SDDMM(const PowerSparseMatrixGPU& m, int N, const float* lhs, const float* rhs,
+           float** out, int stream_count, const ps_stream_t* streams) {
+  CheckSddmmArgs(m, N, lhs, rhs, out);
+  if (stream_count != m.GroupTypeNum() || (stream_count > 1 && !streams))
+    throw std::invalid_argument("Invalid SDDMM buffers or stream count");
+  SDDMMAsync(m, N, lhs, rhs, out, stream_count == 1 ? nullptr : streams[0]);
+  if (stream_count > 1) ThrowOnError(ps_device_synchronize());
+}
+
+}  // namespace PowerSparse

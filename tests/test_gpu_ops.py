@@ -1,0 +1,159 @@
+"""The drop-in API end to end on the GPU: PowerSparseMatrixGPU (GPU
+preprocessing) + SpMM / SDDMM with the reference's stream contract, against
+the oracle; argument errors; and size-independent properties at the full
+BASELINE sizes."""
+import numpy as np
+import pytest
+
+import oracle
+import powersparse_amd as ps
+import tolerance
+from gpu_util import say, setup
+
+pytestmark = pytest.mark.gpu
+
+
+def run_spmm(m, N, B, streams=None):
+    dB = ps.DeviceBuffer(host=B)
+    dC = ps.DeviceBuffer.zeros(m.MatrixRow() * N * 4)
+    S = m.GroupTypeNum()
+    if streams is None and S > 1:
+        streams = [ps.Stream() for _ in range(S)]
+    ps.SpMM(m, N, dB, dC, S, streams)
+    ps.synchronize()
+    return dC.download(np.float32).reshape(m.MatrixRow(), N)
+
+
+@pytest.mark.parametrize("cfg,scale,N", [("C0", 1, 32), ("C1", 20, 32), ("C1", 20, 128),
+                                         ("C4", 16, 64), ("C3", 40, 128)])
+def test_spmm_end_to_end(cfg, scale, N):
+    setup()
+    csr = ps.synth(cfg, seed=11, scale=scale)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr)
+    say(f"spmm {cfg}/{scale} N={N} S={m.GroupTypeNum()} groups={m.GroupNum()}")
+    B = np.random.default_rng(1).uniform(-1, 1, (csr.cols, N)).astype(np.float32)
+    C = run_spmm(m, N, B)
+    E, M = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, N, B, with_mag=True)
+    say("  ", tolerance.check(C, E, M, f"SpMM {cfg} N={N}"))
+
+
+@pytest.mark.parametrize("cfg,scale,N", [("C0", 1, 32), ("C1", 20, 128), ("C4", 16, 64),
+                                         ("C1", 20, 32)])
+def test_sddmm_end_to_end(cfg, scale, N):
+    setup()
+    csr = ps.synth(cfg, seed=12, scale=scale)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr)
+    S = m.GroupTypeNum()
+    say(f"sddmm {cfg}/{scale} N={N} S={S} groups={m.GroupNum()}")
+    rng = np.random.default_rng(2)
+    X = rng.normal(size=(csr.rows, N)).astype(np.float32)
+    Y = rng.normal(size=(csr.cols, N)).astype(np.float32)
+    dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
+    sizes = m.sddmm_output_sizes()
+    outs = [ps.DeviceBuffer.zeros(max(n, 1) * 4) for n in sizes]
+    streams = [ps.Stream() for _ in range(S)] if S > 1 else None
+    ps.SDDMM(m, N, dX, dY, outs, S, streams)
+    ps.synchronize()
+    offs0 = m.residue_offset()
+    for s in range(S):
+        if sizes[s] == 0:
+            continue
+        col, val, des = m.download_workset(s)
+        offs = offs0 if s == 0 else np.arange(m.GroupNum()[s] + 1) * ps.GROUP_SIZE(s)
+        E, Mg = oracle.sddmm(des, offs, col, val, N, X, Y, with_mag=True)
+        tolerance.check(outs[s].download(np.float32, sizes[s]), E, Mg, f"SDDMM {cfg} ws {s}")
+
+
+def test_api_argument_errors():
+    setup()
+    csr = ps.synth("C1", seed=13, scale=50)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=4)
+    S = m.GroupTypeNum()
+    assert S > 1
+    B = ps.DeviceBuffer(csr.cols * 128 * 4)
+    C = ps.DeviceBuffer(csr.rows * 128 * 4)
+    streams = [ps.Stream() for _ in range(S)]
+    with pytest.raises(ValueError, match="positive multiple of 32"):
+        ps.SpMM(m, 48, B, C, S, streams)
+    with pytest.raises(ValueError, match="positive multiple of 32"):
+        ps.SpMM(m, 0, B, C, S, streams)
+    with pytest.raises(ValueError, match="stream count"):
+        ps.SpMM(m, 32, B, C, S - 1, streams)
+    with pytest.raises(ValueError, match="stream count"):
+        ps.SpMM(m, 32, B, C, S, None)
+    with pytest.raises(ValueError, match="Invalid SpMM buffers"):
+        ps.SpMM(m, 32, None, C, S, streams)
+    with pytest.raises(ValueError, match="between 32 and 512"):
+        ps.SDDMM(m, 544, B, B, [C] * S, S, streams)
+    with pytest.raises(ValueError, match="Missing SDDMM output"):
+        ps.SDDMM(m, 32, B, B, [None] * S, S, streams)
+    with pytest.raises(ValueError, match="32-bit kernel indexing"):
+        ps.SpMM(m, 32 * (2 ** 31 // (32 * csr.cols) + 1), B, C, S, streams)
+
+
+def test_single_workset_async_default_stream():
+    # S == 1: the reference launches on the default stream without syncing
+    setup()
+    csr = ps.synth("C0", seed=14)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr)
+    assert m.GroupTypeNum() == 1
+    B = np.random.default_rng(3).uniform(-1, 1, (csr.cols, 32)).astype(np.float32)
+    C = run_spmm(m, 32, B, streams=None)
+    E, M = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, 32, B, with_mag=True)
+    tolerance.check(C, E, M, "SpMM C0 default stream")
+
+
+def per_row_checks(csr, m):
+    """Multiset of (row, col, value) preserved, via per-row counts and sums."""
+    rows = csr.rows
+    cnt = np.zeros(rows, np.int64)
+    s_col = np.zeros(rows, np.float64)
+    s_col2 = np.zeros(rows, np.float64)
+    s_val = np.zeros(rows, np.float64)
+    offs0 = m.residue_offset()
+    for s in range(m.GroupTypeNum()):
+        if m.GroupNum()[s] == 0:
+            continue
+        col, val, des = m.download_workset(s)
+        offs = offs0 if s == 0 else np.arange(m.GroupNum()[s] + 1, dtype=np.int64) * ps.GROUP_SIZE(s)
+        row_of = np.repeat(des, np.diff(offs))
+        cnt += np.bincount(row_of, minlength=rows)
+        s_col += np.bincount(row_of, weights=col.astype(np.float64), minlength=rows)
+        s_col2 += np.bincount(row_of, weights=col.astype(np.float64) ** 2, minlength=rows)
+        s_val += np.bincount(row_of, weights=val.astype(np.float64), minlength=rows)
+        if s > 0:
+            g = col.reshape(-1, ps.GROUP_SIZE(s))
+            assert (np.diff(g, axis=1) >= 0).all()
+    row_of = np.repeat(np.arange(rows), np.diff(csr.row_ptr))
+    np.testing.assert_array_equal(cnt, np.diff(csr.row_ptr))
+    np.testing.assert_array_equal(s_col, np.bincount(row_of, weights=csr.col_ind.astype(np.float64), minlength=rows))
+    np.testing.assert_array_equal(s_col2, np.bincount(row_of, weights=csr.col_ind.astype(np.float64) ** 2, minlength=rows))
+    np.testing.assert_allclose(s_val, np.bincount(row_of, weights=csr.values.astype(np.float64), minlength=rows), rtol=1e-12, atol=1e-9)
+
+
+@pytest.mark.parametrize("cfg", ["C1", "C4"])
+def test_full_size_properties(cfg):
+    """At the BASELINE size: worksets preserve every row's entries; SpMM against
+    an all-ones B gives each row's value sum, and SpMM is linear in B."""
+    setup()
+    csr = ps.synth(cfg, seed=1)
+    say(f"full {cfg}: rows={csr.rows} nnz={csr.nnz}")
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, timings=True)
+    say("  S", m.GroupTypeNum(), "groups", m.GroupNum(), "timings", m.timings)
+    per_row_checks(csr, m)
+    N = 32
+    ones = np.ones((csr.cols, N), np.float32)
+    C1 = run_spmm(m, N, ones)
+    row_sum = np.add.reduceat(np.concatenate([csr.values.astype(np.float64), [0]]),
+                              csr.row_ptr[:-1]) * (np.diff(csr.row_ptr) > 0)
+    row_abs = np.add.reduceat(np.concatenate([np.abs(csr.values.astype(np.float64)), [0]]),
+                              csr.row_ptr[:-1]) * (np.diff(csr.row_ptr) > 0)
+    tolerance.check(C1, np.repeat(row_sum[:, None], N, 1), np.repeat(row_abs[:, None], N, 1),
+                    f"{cfg} SpMM(ones)")
+    rng = np.random.default_rng(4)
+    B1 = rng.uniform(-1, 1, (csr.cols, N)).astype(np.float32)
+    B2 = rng.uniform(-1, 1, (csr.cols, N)).astype(np.float32)
+    Ca, Cb, Cab = run_spmm(m, N, B1), run_spmm(m, N, B2), run_spmm(m, N, B1 + B2)
+    _, M1 = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, N, np.abs(B1) + np.abs(B2),
+                        with_mag=True)
+    tolerance.check(Cab, Ca.astype(np.float64) + Cb, M1, f"{cfg} SpMM linearity")
