@@ -459,7 +459,7 @@ class PowerSparseMatrixGPU:
 def _streams(streams, count):
     if streams is None:
         return None
-    arr = (ctypes.c_void_p * max(count, 1))()
+    arr = (ctypes.c_void_p * max(count, len(streams), 1))()
     for i, s in enumerate(streams):
         arr[i] = _ptr(s)
     return arr

@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <type_traits>
 
 #include "powersparse_hip.h"
 
@@ -73,16 +74,40 @@ __device__ __forceinline__ float xor_shfl(float v) {
   return __int_as_float(r);
 }
 
-// Map a workgroup index to a logical index such that consecutive logical
-// indices stay on one XCD: the hardware deals workgroups round-robin over the 8
-// XCDs, and each XCD has its own L2, so neighbouring work (which shares B/Y rows
-// after the signature ordering) should land on the same XCD.
-__device__ __forceinline__ uint32_t xcd_remap(uint32_t block, uint32_t nblocks) {
-  constexpr uint32_t kXcd = 8;
-  const uint32_t q = nblocks / kXcd, r = nblocks % kXcd;
-  const uint32_t xcd = block % kXcd, idx = block / kXcd;
-  const uint32_t base = xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q;
-  return base + idx;
+// Workgroup -> logical index. The hardware deals workgroups round-robin over
+// the 8 XCDs, each with its own L2. Windows of 8 * kXcdChunk consecutive
+// workgroups are re-dealt so that each XCD takes kXcdChunk consecutive logical
+// indices: neighbouring tasks (which share B / Y rows after the signature
+// ordering) run under one L2, while every XCD still gets a slice of every
+// window, which keeps the XCDs balanced when task costs vary along the list.
+// The last, partial window keeps the hardware order.
+constexpr uint32_t kXcd = 8, kXcdChunk = 16;
+__device__ __forceinline__ uint32_t balanced_block(uint32_t b, uint32_t n) {
+  constexpr uint32_t kWin = kXcd * kXcdChunk;
+  const uint32_t w = b / kWin;
+  if ((w + 1) * kWin > n) return b;
+  return w * kWin + (b % kXcd) * kXcdChunk + (b / kXcd) % kXcdChunk;
 }
+
+// 128-bit loads at byte offsets from a base: through a buffer resource with
+// 32-bit offsets when the whole array fits 4 GiB (Off = uint32_t), plain
+// global loads with 64-bit offsets otherwise (Off = uint64_t).
+template <bool kBuf>
+struct Rows {
+  using Off = typename std::conditional<kBuf, uint32_t, uint64_t>::type;
+  __amdgpu_buffer_rsrc_t rsrc;
+  const char* base;
+  __device__ Rows(const float* m, uint64_t bytes) : base(reinterpret_cast<const char*>(m)) {
+    if constexpr (kBuf)
+      rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(m), (short)0, int(bytes),
+                                               0x00020000);
+  }
+  __device__ __forceinline__ float4 load(Off off) const {
+    if constexpr (kBuf)
+      return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+    else
+      return *reinterpret_cast<const float4*>(base + off);
+  }
+};
 
 }  // namespace ps

@@ -34,21 +34,9 @@ struct SddmmArgs {
   const int* residue_offset;
   const float* lhs;
   const float* rhs;
+  uint64_t lhs_bytes;
+  uint64_t rhs_bytes;
 };
-
-template <int KQ>
-__device__ __forceinline__ float partial_dot(const float4 (&x)[KQ], const float* y) {
-  float s = 0.f;
-#pragma unroll
-  for (int q = 0; q < KQ; ++q) {
-    const float4 v = *reinterpret_cast<const float4*>(y + 32 * q);
-    s = fmaf(x[q].x, v.x, s);
-    s = fmaf(x[q].y, v.y, s);
-    s = fmaf(x[q].z, v.z, s);
-    s = fmaf(x[q].w, v.w, s);
-  }
-  return s;
-}
 
 // Transposing reduction over the 8 lanes of a slot: in p[j] each lane holds
 // its partial for nonzero j of the slot; returns the full sum for j == sub.
@@ -73,10 +61,42 @@ __device__ __forceinline__ float slot_transpose_sum(const float (&p)[8], int sub
   return keep + xor_shfl<1>(send);
 }
 
-template <int KQ>
+// Partial dots of the 8 nonzeros of this lane's slot (Y row byte offsets in
+// yoff[]), `kSteps` nonzeros per batch so that about 16 loads are in flight.
+template <int KQ, bool kBuf>
+__device__ __forceinline__ void slot_dots(const Rows<kBuf>& Y,
+                                          const typename Rows<kBuf>::Off (&yoff)[8],
+                                          const float4 (&x)[KQ], float (&p)[8]) {
+  // a power of two dividing the 8 steps, about 16 / KQ
+  constexpr int kSteps = KQ <= 2 ? 8 : (KQ <= 4 ? 4 : (KQ <= 8 ? 2 : 1));
+  static_assert(8 % kSteps == 0, "batches must tile the slot's 8 nonzeros");
+#pragma unroll
+  for (int b = 0; b < 8; b += kSteps) {
+    float4 y[kSteps][KQ];
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u)
+#pragma unroll
+      for (int q = 0; q < KQ; ++q) y[u][q] = Y.load(yoff[b + u] + 128u * uint32_t(q));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+      float s = 0.f;
+#pragma unroll
+      for (int q = 0; q < KQ; ++q) {
+        s = fmaf(x[q].x, y[u][q].x, s);
+        s = fmaf(x[q].y, y[u][q].y, s);
+        s = fmaf(x[q].z, y[u][q].z, s);
+        s = fmaf(x[q].w, y[u][q].w, s);
+      }
+      p[b + u] = s;
+    }
+  }
+}
+
+template <int KQ, bool kBuf>
 __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs args) {
   constexpr int K = 32 * KQ;
-  const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x);
+  const uint32_t blk = balanced_block(blockIdx.x, gridDim.x);
   const uint32_t task =
       __builtin_amdgcn_readfirstlane(blk * kWavesPerBlock + threadIdx.x / kWave);
   if (task >= args.total_tasks) return;
@@ -88,9 +108,13 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
 
   const int lane = lane_id();
   const int slot = lane / 8, sub = lane % 8;
-  const float* __restrict__ Y = args.rhs + sub * 4;
+  const Rows<kBuf> X(args.lhs, args.lhs_bytes), Y(args.rhs, args.rhs_bytes);
+  using Off = typename Rows<kBuf>::Off;
+  const uint32_t row_bytes = uint32_t(K) * 4u;
+  const uint32_t piece = uint32_t(sub) * 16u;
   float4 x[KQ];
   float p[8];
+  Off yoff[8];
 
   if (ws.group_size > 0) {
     const int total = ws.group_num * ws.group_size;
@@ -98,17 +122,17 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     const bool valid = p0 < total;
     const int g = valid ? p0 / ws.group_size : 0;
     const int row = valid ? ws.group_des[g] : 0;
-    const float* xr = args.lhs + row * K + sub * 4;
-#pragma unroll
-    for (int q = 0; q < KQ; ++q) x[q] = *reinterpret_cast<const float4*>(xr + 32 * q);
     int4 c0 = make_int4(0, 0, 0, 0), c1 = make_int4(0, 0, 0, 0);
     if (valid) {
       c0 = *reinterpret_cast<const int4*>(ws.col_ind + p0);
       c1 = *reinterpret_cast<const int4*>(ws.col_ind + p0 + 4);
     }
+#pragma unroll
+    for (int q = 0; q < KQ; ++q) x[q] = X.load(Off(uint32_t(row)) * row_bytes + piece + 128u * q);
     const int c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) p[j] = partial_dot<KQ>(x, Y + c[j] * K);
+    for (int j = 0; j < 8; ++j) yoff[j] = Off(uint32_t(c[j])) * row_bytes + piece;
+    slot_dots<KQ, kBuf>(Y, yoff, x, p);
     const float dot = slot_transpose_sum(p, sub);
     const int pos = local * 64 + lane;
     if (valid) out[pos] = dot * ws.sp_data[pos];
@@ -120,17 +144,20 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     const int beg = has ? args.residue_offset[g] : 0;
     const int len = has ? args.residue_offset[g + 1] - beg : 0;
     const int row = has ? ws.group_des[g] : 0;
-    const float* xr = args.lhs + row * K + sub * 4;
 #pragma unroll
-    for (int qq = 0; qq < KQ; ++qq) x[qq] = *reinterpret_cast<const float4*>(xr + 32 * qq);
+    for (int qq = 0; qq < KQ; ++qq)
+      x[qq] = X.load(Off(uint32_t(row)) * row_bytes + piece + 128u * qq);
     const int first = (q / 8) * 8;  // first nonzero of this lane's slot in a chunk
+#pragma unroll 1
     for (int c0 = 0; __any(c0 < len); c0 += rcap) {
+      // nonzeros past the group's end re-read its last column and are dropped
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int k = c0 + first + j;
-        const int col = k < len ? ws.col_ind[beg + k] : -1;
-        p[j] = col >= 0 ? partial_dot<KQ>(x, Y + col * K) : 0.f;
+        const int kk = k < len ? k : len - 1;
+        yoff[j] = len > 0 ? Off(uint32_t(ws.col_ind[beg + kk])) * row_bytes + piece : Off(piece);
       }
+      slot_dots<KQ, kBuf>(Y, yoff, x, p);
       const float dot = slot_transpose_sum(p, sub);
       const int k = c0 + q;
       if (k < len) unsafeAtomicAdd(out + beg + k, dot * ws.sp_data[beg + k]);
@@ -139,8 +166,9 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
 }
 
 template <int KQ>
-void launch_kq(const SddmmArgs& a, unsigned grid, hipStream_t stream) {
-  sddmm_kernel<KQ><<<grid, kWave * kWavesPerBlock, 0, stream>>>(a);
+void launch_kq(const SddmmArgs& a, bool buf, unsigned grid, hipStream_t stream) {
+  if (buf) sddmm_kernel<KQ, true><<<grid, kWave * kWavesPerBlock, 0, stream>>>(a);
+  else sddmm_kernel<KQ, false><<<grid, kWave * kWavesPerBlock, 0, stream>>>(a);
 }
 
 int launch(int count, const int* order, const ps_workset* worksets, float* const* outs,
@@ -156,6 +184,11 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
   a.rcap = rcap;
   a.lhs = lhs;
   a.rhs = rhs;
+  const uint64_t lhs_bytes = uint64_t(rows) * uint64_t(N) * 4u;
+  const uint64_t rhs_bytes = uint64_t(cols) * uint64_t(N) * 4u;
+  const bool buf = lhs_bytes <= 0xFFFFFFFFull && rhs_bytes <= 0xFFFFFFFFull;
+  a.lhs_bytes = lhs_bytes;
+  a.rhs_bytes = rhs_bytes;
   a.residue_offset = residue_offset;
   uint64_t tasks = 0;
   int n = 0;
@@ -189,22 +222,22 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
   a.total_tasks = uint32_t(tasks);
   const unsigned grid = unsigned((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
   switch (N / 32) {
-    case 1: launch_kq<1>(a, grid, stream); break;
-    case 2: launch_kq<2>(a, grid, stream); break;
-    case 3: launch_kq<3>(a, grid, stream); break;
-    case 4: launch_kq<4>(a, grid, stream); break;
-    case 5: launch_kq<5>(a, grid, stream); break;
-    case 6: launch_kq<6>(a, grid, stream); break;
-    case 7: launch_kq<7>(a, grid, stream); break;
-    case 8: launch_kq<8>(a, grid, stream); break;
-    case 9: launch_kq<9>(a, grid, stream); break;
-    case 10: launch_kq<10>(a, grid, stream); break;
-    case 11: launch_kq<11>(a, grid, stream); break;
-    case 12: launch_kq<12>(a, grid, stream); break;
-    case 13: launch_kq<13>(a, grid, stream); break;
-    case 14: launch_kq<14>(a, grid, stream); break;
-    case 15: launch_kq<15>(a, grid, stream); break;
-    default: launch_kq<16>(a, grid, stream); break;
+    case 1: launch_kq<1>(a, buf, grid, stream); break;
+    case 2: launch_kq<2>(a, buf, grid, stream); break;
+    case 3: launch_kq<3>(a, buf, grid, stream); break;
+    case 4: launch_kq<4>(a, buf, grid, stream); break;
+    case 5: launch_kq<5>(a, buf, grid, stream); break;
+    case 6: launch_kq<6>(a, buf, grid, stream); break;
+    case 7: launch_kq<7>(a, buf, grid, stream); break;
+    case 8: launch_kq<8>(a, buf, grid, stream); break;
+    case 9: launch_kq<9>(a, buf, grid, stream); break;
+    case 10: launch_kq<10>(a, buf, grid, stream); break;
+    case 11: launch_kq<11>(a, buf, grid, stream); break;
+    case 12: launch_kq<12>(a, buf, grid, stream); break;
+    case 13: launch_kq<13>(a, buf, grid, stream); break;
+    case 14: launch_kq<14>(a, buf, grid, stream); break;
+    case 15: launch_kq<15>(a, buf, grid, stream); break;
+    default: launch_kq<16>(a, buf, grid, stream); break;
   }
   PS_LAUNCHED();
   return PS_OK;

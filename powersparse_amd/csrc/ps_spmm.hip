@@ -1,16 +1,34 @@
 // SpMM (node aggregation), C += A * B, FP32, on gfx950.
 //
 // One launch covers every workset of a PowerSparse matrix. The grid is a flat
-// list of wave tasks; each wave64 decodes its task from a small table in the
-// kernel arguments:
-//   block workset s (groups of GS = 32 * 2^(s-1) nonzeros): a task is a tile of
-//     T = min(GS, 256) consecutive nonzeros of one group and one N-slice;
-//   residue workset: a task is one residue group and one N-slice.
-// Inside a wave the 64 lanes form SL = 64 / LPN slots of LPN lanes; a slot
-// reads one B row slice of 4 * LPN floats with 128-bit loads, so one wave
-// instruction gathers SL rows. Each slot walks its own run of nonzeros, then
-// the slots are summed with DPP / swizzle butterflies and the row result is
-// added atomically (or stored, for residue groups whose row has no other group).
+// list of wave tasks; each wave64 decodes its task from a table in the kernel
+// arguments. Lanes form SL = 64 / LPN slots of LPN lanes; a slot reads one B-row
+// slice of 4 * LPN floats with 128-bit loads, so one wave instruction gathers SL
+// B rows. Every lane accumulates a float4 of its slot's output row.
+//
+//   block workset (groups of GS = 32 * 2^(s-1) nonzeros): a task is a tile of
+//     T = 32 * SL consecutive stored nonzeros; slot q owns nonzeros
+//     [32q, 32q + 32) of the tile. When GS < T a tile holds T / GS whole groups
+//     (GS / 32 slots each), otherwise it is a piece of one group. Slots of the
+//     same group are summed with DPP / swizzle butterflies and the group's row
+//     is added to C with atomics.
+//   residue workset: a task is SL consecutive groups, one per slot; a slot
+//     walks its group (at most 31 nonzeros) alone, so no cross-slot sum is
+//     needed, and writes its row with atomics when the row has other groups,
+//     with a plain store otherwise.
+//
+// Each task first stages its nonzeros in LDS with coalesced loads, as
+// (byte offset of the B row, value) pairs, so the gather loop issues 16
+// independent 128-bit B loads per lane with no dependent index load in
+// between. B is addressed through a buffer resource with 32-bit offsets when
+// cols * N * 4 fits in 32 bits.
+//
+// Workgroup -> task mapping: the hardware deals workgroups round-robin over
+// the 8 XCDs. Windows of 8 * kChunk consecutive workgroups are re-dealt so
+// that each XCD takes kChunk consecutive ones: neighbouring tasks (similar
+// column signatures) share an XCD's L2, while every XCD still gets a slice of
+// every window, which keeps the XCDs balanced when task costs vary along the
+// list (blocks of large groups first, residue groups last).
 //
 // Reference behaviour kept (PowerSparse_SpMM/spmm_solution.cu:7-34,
 // spmm_kernel_block.cu:60-162, spmm_kernel_residue.cu:5-82): block groups and
@@ -22,16 +40,18 @@ namespace ps {
 namespace {
 
 constexpr int kWavesPerBlock = 4;
-constexpr int kBlockTile = 256;  // nonzeros per block-workset wave task (max)
+constexpr int kPer = 32;          // nonzeros per slot per block tile
+constexpr int kSlotWords = 2 * kPer + 4;  // LDS words per slot (pairs + pad)
+constexpr int kBatch = 16;        // B loads in flight per lane
 
 struct SpmmArgs {
   ps_workset ws[PS_MAX_WORKSETS];
   uint32_t task_begin[PS_MAX_WORKSETS + 1];
-  int32_t tiles_per_group[PS_MAX_WORKSETS];
   int32_t count;
   int32_t N;
   int32_t slices;
   uint32_t total_tasks;
+  uint64_t b_bytes;  // size of B in bytes
   const int* residue_offset;
   const uint8_t* residue_atomic;
   const float* B;
@@ -45,42 +65,34 @@ __device__ __forceinline__ void fma4(float4& acc, float a, const float4& b) {
   acc.w = fmaf(a, b.w, acc.w);
 }
 
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Sums acc over the `spg` slots of each group (spg a power of two <= SL).
 template <int LPN>
-__device__ __forceinline__ float slot_sum(float v) {
-  if constexpr (LPN <= 8) v += xor_shfl<8>(v);
-  if constexpr (LPN <= 16) v += xor_shfl<16>(v);
-  if constexpr (LPN <= 32) v += xor_shfl<32>(v);
+__device__ __forceinline__ float group_sum(float v, int spg) {
+  if constexpr (LPN <= 32) {
+    if (spg >= 2) v += xor_shfl<LPN>(v);
+  }
+  if constexpr (LPN <= 16) {
+    if (spg >= 4) v += xor_shfl<2 * LPN>(v);
+  }
+  if constexpr (LPN <= 8) {
+    if (spg >= 8) v += xor_shfl<4 * LPN>(v);
+  }
   return v;
 }
 
-// Adds (atomic) or stores the slot-reduced float4 of every lane into row `row`.
-template <int LPN>
-__device__ __forceinline__ void write_row(float* C, int row, int N, int col0, float4 acc,
-                                          bool atomic) {
-  constexpr int SL = 64 / LPN;
-  const int lane = lane_id();
-  const int slot = lane / LPN, sub = lane % LPN;
-  acc.x = slot_sum<LPN>(acc.x);
-  acc.y = slot_sum<LPN>(acc.y);
-  acc.z = slot_sum<LPN>(acc.z);
-  acc.w = slot_sum<LPN>(acc.w);
-  float* out = C + row * N + col0 + sub * 4;
-  if (atomic) {
-    const float v[4] = {acc.x, acc.y, acc.z, acc.w};
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      if (c % SL == slot) unsafeAtomicAdd(out + c, v[c]);
-  } else if (slot == 0) {
-    *reinterpret_cast<float4*>(out) = acc;
-  }
-}
-
-template <int LPN>
+template <int LPN, bool kBuf>
 __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs args) {
   constexpr int SL = 64 / LPN;
-  const uint32_t blk = xcd_remap(blockIdx.x, gridDim.x);
-  const uint32_t task =
-      __builtin_amdgcn_readfirstlane(blk * kWavesPerBlock + threadIdx.x / kWave);
+  __shared__ __attribute__((aligned(16))) int lds[kWavesPerBlock][SL * kSlotWords];
+  const int wave = threadIdx.x / kWave;
+  const uint32_t blk = balanced_block(blockIdx.x, gridDim.x);
+  const uint32_t task = __builtin_amdgcn_readfirstlane(blk * kWavesPerBlock + wave);
   if (task >= args.total_tasks) return;
   int i = 0;
   while (i + 1 < args.count && task >= args.task_begin[i + 1]) ++i;
@@ -93,74 +105,137 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs ar
 
   const int lane = lane_id();
   const int slot = lane / LPN, sub = lane % LPN;
-  const float4* __restrict__ B4 = reinterpret_cast<const float4*>(args.B + col0) + sub;
-  const int n4 = N / 4;
+  using Off = typename Rows<kBuf>::Off;
+  const uint32_t row_bytes = uint32_t(N) * 4u;
+  const Rows<kBuf> Bq(args.B + col0, args.b_bytes - uint64_t(col0) * 4u);
+  const uint32_t my_off = uint32_t(sub) * 16u;
+  // LDS holds B-row byte offsets when they fit 32 bits, column ids otherwise
+  auto stage_key = [&](int c) -> int { return kBuf ? int(uint32_t(c) * row_bytes) : c; };
+  auto row_off = [&](int key) -> Off {
+    return kBuf ? Off(uint32_t(key)) + my_off : Off(uint32_t(key)) * row_bytes + my_off;
+  };
+  int* const my_lds = lds[wave];
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 
   if (ws.group_size > 0) {
-    // Block workset: tile `t` of group `g`, every slot owns per = T / SL
-    // consecutive nonzeros (a multiple of 4, so 128-bit index loads).
-    const int tiles = args.tiles_per_group[i];
-    const int g = int(local / uint32_t(tiles));
-    const int t = int(local % uint32_t(tiles));
-    const int T = ws.group_size / tiles;
-    const int per = T / SL;
-    const int begin = g * ws.group_size + t * T + slot * per;
-    const int* cp = ws.col_ind + begin;
-    const float* vp = ws.sp_data + begin;
-    int j = 0;
-    for (; j + 8 <= per; j += 8) {
-      const int4 c0 = *reinterpret_cast<const int4*>(cp + j);
-      const int4 c1 = *reinterpret_cast<const int4*>(cp + j + 4);
-      const float4 v0 = *reinterpret_cast<const float4*>(vp + j);
-      const float4 v1 = *reinterpret_cast<const float4*>(vp + j + 4);
-      const float4 b0 = B4[c0.x * n4], b1 = B4[c0.y * n4], b2 = B4[c0.z * n4],
-                   b3 = B4[c0.w * n4], b4 = B4[c1.x * n4], b5 = B4[c1.y * n4],
-                   b6 = B4[c1.z * n4], b7 = B4[c1.w * n4];
-      fma4(acc, v0.x, b0);
-      fma4(acc, v0.y, b1);
-      fma4(acc, v0.z, b2);
-      fma4(acc, v0.w, b3);
-      fma4(acc, v1.x, b4);
-      fma4(acc, v1.y, b5);
-      fma4(acc, v1.z, b6);
-      fma4(acc, v1.w, b7);
-    }
-    if (j < per) {  // per == 4
-      const int4 c0 = *reinterpret_cast<const int4*>(cp + j);
-      const float4 v0 = *reinterpret_cast<const float4*>(vp + j);
-      const float4 b0 = B4[c0.x * n4], b1 = B4[c0.y * n4], b2 = B4[c0.z * n4],
-                   b3 = B4[c0.w * n4];
-      fma4(acc, v0.x, b0);
-      fma4(acc, v0.y, b1);
-      fma4(acc, v0.z, b2);
-      fma4(acc, v0.w, b3);
-    }
-    write_row<LPN>(args.C, ws.group_des[g], N, col0, acc, true);
-  } else {
-    // Residue workset: one group per wave, nonzero k goes to slot k % SL.
-    const int g = int(local);
-    const int beg = args.residue_offset[g];
-    const int len = args.residue_offset[g + 1] - beg;
-    const int* cp = ws.col_ind + beg;
-    const float* vp = ws.sp_data + beg;
-    for (int k0 = 0; k0 < len; k0 += 4 * SL) {
-      int c[4];
-      float v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int k = k0 + u * SL + slot;
-        const bool ok = k < len;
-        c[u] = ok ? cp[k] : 0;
-        v[u] = ok ? vp[k] : 0.f;
+    // ---------------------------------------------------------- block tile
+    constexpr int T = kPer * SL;
+    const int GS = ws.group_size;
+    const int spg = GS / kPer < SL ? GS / kPer : SL;  // slots per group
+    const long long total = (long long)ws.group_num * GS;
+    const long long tile = (long long)local * T;
+    // stage: lane l holds nonzeros 4l .. 4l+3 of the tile
+    if (lane * 4 < T) {
+      const long long p = tile + lane * 4;
+      int4 c = make_int4(0, 0, 0, 0);
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (p < total) {
+        c = *reinterpret_cast<const int4*>(ws.col_ind + p);
+        v = *reinterpret_cast<const float4*>(ws.sp_data + p);
       }
-      float4 b[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) b[u] = B4[c[u] * n4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) fma4(acc, v[u], b[u]);
+      const int k = lane * 4, q = k / kPer, j = k % kPer;
+      int4* dst = reinterpret_cast<int4*>(my_lds + q * kSlotWords + 2 * j);
+      dst[0] = make_int4(stage_key(c.x), __float_as_int(v.x), stage_key(c.y), __float_as_int(v.y));
+      dst[1] = make_int4(stage_key(c.z), __float_as_int(v.z), stage_key(c.w), __float_as_int(v.w));
     }
-    write_row<LPN>(args.C, ws.group_des[g], N, col0, acc, args.residue_atomic[g] != 0);
+    wave_lds_sync();
+    const long long slot_first = tile + slot * kPer;
+    const int4* src = reinterpret_cast<const int4*>(my_lds + slot * kSlotWords);
+#pragma unroll 1
+    for (int b0 = 0; b0 < kPer; b0 += kBatch) {
+      Off off[kBatch];
+      float val[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; u += 2) {
+        const int4 w = src[(b0 + u) / 2];
+        off[u] = row_off(w.x);
+        val[u] = __int_as_float(w.y);
+        off[u + 1] = row_off(w.z);
+        val[u + 1] = __int_as_float(w.w);
+      }
+      float4 bv[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) bv[u] = Bq.load(off[u]);
+      // keep the whole batch of loads in flight before the first use
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) fma4(acc, val[u], bv[u]);
+    }
+    acc.x = group_sum<LPN>(acc.x, spg);
+    acc.y = group_sum<LPN>(acc.y, spg);
+    acc.z = group_sum<LPN>(acc.z, spg);
+    acc.w = group_sum<LPN>(acc.w, spg);
+    if (slot_first < total) {
+      const int r = slot % spg;  // this slot's rank inside its group
+      const int row = ws.group_des[int(slot_first / GS)];
+      float* out = args.C + row * N + col0 + sub * 4;
+      // every slot of the group holds the sum; component c goes to rank c % spg
+      const float v4[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (c % spg == r) unsafeAtomicAdd(out + c, v4[c]);
+    }
+  } else {
+    // ------------------------------------------------------- residue groups
+    const int G = ws.group_num;
+    const int g0 = int(local) * SL;
+    const int gend = g0 + SL < G ? g0 + SL : G;
+    const int range_begin = args.residue_offset[g0];
+    const int range_len = args.residue_offset[gend] - range_begin;
+    // Residue groups built by the preprocessing hold at most 31 nonzeros, so
+    // the wave's groups fit the LDS slot area; longer ones are read directly.
+    const bool staged = range_len <= SL * kSlotWords / 2;
+    if (staged) {
+      for (int k = lane; k < range_len; k += kWave) {
+        const int c = ws.col_ind[range_begin + k];
+        const float v = ws.sp_data[range_begin + k];
+        *reinterpret_cast<int2*>(my_lds + 2 * k) = make_int2(stage_key(c), __float_as_int(v));
+      }
+    }
+    wave_lds_sync();
+    const int g = g0 + slot;
+    const bool has = g < gend;
+    const int start = has ? args.residue_offset[g] - range_begin : 0;
+    const int len = has ? args.residue_offset[g + 1] - range_begin - start : 0;
+#pragma unroll 1
+    for (int j0 = 0; __any(j0 < len); j0 += kBatch) {
+      Off off[kBatch];
+      float val[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int j = j0 + u;
+        const int jj = j < len ? j : (len > 0 ? len - 1 : 0);
+        int2 w;
+        if (staged) {
+          w = *reinterpret_cast<const int2*>(my_lds + 2 * (start + jj));
+        } else {
+          const int p = range_begin + start + jj;
+          w = make_int2(stage_key(len > 0 ? ws.col_ind[p] : 0),
+                        __float_as_int(len > 0 ? ws.sp_data[p] : 0.f));
+        }
+        off[u] = row_off(len > 0 ? w.x : 0);
+        val[u] = j < len ? __int_as_float(w.y) : 0.f;
+      }
+      float4 bv[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) bv[u] = Bq.load(off[u]);
+      // keep the whole batch of loads in flight before the first use
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) fma4(acc, val[u], bv[u]);
+    }
+    if (has && len > 0) {
+      const int row = ws.group_des[g];
+      float* out = args.C + row * N + col0 + sub * 4;
+      if (args.residue_atomic[g]) {
+        unsafeAtomicAdd(out + 0, acc.x);
+        unsafeAtomicAdd(out + 1, acc.y);
+        unsafeAtomicAdd(out + 2, acc.z);
+        unsafeAtomicAdd(out + 3, acc.w);
+      } else {
+        *reinterpret_cast<float4*>(out) = acc;
+      }
+    }
   }
 }
 
@@ -173,15 +248,22 @@ int pick_lpn(int N) {
   return 8;
 }
 
+template <int LPN>
+void launch_lpn(const SpmmArgs& a, bool buf, unsigned grid, hipStream_t stream) {
+  const dim3 block(kWave * kWavesPerBlock);
+  if (buf) spmm_kernel<LPN, true><<<grid, block, 0, stream>>>(a);
+  else spmm_kernel<LPN, false><<<grid, block, 0, stream>>>(a);
+}
+
 int launch(int count, const int* order, const ps_workset* worksets, const int* residue_offset,
            const uint8_t* residue_atomic, int rows, int cols, int N, const float* B, float* C,
            hipStream_t stream) {
-  PS_CHECK_ARG(N > 0 && N % 32 == 0,
-               "SpMM requires N to be a positive multiple of 32");
+  PS_CHECK_ARG(N > 0 && N % 32 == 0, "SpMM requires N to be a positive multiple of 32");
   PS_CHECK_ARG(int64_t(rows) * N <= INT32_MAX && int64_t(cols) * N <= INT32_MAX,
                "Dense dimensions exceed the 32-bit kernel indexing range");
   PS_CHECK_ARG(B && C, "Invalid SpMM buffers");
   const int lpn = pick_lpn(N);
+  const int SL = 64 / lpn;
   SpmmArgs a{};
   a.N = N;
   a.slices = N / (4 * lpn);
@@ -189,6 +271,10 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
   a.C = C;
   a.residue_offset = residue_offset;
   a.residue_atomic = residue_atomic;
+  const uint64_t b_bytes = uint64_t(cols) * uint64_t(N) * 4u;
+  // Buffer offsets are 32-bit: use them when every byte of B is addressable.
+  const bool buf = b_bytes <= 0xFFFFFFFFull;
+  a.b_bytes = b_bytes;
   uint64_t tasks = 0;
   int n = 0;
   for (int q = 0; q < count; ++q) {
@@ -196,19 +282,20 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
     const ps_workset& w = worksets[q];
     if (w.group_num <= 0) continue;
     PS_CHECK_ARG(w.col_ind && w.sp_data && w.group_des, "Invalid SpMM workset buffers");
-    int tiles = 1;
+    uint64_t t;
     if (s > 0) {
       PS_CHECK_ARG(w.group_size >= 32 && (w.group_size & (w.group_size - 1)) == 0,
                    "Block workset group size must be a power of two >= 32");
-      tiles = w.group_size > kBlockTile ? w.group_size / kBlockTile : 1;
+      const uint64_t T = uint64_t(kPer) * SL;
+      t = (uint64_t(w.group_num) * uint64_t(w.group_size) + T - 1) / T;
     } else {
       PS_CHECK_ARG(residue_offset && residue_atomic, "Missing residue offsets or flags");
+      t = (uint64_t(w.group_num) + SL - 1) / SL;
     }
     a.ws[n] = w;
     if (s == 0) a.ws[n].group_size = 0;
-    a.tiles_per_group[n] = tiles;
     a.task_begin[n] = uint32_t(tasks);
-    tasks += uint64_t(w.group_num) * tiles * a.slices;
+    tasks += t * uint64_t(a.slices);
     ++n;
   }
   if (n == 0) return PS_OK;
@@ -217,12 +304,11 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
   a.task_begin[n] = uint32_t(tasks);
   a.total_tasks = uint32_t(tasks);
   const unsigned grid = unsigned((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
-  const dim3 block(kWave * kWavesPerBlock);
   switch (lpn) {
-    case 8: spmm_kernel<8><<<grid, block, 0, stream>>>(a); break;
-    case 16: spmm_kernel<16><<<grid, block, 0, stream>>>(a); break;
-    case 32: spmm_kernel<32><<<grid, block, 0, stream>>>(a); break;
-    default: spmm_kernel<64><<<grid, block, 0, stream>>>(a); break;
+    case 8: launch_lpn<8>(a, buf, grid, stream); break;
+    case 16: launch_lpn<16>(a, buf, grid, stream); break;
+    case 32: launch_lpn<32>(a, buf, grid, stream); break;
+    default: launch_lpn<64>(a, buf, grid, stream); break;
   }
   PS_LAUNCHED();
   return PS_OK;
