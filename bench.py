@@ -55,6 +55,20 @@ def algorithmic_bytes(op, nnz, rows, cols, n):
     return 12 * nnz + 4 * (rows + 1) + 4 * n * rows + 4 * n * cols  # + outputs
 
 
+def measured_traffic(config, op, n):
+    """HBM bytes per launch of the operator kernel, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary of the same workload
+    (profiles/traffic_<config>.json, made by `python -m powersparse_amd.perf
+    summarize`), or None when no summary exists."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{config}.json")
+    try:
+        with open(path) as fh:
+            t = json.load(fh)["traffic"][f"{op}_N{n}"]
+        return t["traffic_bytes"], os.path.relpath(path, ROOT)
+    except (OSError, KeyError, ValueError):
+        return None, None
+
+
 def cpu_baseline(csr, host_ops, reps=3):
     """Times the oracle (OpenMP, double accumulation) on the same workload."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -172,6 +186,7 @@ def main():
             f"{detail[-1]['alg_GBps']:.0f} GB/s ({100 * detail[-1]['roofline_frac']:.1f}% of 8 TB/s)")
     dom = max(detail, key=lambda d: d["ms"])
     kernel = "ps::spmm_kernel" if dom["op"] == "spmm" else "ps::sddmm_kernel"
+    traffic, traffic_src = measured_traffic(args.config, dom["op"], dom["N"])
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -206,7 +221,8 @@ def main():
         "ops": detail,
         "roofline": {"bound": "hbm", "kernel": kernel, "op": f"{dom['op']} N={dom['N']}",
                      "achieved": dom["alg_GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": dom["roofline_frac"], "traffic": None},
+                     "frac": dom["roofline_frac"], "traffic": traffic,
+                     "traffic_source": traffic_src},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -83,6 +83,11 @@ int ps_memset_async(void* dst, int value, size_t bytes, ps_stream_t stream);
 int ps_fill_random_async(float* dst, size_t count, uint64_t seed, float lo, float hi,
                          int normal, ps_stream_t stream);
 
+/* Streaming copy of `count` floats with 128-bit loads and stores (a plain
+ * kernel, never a DMA engine): the reference point for HBM bandwidth and for
+ * scaling the FETCH_SIZE / WRITE_SIZE counters. No reference counterpart. */
+int ps_copy_f32_async(float* dst, const float* src, size_t count, ps_stream_t stream);
+
 /* ------------------------------------------------------- streams, events */
 /* Replaces: cudaStreamCreate / cudaStreamDestroy (benchmark_utils.h:48-66). */
 int ps_stream_create(ps_stream_t* stream);

@@ -75,6 +75,7 @@ HIP_API = [
     ("ps_fill_random_async", ctypes.c_int,
      [c_void_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_int,
       c_void_p]),
+    ("ps_copy_f32_async", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
     ("ps_stream_create", ctypes.c_int, [ctypes.POINTER(c_void_p)]),
     ("ps_stream_destroy", ctypes.c_int, [c_void_p]),
     ("ps_stream_synchronize", ctypes.c_int, [c_void_p]),

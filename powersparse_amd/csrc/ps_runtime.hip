@@ -45,10 +45,45 @@ __global__ void fill_random_kernel(float* __restrict__ dst, size_t count, uint64
   }
 }
 
+__global__ void copy_f32_kernel(float4* __restrict__ dst, const float4* __restrict__ src,
+                                size_t n4) {
+  const size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride)
+    dst[i] = src[i];
+}
+
+__global__ void copy_tail_kernel(float* __restrict__ dst, const float* __restrict__ src,
+                                 size_t begin, size_t count) {
+  const size_t i = begin + size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < count) dst[i] = src[i];
+}
+
 }  // namespace
 }  // namespace ps
 
 extern "C" {
+
+int ps_copy_f32_async(float* dst, const float* src, size_t count, ps_stream_t stream) {
+  if (count == 0) return PS_OK;
+  PS_CHECK_ARG(dst && src, "ps_copy_f32_async: null pointer");
+  PS_CHECK_ARG((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) % 16 == 0,
+               "ps_copy_f32_async: buffers must be 16-byte aligned");
+  hipStream_t st = ps::to_hip(stream);
+  const size_t n4 = count / 4;
+  if (n4) {
+    // 8 workgroups of 256 per CU-ish: enough to saturate HBM with a grid-stride loop
+    const size_t blocks = (n4 + 255) / 256;
+    ps::copy_f32_kernel<<<unsigned(blocks < 8192 ? blocks : 8192), 256, 0, st>>>(
+        reinterpret_cast<float4*>(dst), reinterpret_cast<const float4*>(src), n4);
+    PS_LAUNCHED();
+  }
+  if (count % 4) {
+    ps::copy_tail_kernel<<<1, 4, 0, st>>>(dst, src, n4 * 4, count);
+    PS_LAUNCHED();
+  }
+  return PS_OK;
+}
+
 
 const char* ps_last_error(void) { return ps::g_last_error.c_str(); }
 
