@@ -88,6 +88,15 @@ int ps_fill_random_async(float* dst, size_t count, uint64_t seed, float lo, floa
  * scaling the FETCH_SIZE / WRITE_SIZE counters. No reference counterpart. */
 int ps_copy_f32_async(float* dst, const float* src, size_t count, ps_stream_t stream);
 
+/* Measurement probe for the operators' row gathers: gathers `n` rows of a
+ * rows x row_floats FP32 table (row_floats 32 or 128) at indices hash(seed, i)
+ * mod rows, uniformly random, with 128-bit loads and 16 rows in flight per
+ * lane, and writes a checksum to out[0]. Its throughput for a given table size
+ * is the gather ceiling the SpMM / SDDMM kernels work against. No reference
+ * counterpart. */
+int ps_probe_gather_async(const float* table, int rows, int row_floats, long long n,
+                          uint64_t seed, float* out, ps_stream_t stream);
+
 /* ------------------------------------------------------- streams, events */
 /* Replaces: cudaStreamCreate / cudaStreamDestroy (benchmark_utils.h:48-66). */
 int ps_stream_create(ps_stream_t* stream);

@@ -58,10 +58,64 @@ __global__ void copy_tail_kernel(float* __restrict__ dst, const float* __restric
   if (i < count) dst[i] = src[i];
 }
 
+template <int LPN>
+__global__ __launch_bounds__(256) void probe_gather_kernel(const float* table, uint32_t rows,
+                                                           uint64_t n, uint64_t seed,
+                                                           float* out) {
+  constexpr int SL = 64 / LPN;
+  const int lane = threadIdx.x & 63, slot = lane / LPN, sub = lane % LPN;
+  const uint64_t wave = (uint64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  const uint64_t waves = (uint64_t(gridDim.x) * blockDim.x) >> 6;
+  const Rows<true> t(table, uint64_t(rows) * LPN * 16);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (uint64_t base = wave * 16 * SL; base < n; base += waves * 16 * SL) {
+    float4 v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const uint64_t k = base + u * SL + slot;
+      // 32-bit mix (two xorshift-multiply rounds), range-reduced by a
+      // multiply-high, so index arithmetic stays off the critical path
+      uint32_t h = uint32_t(k) ^ uint32_t(seed);
+      h = (h ^ (h >> 16)) * 0x7feb352du;
+      h = (h ^ (h >> 15)) * 0x846ca68bu;
+      h ^= h >> 16;
+      const uint32_t r = k < n ? uint32_t((uint64_t(h) * rows) >> 32) : 0u;
+      v[u] = t.load(r * uint32_t(LPN * 16) + uint32_t(sub) * 16u);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      acc.x += v[u].x;
+      acc.y += v[u].y;
+      acc.z += v[u].z;
+      acc.w += v[u].w;
+    }
+  }
+  const float s = acc.x + acc.y + acc.z + acc.w;
+  if (s == -1.2345e-37f) out[0] = s;  // keeps the loads alive; never true for the fills used
+}
+
 }  // namespace
 }  // namespace ps
 
 extern "C" {
+
+int ps_probe_gather_async(const float* table, int rows, int row_floats, long long n,
+                          uint64_t seed, float* out, ps_stream_t stream) {
+  PS_CHECK_ARG(table && out && rows > 0 && n >= 0 && (row_floats == 32 || row_floats == 128),
+               "ps_probe_gather_async: bad argument");
+  PS_CHECK_ARG(uint64_t(rows) * uint64_t(row_floats) * 4u <= 0xFFFFFFFFull,
+               "ps_probe_gather_async: table must fit 4 GiB");
+  const unsigned grid = 256 * 16;
+  if (row_floats == 32)
+    ps::probe_gather_kernel<8><<<grid, 256, 0, ps::to_hip(stream)>>>(table, uint32_t(rows),
+                                                                      uint64_t(n), seed, out);
+  else
+    ps::probe_gather_kernel<32><<<grid, 256, 0, ps::to_hip(stream)>>>(table, uint32_t(rows),
+                                                                       uint64_t(n), seed, out);
+  PS_LAUNCHED();
+  return PS_OK;
+}
 
 int ps_copy_f32_async(float* dst, const float* src, size_t count, ps_stream_t stream) {
   if (count == 0) return PS_OK;

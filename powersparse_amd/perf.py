@@ -6,6 +6,11 @@
       1 GiB) and the bench operators of the configuration. Meant to run under
       `rocprofv3 --pmc FETCH_SIZE` and `rocprofv3 --pmc WRITE_SIZE`.
 
+  python -m powersparse_amd.perf ceiling
+      Streaming-copy bandwidth and the throughput of uniformly random row
+      gathers (128- and 512-byte rows) against table size: the hardware ceiling
+      of the operators' per-nonzero B / Y row gathers.
+
   python -m powersparse_amd.perf summarize --trace KT.db [--fetch F.db --write W.db]
         [--config C1] [--json OUT.json]
       Reads rocprofv3 SQLite result databases: per kernel the dispatch count and
@@ -37,16 +42,6 @@ def kernel_op(name):
     """(op, lanes-template) of an operator kernel name, else None."""
     m = re.search(r"(spmm|sddmm)_kernel<(\d+), (true|false)>", short_name(name))
     return (m.group(1), int(m.group(2))) if m else None
-
-
-def op_of(op, n):
-    """Operator kernel template argument for a width N (see pick_lpn / KQ)."""
-    if op == "spmm":
-        for lanes, width in ((64, 256), (32, 128), (16, 64)):
-            if n % width == 0:
-                return lanes
-        return 8
-    return n // 32
 
 
 def workload(args):
@@ -87,65 +82,110 @@ def workload(args):
     print(f"workload {args.config}: nnz={csr.nnz} done", flush=True)
 
 
+def ceiling(args):
+    """Streaming-copy bandwidth and random row-gather throughput vs table size."""
+    import powersparse_amd as ps
+    from powersparse_amd import _native
+
+    ps.set_device(0)
+    st = ps.Stream()
+    t0, t1 = ps.Event(), ps.Event()
+
+    def timed(fn, reps=4):
+        fn()
+        best = None
+        for _ in range(reps):
+            t0.record(st)
+            fn()
+            t1.record(st)
+            t1.synchronize()
+            ms = t0.elapsed_ms(t1)
+            best = ms if best is None else min(best, ms)
+        return best
+
+    big = 2048 << 20
+    table = ps.DeviceBuffer(big)
+    ps.fill_random(table, big // 4, 3, 0.0, 1.0, stream=st)
+    dst = ps.DeviceBuffer(1 << 30)
+    out = ps.DeviceBuffer(4)
+    ms = timed(lambda: ps.copy_f32(dst, table, (1 << 30) // 4, st))
+    lines = ["| probe | working set | time (ms) | GB/s |", "|---|---|---|---|",
+             f"| streaming copy (read + write) | 1 GiB | {ms:.3f} | {2 * (1 << 30) / ms / 1e6:.0f} |"]
+    n = 1 << 24
+    for row_floats in (32, 128):
+        for mb in (8, 32, 128, 256, 512, 2048):
+            rows = (mb << 20) // (4 * row_floats)
+            ms = timed(lambda: ps._hip_call(_native.hip().ps_probe_gather_async(
+                table.ptr, rows, row_floats, n, 9, out.ptr, st.ptr)))
+            lines.append(f"| random {4 * row_floats}-byte row gathers | {mb} MB table | "
+                         f"{ms:.3f} | {n * 4 * row_floats / ms / 1e6:.0f} |")
+    print("\n".join(lines))
+
+
 def read_counters(db, counter):
+    """[(kernel, grid, value)] of every dispatch, in dispatch order."""
     con = sqlite3.connect(db)
-    rows = con.execute("select kernel_name, value, grid_size from counters_collection "
-                       "where counter_name = ?", (counter,)).fetchall()
-    out = collections.defaultdict(list)
-    for name, value, grid in rows:
-        out[short_name(name)].append((float(value), int(grid)))
-    return out
+    rows = con.execute("select kernel_name, grid_size, value from counters_collection "
+                       "where counter_name = ? order by dispatch_id", (counter,)).fetchall()
+    return [(short_name(k), int(g), float(v)) for k, g, v in rows]
 
 
 def read_trace(db):
+    """Per (kernel, grid): dispatches and mean duration in us, busiest first."""
     con = sqlite3.connect(db)
-    rows = con.execute("select name, total_calls, average from top_kernels").fetchall()
-    return [(short_name(n), int(c), float(a)) for n, c, a in rows]  # average in us
+    rows = con.execute("select name, grid_x * grid_y * grid_z, count(*), avg(duration) "
+                       "from kernels group by name, grid_x * grid_y * grid_z").fetchall()
+    out = [(short_name(n), int(g), int(c), float(d) / 1e3) for n, g, c, d in rows]
+    return sorted(out, key=lambda r: -r[2] * r[3])
 
 
-def calibration(counts):
-    """Scale factor bytes / (KiB * 1024) from the calibration copy dispatches:
-    the copy kernel dispatch whose grid matches a 1 GiB copy."""
-    vals = [v for v, g in counts.get("ps::copy_f32_kernel", [])]
-    if not vals:
-        return None
-    return CALIB_BYTES / (max(vals) * 1024.0)
+def operator_runs(dispatches):
+    """Groups operator-kernel dispatches into runs of equal (kernel, grid), in
+    order: one run per operator of the workload."""
+    runs = []
+    for k, g, v in dispatches:
+        if kernel_op(k) is None:
+            continue
+        if runs and runs[-1][0] == (k, g):
+            runs[-1][1].append(v)
+        else:
+            runs.append(((k, g), [v]))
+    return runs
+
+
+def calibration(dispatches):
+    """bytes / (KiB * 1024) that makes the 1 GiB calibration copy exact."""
+    vals = [v for k, _, v in dispatches if k == "ps::copy_f32_kernel"]
+    return CALIB_BYTES / (max(vals) * 1024.0) if vals else None
 
 
 def summarize(args):
-    lines = []
+    lines = ["| kernel | grid (work-items) | dispatches | mean duration (us) |",
+             "|---|---|---|---|"]
     trace = read_trace(args.trace)
-    lines.append("| kernel | dispatches | mean duration (us) |")
-    lines.append("|---|---|---|")
-    for name, calls, avg in trace[:25]:
-        lines.append(f"| `{name}` | {calls} | {avg:.1f} |")
-    result = {"config": args.config, "kernels": {}}
-    for name, calls, avg in trace:
-        result["kernels"][name] = {"dispatches": calls, "mean_us": avg}
+    result = {"config": args.config, "kernels": []}
+    for name, grid, calls, avg in trace:
+        result["kernels"].append({"kernel": name, "grid": grid, "dispatches": calls,
+                                  "mean_us": avg})
+    for name, grid, calls, avg in trace[:25]:
+        lines.append(f"| `{name}` | {grid} | {calls} | {avg:.1f} |")
     if args.fetch and args.write:
         fetch = read_counters(args.fetch, "FETCH_SIZE")
         write = read_counters(args.write, "WRITE_SIZE")
         kf, kw = calibration(fetch), calibration(write)
-        lines.append("")
-        lines.append(f"Calibration (1 GiB ps::copy_f32_kernel): FETCH x{kf:.4f}, WRITE x{kw:.4f}")
-        lines.append("")
-        lines.append("| operator | kernel | FETCH (MB) | WRITE (MB) | HBM traffic per launch (MB) |")
-        lines.append("|---|---|---|---|---|")
+        lines += ["", f"Calibration (1 GiB ps::copy_f32_kernel): FETCH x{kf:.4f}, "
+                      f"WRITE x{kw:.4f}", "",
+                  "| operator | kernel | grid | FETCH (MB) | WRITE (MB) | traffic per launch (MB) |",
+                  "|---|---|---|---|---|---|"]
         result["calibration"] = {"fetch": kf, "write": kw}
         result["traffic"] = {}
-        # operator dispatches appear in launch order: 1 + steps per operator
-        for op, n in CONFIG_OPS[args.config]:
-            tmpl = op_of(op, n)
-            names = [k for k in fetch if kernel_op(k) == (op, tmpl)]
-            if not names:
-                continue
-            f = [v for k in names for v, _ in fetch[k]]
-            w = [v for k in names for v, _ in write.get(k, [])]
-            fb = sum(f) / len(f) * 1024.0 * kf
-            wb = sum(w) / len(w) * 1024.0 * kw if w else 0.0
-            result["traffic"][f"{op}_N{n}"] = {"kernel": names[0], "fetch_bytes": fb,
+        fr, wr = operator_runs(fetch), operator_runs(write)
+        for (op, n), ((k, g), fv), (_, wv) in zip(CONFIG_OPS[args.config], fr, wr):
+            fb = sum(fv) / len(fv) * 1024.0 * kf
+            wb = sum(wv) / len(wv) * 1024.0 * kw
+            result["traffic"][f"{op}_N{n}"] = {"kernel": k, "grid": g, "fetch_bytes": fb,
                                                 "write_bytes": wb, "traffic_bytes": fb + wb}
-            lines.append(f"| {op} N={n} | `{names[0]}` | {fb / 1e6:.1f} | {wb / 1e6:.1f} | "
+            lines.append(f"| {op} N={n} | `{k}` | {g} | {fb / 1e6:.1f} | {wb / 1e6:.1f} | "
                          f"{(fb + wb) / 1e6:.1f} |")
     print("\n".join(lines))
     if args.json:
@@ -159,6 +199,7 @@ def main(argv=None):
     w = sub.add_parser("workload")
     w.add_argument("--config", default="C1", choices=sorted(CONFIG_OPS))
     w.add_argument("--steps", type=int, default=3)
+    sub.add_parser("ceiling")
     s = sub.add_parser("summarize")
     s.add_argument("--trace", required=True)
     s.add_argument("--fetch")
@@ -168,6 +209,8 @@ def main(argv=None):
     args = ap.parse_args(argv)
     if args.cmd == "workload":
         workload(args)
+    elif args.cmd == "ceiling":
+        ceiling(args)
     else:
         summarize(args)
     return 0
