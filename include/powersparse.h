@@ -39,6 +39,24 @@ const char* psx_last_error(void);
 int psx_matrix_create(int rows, int cols, int nnz, const int* row_ptr, const int* col_ind,
                       const float* sp_data, int cu_count, double* timings_ms,
                       psx_matrix** out);
+
+/* Build options of psx_matrix_create_ex. signature_order picks how groups are
+ * put in signature order (both give the reference's order,
+ * matrix_utils.cu:588-593): PSX_ORDER_AUTO, PSX_ORDER_BITMAP_WORDS (per-word
+ * sorts of the groups x L/32 signature bitmaps) or PSX_ORDER_BIT_LISTS (sorted
+ * bit lists, memory bounded by nnz). */
+enum { PSX_ORDER_AUTO = 0, PSX_ORDER_BITMAP_WORDS = 1, PSX_ORDER_BIT_LISTS = 2 };
+typedef struct psx_build_options {
+  int cu_count;
+  int signature_order;
+} psx_build_options;
+/* psx_matrix_create with options (NULL: all defaults). No reference counterpart. */
+int psx_matrix_create_ex(int rows, int cols, int nnz, const int* row_ptr, const int* col_ind,
+                         const float* sp_data, const psx_build_options* options,
+                         double* timings_ms, psx_matrix** out);
+/* The signature order method the build used (PSX_ORDER_BITMAP_WORDS or
+ * PSX_ORDER_BIT_LISTS). No reference counterpart. */
+int psx_matrix_signature_order(const psx_matrix* m, int* method);
 /* Replaces: ~PowerSparseMatrixGPU (matrix_utils.h:24). */
 int psx_matrix_destroy(psx_matrix* m);
 /* Replaces: MatrixRow/MatrixCol/MatrixNNZ/GroupTypeNum/GroupFineSize (matrix_utils.h:30-34);

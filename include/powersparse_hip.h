@@ -170,7 +170,9 @@ size_t ps_scan_workspace_bytes(size_t n);
 int ps_exclusive_scan_u32(const uint32_t* in, uint32_t* out, size_t n, void* workspace,
                           ps_stream_t stream);
 
-/* Stable LSD radix sort of (key, value) pairs by key bits [begin_bit, end_bit).
+/* Stable LSD radix sort of (key, value) pairs by key bits [begin_bit, end_bit);
+ * vals and vals_alt both NULL sorts the keys alone. Bits above end_bit inside
+ * the last 8-bit digit take part in that digit: keep them equal in all keys.
  * Keys and values ping-pong between the two buffer pairs; *result_in_alt is set
  * to 1 when the sorted data ended in the *_alt buffers. workspace:
  * ps_radix_workspace_bytes(n) bytes.
@@ -240,6 +242,32 @@ int ps_pre_signature_keys(const uint32_t* sig_word, const uint32_t* perm, int n,
  * to skip digits that cannot reorder the groups. */
 int ps_pre_signature_span(const uint32_t* sig, int groups, int words, uint32_t* or_host,
                           uint32_t* and_host, ps_stream_t stream);
+
+/* Sparse form of the signatures, for long signatures where the bitmaps of
+ * ps_pre_signatures would not fit: the ascending list of distinct signature
+ * bits of every group. Groups are numbered globally, workset after workset
+ * (global id = group_num[0] + ... + group_num[s-1] + g); group q's list is
+ * lists[list_begin[q] .. list_begin[q+1]). lists holds up to nnz entries,
+ * list_begin sum(group_num) + 1. Every group must have a member. Synchronises
+ * the stream. Same inputs as ps_pre_signatures.
+ * Replaces: GetResidueSignature / GetBlockSignature (matrix_utils.cu:261-327). */
+int ps_pre_signature_lists(const int* row_ptr, int rows, int group_type_num, int fine,
+                           const uint64_t* ranked_keys, int count_bits,
+                           const uint32_t* ranked_vals, int nnz, const int* col_ind,
+                           const int* sigbit, int signature_len, const uint32_t* prefix,
+                           const int* group_num, uint32_t* lists, uint32_t* list_begin,
+                           ps_stream_t stream);
+
+/* perm[s][k] = the group of workset s at position k of the stable descending
+ * signature order, from the lists of ps_pre_signature_lists: the same order as
+ * the per-word stable sorts, found by refining ties a few list elements at a
+ * time (cost follows the tied prefixes, not the signature length). Synchronises
+ * the stream.
+ * Replaces: the stable_sort loop over signature words (matrix_utils.cu:588-593)
+ * with CompareDescending (:394-401). */
+int ps_pre_signature_order(const uint32_t* lists, const uint32_t* list_begin,
+                           int group_type_num, const int* group_num, int signature_len,
+                           uint32_t* const* perm, ps_stream_t stream);
 
 /* Final metadata in sorted order: des[k] = src_des[perm[k]]; for the residue
  * workset also len[k] = src_len[perm[k]] and atomic[k] = src_atomic[perm[k]].

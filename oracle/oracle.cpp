@@ -80,6 +80,36 @@ int SigBits(int cols, const int* col_nnz, int ffc, int* sigbit) {
   return len;
 }
 
+// Stable order of groups by signature, descending, read as one bit string with
+// bit b at word b / 32, position 31 - b % 32 (matrix_utils.cu:286-290): bit 0 is
+// the most significant. A larger string has a 1 where the other first differs,
+// so the order is that of each group's ascending list of distinct bits,
+// compared lexicographically ascending, a list's end ranking after every bit;
+// equal lists keep group order (the stable sorts of :590-592 start from iota).
+// `bits[g]` may hold duplicates, in any order; it is sorted in place.
+std::vector<int> OrderByBitLists(std::vector<std::vector<int>>& bits) {
+  for (auto& b : bits) {
+    std::sort(b.begin(), b.end());
+    b.erase(std::unique(b.begin(), b.end()), b.end());
+  }
+  std::vector<int> perm(bits.size());
+  std::iota(perm.begin(), perm.end(), 0);
+  std::stable_sort(perm.begin(), perm.end(), [&bits](int x, int y) {
+    const std::vector<int>& a = bits[size_t(x)];
+    const std::vector<int>& b = bits[size_t(y)];
+    const size_t n = std::min(a.size(), b.size());
+    for (size_t i = 0; i < n; ++i)
+      if (a[i] != b[i]) return a[i] < b[i];
+    return a.size() > b.size();  // the shorter list ends first: it ranks after
+  });
+  return perm;
+}
+
+// 0: bitmaps while groups x words stays below kBitmapLimit words, else lists;
+// 1: always the per-word sorts of the bitmaps; 2: always the bit lists.
+int g_order_mode = 0;
+constexpr size_t kBitmapLimit = size_t(1) << 28;
+
 }  // namespace
 
 struct or_worksets {
@@ -101,6 +131,15 @@ int or_analyze_group_type_num(int rows, const int* row_ptr, int cu_count) {
 
 int or_generate_sigbit(int cols, const int* col_nnz, int ffc, int* sigbit) {
   return SigBits(cols, col_nnz, ffc, sigbit);
+}
+
+void or_set_signature_order(int mode) { g_order_mode = mode; }
+
+void or_order_bit_lists(int groups, const int* begin, const int* bits, int* perm) {
+  std::vector<std::vector<int>> b(static_cast<size_t>(groups));
+  for (int g = 0; g < groups; ++g) b[size_t(g)].assign(bits + begin[g], bits + begin[g + 1]);
+  const std::vector<int> p = OrderByBitLists(b);
+  std::copy(p.begin(), p.end(), perm);
 }
 
 or_worksets* or_preprocess(int rows, int cols, int nnz, const int* rp, const int* ci,
@@ -230,6 +269,16 @@ or_worksets* or_preprocess(int rows, int cols, int nnz, const int* rp, const int
     w->perm[s].resize(G);
     std::iota(w->perm[s].begin(), w->perm[s].end(), 0);
     if (G == 0) continue;
+    const bool lists = g_order_mode == 2 ||
+                       (g_order_mode == 0 && size_t(G) * size_t(words) > kBitmapLimit);
+    if (lists) {  // same order without the bitmaps (see OrderByBitLists)
+      std::vector<std::vector<int>> bits(static_cast<size_t>(G));
+      for (int g = 0; g < G; ++g)
+        for (int q = 0; q < member_len[s][g]; ++q)
+          bits[size_t(g)].push_back(w->sigbit[ci[w->ranked[member_first[s][g] + q]]]);
+      w->perm[s] = OrderByBitLists(bits);
+      continue;
+    }
     std::vector<uint32_t>& sig = w->signature[s];
     sig.assign(size_t(G) * words, 0u);
     for (int g = 0; g < G; ++g)
@@ -315,6 +364,9 @@ void or_copy_initial_residue(const or_worksets* w, int* offset, uint8_t* atomic)
 }
 void or_copy_signature(const or_worksets* w, int s, uint32_t* out) {
   std::copy(w->signature[s].begin(), w->signature[s].end(), out);
+}
+int or_has_signature(const or_worksets* w, int s) {
+  return w->group_num[s] > 0 && !w->signature[s].empty();
 }
 void or_copy_group_perm(const or_worksets* w, int s, int* out) {
   std::copy(w->perm[s].begin(), w->perm[s].end(), out);

@@ -53,8 +53,11 @@ void or_copy_ranked_pos(const or_worksets* w, int* pos);         /* nnz: CSR pos
 void or_copy_sigbit(const or_worksets* w, int* sigbit);          /* cols */
 void or_copy_initial_des(const or_worksets* w, int s, int* des); /* group_num[s], row order */
 void or_copy_initial_residue(const or_worksets* w, int* offset, uint8_t* atomic);
-/* signature words of workset s, word-major: sig[word * G + g], L/32 words */
+/* signature words of workset s, word-major: sig[word * G + g], L/32 words
+ * (left untouched when the workset was ordered by bit lists) */
 void or_copy_signature(const or_worksets* w, int s, uint32_t* sig);
+/* 1 if workset s kept its signature bitmaps (ordered by the per-word sorts) */
+int or_has_signature(const or_worksets* w, int s);
 /* group permutation of workset s: sorted position -> initial group id */
 void or_copy_group_perm(const or_worksets* w, int s, int* perm);
 
@@ -63,6 +66,17 @@ int or_analyze_group_type_num(int rows, const int* row_ptr, int cu_count);
 
 /* GenerateSigBit, FFC mode with ffc (matrix_utils.cu:65-128). Returns L. */
 int or_generate_sigbit(int cols, const int* col_nnz, int ffc, int* sigbit);
+
+/* How or_preprocess orders groups by signature (the order of the per-word
+ * stable sorts, matrix_utils.cu:588-593, either way): 0 = bitmaps unless
+ * groups x L/32 exceeds 2^28 words, then bit lists; 1 = always the per-word
+ * sorts of the bitmaps; 2 = always the bit lists. Process-wide. */
+void or_set_signature_order(int mode);
+
+/* The stable descending-signature order of `groups` groups given as sets of
+ * signature bits: group g's bits are bits[begin[g] .. begin[g+1]) (any order,
+ * duplicates allowed). perm[k] = group at position k. */
+void or_order_bit_lists(int groups, const int* begin, const int* bits, int* perm);
 
 /* CheckSpmm (benchmark.cu:64-77): C[r,j] = sum_p double(val[p]) * B[col[p],j]
  * in double. mag (optional) receives sum_p |val[p]| * |B[col[p],j]|. */

@@ -41,6 +41,10 @@ def lib():
         L.or_copy_initial_residue.argtypes = [vp, vp, vp]
         L.or_copy_signature.argtypes = [vp, ip, vp]
         L.or_copy_group_perm.argtypes = [vp, ip, vp]
+        L.or_has_signature.restype = ip
+        L.or_has_signature.argtypes = [vp, ip]
+        L.or_set_signature_order.argtypes = [ip]
+        L.or_order_bit_lists.argtypes = [ip, vp, vp, vp]
         L.or_analyze_group_type_num.restype = ip
         L.or_analyze_group_type_num.argtypes = [ip, vp, ip]
         L.or_generate_sigbit.restype = ip
@@ -97,10 +101,12 @@ class Worksets:
             d = np.empty(self.group_num[s], np.int32)
             L.or_copy_initial_des(h, s, d.ctypes.data)
             self.initial_des.append(d)
-            sg = np.zeros(self.group_num[s] * words, np.uint32)
-            if self.group_num[s]:
+            if L.or_has_signature(h, s):  # None when ordered by bit lists
+                sg = np.zeros(self.group_num[s] * words, np.uint32)
                 L.or_copy_signature(h, s, sg.ctypes.data)
-            self.signature.append(sg.reshape(words, self.group_num[s]))
+                self.signature.append(sg.reshape(words, self.group_num[s]))
+            else:
+                self.signature.append(None)
             p = np.empty(self.group_num[s], np.int32)
             L.or_copy_group_perm(h, s, p.ctypes.data)
             self.perm.append(p)
@@ -117,20 +123,47 @@ class Worksets:
         return np.arange(self.group_num[s] + 1, dtype=np.int64) * gs
 
 
-def preprocess(rows, cols, row_ptr, col_ind, values, cu_count):
-    """Runs the CPU restatement; raises ValueError with the reference message."""
+ORDER_MODES = {"auto": 0, "bitmap_words": 1, "bit_lists": 2}
+
+
+def preprocess(rows, cols, row_ptr, col_ind, values, cu_count, signature_order="auto"):
+    """Runs the CPU restatement; raises ValueError with the reference message.
+
+    signature_order: how groups are put in signature order (the same order
+    either way): "auto", "bitmap_words" (per-word stable sorts of the bitmaps,
+    as the reference) or "bit_lists" (comparison of sorted bit lists)."""
     row_ptr, col_ind, values = _i32(row_ptr), _i32(col_ind), _f32(values)
     err = ctypes.create_string_buffer(256)
     nnz = int(col_ind.size)
-    h = lib().or_preprocess(rows, cols, nnz, row_ptr.ctypes.data if row_ptr.size else None,
-                            col_ind.ctypes.data if col_ind.size else None,
-                            values.ctypes.data if values.size else None, cu_count, err, 256)
+    lib().or_set_signature_order(ORDER_MODES[signature_order])
+    try:
+        h = lib().or_preprocess(rows, cols, nnz, row_ptr.ctypes.data if row_ptr.size else None,
+                                col_ind.ctypes.data if col_ind.size else None,
+                                values.ctypes.data if values.size else None, cu_count, err, 256)
+    finally:
+        lib().or_set_signature_order(0)
     if not h:
         raise ValueError(err.value.decode())
     try:
         return Worksets(h, rows, cols, nnz)
     finally:
         lib().or_free(h)
+
+
+def order_bit_lists(bit_sets):
+    """Stable descending-signature order of groups given as iterables of
+    signature bits: perm[k] = group at position k."""
+    begin = np.zeros(len(bit_sets) + 1, np.int32)
+    flat = []
+    for g, bits in enumerate(bit_sets):
+        flat.extend(int(b) for b in bits)
+        begin[g + 1] = len(flat)
+    flat = np.asarray(flat if flat else [0], np.int32)
+    perm = np.empty(len(bit_sets), np.int32)
+    if len(bit_sets):
+        lib().or_order_bit_lists(len(bit_sets), begin.ctypes.data, flat.ctypes.data,
+                                 perm.ctypes.data)
+    return perm
 
 
 def analyze_group_type_num(row_ptr, cu_count):

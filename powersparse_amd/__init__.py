@@ -334,27 +334,37 @@ class PowerSparseMatrixGPU:
     """Owns the GPU worksets built from host CSR arrays (utils/matrix_utils.h:20-69).
 
     cu_count=0 partitions for the current device; a positive value reproduces
-    the partition for a device with that many CUs/SMs. With timings=True the
+    the partition for a device with that many CUs/SMs. signature_order picks
+    how groups are put in signature order ("auto", "bitmap_words" or
+    "bit_lists"; both methods give the same order). With timings=True the
     stage times (ms) are kept in `.timings`.
     """
 
     TIMING_KEYS = ("upload", "analyze", "rank", "groups", "sigbit", "signature", "order",
                    "gather", "total")
+    ORDER_METHODS = ("auto", "bitmap_words", "bit_lists")
 
     def __init__(self, row_num, col_num, nnz_num, row_ptr, col_ind, sp_data, cu_count=0,
-                 timings=False):
+                 timings=False, signature_order="auto"):
         row_ptr = np.ascontiguousarray(row_ptr, dtype=np.int32)
         col_ind = np.ascontiguousarray(col_ind, dtype=np.int32)
         sp_data = np.ascontiguousarray(sp_data, dtype=np.float32)
         self._h = None
         t = (ctypes.c_double * 9)() if timings else None
         h = ctypes.c_void_p()
-        _host_call(_native.host().psx_matrix_create(
+        if signature_order not in self.ORDER_METHODS:
+            raise ValueError(f"signature_order must be one of {self.ORDER_METHODS}")
+        opts = _native.BuildOptions(int(cu_count), self.ORDER_METHODS.index(signature_order))
+        _host_call(_native.host().psx_matrix_create_ex(
             int(row_num), int(col_num), int(nnz_num),
             row_ptr.ctypes.data if row_ptr.size else None,
             col_ind.ctypes.data if col_ind.size else None,
-            sp_data.ctypes.data if sp_data.size else None, int(cu_count), t, ctypes.byref(h)))
+            sp_data.ctypes.data if sp_data.size else None, ctypes.byref(opts), t,
+            ctypes.byref(h)))
         self._h = h.value
+        method = ctypes.c_int()
+        _host_call(_native.host().psx_matrix_signature_order(self._h, ctypes.byref(method)))
+        self.signature_order = self.ORDER_METHODS[method.value]
         self.timings = dict(zip(self.TIMING_KEYS, list(t))) if timings else None
         rows, cols, nnz, S, fine, L, cu = (ctypes.c_int() for _ in range(7))
         _host_call(_native.host().psx_matrix_info(
@@ -367,9 +377,9 @@ class PowerSparseMatrixGPU:
         self._group_num = list(g)
 
     @classmethod
-    def from_csr(cls, csr, cu_count=0, timings=False):
+    def from_csr(cls, csr, cu_count=0, timings=False, signature_order="auto"):
         return cls(csr.rows, csr.cols, csr.nnz, csr.row_ptr, csr.col_ind, csr.values,
-                   cu_count=cu_count, timings=timings)
+                   cu_count=cu_count, timings=timings, signature_order=signature_order)
 
     def close(self):
         if self._h:

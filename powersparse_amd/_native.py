@@ -27,6 +27,11 @@ c_u64_p = ctypes.POINTER(ctypes.c_uint64)
 c_void_p = ctypes.c_void_p
 
 
+class BuildOptions(ctypes.Structure):
+    """psx_build_options (include/powersparse.h)."""
+    _fields_ = [("cu_count", ctypes.c_int), ("signature_order", ctypes.c_int)]
+
+
 class DeviceProps(ctypes.Structure):
     _fields_ = [
         ("name", ctypes.c_char * 256),
@@ -128,6 +133,13 @@ HIP_API = [
      [c_void_p, c_void_p, ctypes.c_int, c_void_p, c_void_p]),
     ("ps_pre_signature_span", ctypes.c_int,
      [c_void_p, ctypes.c_int, ctypes.c_int, c_u32_p, c_u32_p, c_void_p]),
+    ("ps_pre_signature_lists", ctypes.c_int,
+     [c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int, c_void_p,
+      ctypes.c_int, c_void_p, c_void_p, ctypes.c_int, c_void_p, c_int_p, c_void_p, c_void_p,
+      c_void_p]),
+    ("ps_pre_signature_order", ctypes.c_int,
+     [c_void_p, c_void_p, ctypes.c_int, c_int_p, ctypes.c_int, ctypes.POINTER(c_void_p),
+      c_void_p]),
     ("ps_pre_permute_meta", ctypes.c_int,
      [c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
       c_void_p]),
@@ -141,6 +153,10 @@ HOST_API = [
     ("psx_matrix_create", ctypes.c_int,
      [ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, c_void_p, ctypes.c_int,
       c_double_p, ctypes.POINTER(c_void_p)]),
+    ("psx_matrix_create_ex", ctypes.c_int,
+     [ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, c_void_p,
+      ctypes.POINTER(BuildOptions), c_double_p, ctypes.POINTER(c_void_p)]),
+    ("psx_matrix_signature_order", ctypes.c_int, [c_void_p, c_int_p]),
     ("psx_matrix_destroy", ctypes.c_int, [c_void_p]),
     ("psx_matrix_info", ctypes.c_int,
      [c_void_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p]),

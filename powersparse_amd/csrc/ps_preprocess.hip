@@ -136,6 +136,34 @@ __global__ void group_meta_kernel(const int* __restrict__ row_ptr, int rows, int
   }
 }
 
+// Workset s and group g of the nonzero at ranked position i of row r: block
+// groups of the largest size first, the residue takes the tail (fine mode:
+// chunks of `fine`).
+__device__ __forceinline__ void locate_group(const int* __restrict__ row_ptr, int r, int i, int S,
+                                             int fine, const uint32_t* __restrict__ prefix,
+                                             size_t stride, int& s, int& g) {
+  const int base = row_ptr[r];
+  const int j = i - base;  // rank of this nonzero inside its row
+  s = 0;
+  if (S == 1) {
+    g = int(prefix[r]) + j / fine;
+    return;
+  }
+  int rem = row_ptr[r + 1] - base, off = 0;
+  for (int t = S - 1; t > 0; --t) {
+    const int gs = group_size(t);
+    const int n = rem / gs;
+    if (j < off + n * gs) {
+      s = t;
+      g = int(prefix[t * stride + r]) + (j - off) / gs;
+      return;
+    }
+    off += n * gs;
+    rem -= n * gs;
+  }
+  g = int(prefix[r]);
+}
+
 __global__ void signatures_kernel(const int* __restrict__ row_ptr, int rows, int S, int fine,
                                   const uint64_t* __restrict__ ranked_keys, int count_bits,
                                   const uint32_t* __restrict__ ranked_vals, int nnz,
@@ -143,30 +171,197 @@ __global__ void signatures_kernel(const int* __restrict__ row_ptr, int rows, int
                                   const uint32_t* __restrict__ prefix, SigTable sig) {
   const size_t stride = size_t(rows) + 1;
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nnz; i += gridDim.x * blockDim.x) {
-    const int r = int(ranked_keys[i] >> count_bits);
-    const int base = row_ptr[r];
-    const int j = i - base;  // rank of this nonzero inside its row
-    int s = 0, g;
-    if (S == 1) {
-      g = int(prefix[r]) + j / fine;
-    } else {
-      int rem = row_ptr[r + 1] - base, off = 0;
-      g = -1;
-      for (int t = S - 1; t > 0; --t) {
-        const int gs = group_size(t);
-        const int n = rem / gs;
-        if (j < off + n * gs) {
-          s = t;
-          g = int(prefix[t * stride + r]) + (j - off) / gs;
-          break;
-        }
-        off += n * gs;
-        rem -= n * gs;
-      }
-      if (g < 0) g = int(prefix[r]);
-    }
+    int s, g;
+    locate_group(row_ptr, int(ranked_keys[i] >> count_bits), i, S, fine, prefix, stride, s, g);
     const int bit = sigbit[col_ind[ranked_vals[i]]];
     atomicOr(&sig.p[s][size_t(bit >> 5) * sig.groups[s] + g], 1u << (31 - (bit & 31)));
+  }
+}
+
+// ---- signature order from sorted bit lists (long signatures) ----
+//
+// The stable per-word sort orders groups by their signature read as one
+// big-endian bit string (bit b of the string is bit 31 - b % 32 of word b / 32),
+// descending, ties in group order. Equivalently: by the ascending list of the
+// group's distinct signature bits, compared lexicographically ascending with
+// the end of a list ranking after every bit, ties in group order. The lists
+// cost at most one entry per nonzero, whatever the signature length.
+
+// First group id of each workset in one global numbering; base[S] = total.
+struct GroupBase {
+  uint32_t base[PS_MAX_WORKSETS + 1];
+  int S;
+};
+
+__device__ __forceinline__ int workset_of(const GroupBase& gb, uint32_t global) {
+  int s = 0;
+  while (global >= gb.base[s + 1]) ++s;
+  return s;
+}
+
+// entry[i] = (global group of ranked position i) << bit_bits | signature bit.
+__global__ void signature_entries_kernel(const int* __restrict__ row_ptr, int rows, int S,
+                                         int fine, const uint64_t* __restrict__ ranked_keys,
+                                         int count_bits, const uint32_t* __restrict__ ranked_vals,
+                                         int nnz, const int* __restrict__ col_ind,
+                                         const int* __restrict__ sigbit,
+                                         const uint32_t* __restrict__ prefix, GroupBase gb,
+                                         int bit_bits, uint64_t* __restrict__ entries) {
+  const size_t stride = size_t(rows) + 1;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nnz; i += gridDim.x * blockDim.x) {
+    int s, g;
+    locate_group(row_ptr, int(ranked_keys[i] >> count_bits), i, S, fine, prefix, stride, s, g);
+    const uint32_t bit = uint32_t(sigbit[col_ind[ranked_vals[i]]]);
+    entries[i] = (uint64_t(gb.base[s] + uint32_t(g)) << bit_bits) | bit;
+  }
+}
+
+// flag[i] = 1 where sorted entry i differs from entry i - 1 (first of its value).
+__global__ void entry_flags_kernel(const uint64_t* __restrict__ e, uint32_t n,
+                                   uint32_t* __restrict__ flag) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    flag[i] = (i == 0 || e[i] != e[i - 1]) ? 1u : 0u;
+}
+
+// Distinct entries compacted into lists; list_begin[g] = first list slot of
+// group g, list_begin[total] = number of distinct entries.
+__global__ void entry_lists_kernel(const uint64_t* __restrict__ e, uint32_t n, int bit_bits,
+                                   const uint32_t* __restrict__ flag,
+                                   const uint32_t* __restrict__ pos, uint32_t total,
+                                   uint32_t* __restrict__ lists,
+                                   uint32_t* __restrict__ list_begin) {
+  const uint64_t mask = (uint64_t(1) << bit_bits) - 1;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    if (flag[i]) {
+      lists[pos[i]] = uint32_t(e[i] & mask);
+      const uint64_t g = e[i] >> bit_bits;
+      if (i == 0 || (e[i - 1] >> bit_bits) != g) list_begin[g] = pos[i];
+    }
+    if (i == n - 1) list_begin[total] = pos[i] + flag[i];
+  }
+}
+
+// Refinement state: the active groups (still tied with another group) in
+// class order, each with its class base = final position of the class's first
+// member. Initially every group is active and the classes are the worksets.
+__global__ void order_init_kernel(uint32_t n, GroupBase gb, uint32_t* __restrict__ act_group,
+                                  uint32_t* __restrict__ act_base) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    act_group[i] = i;
+    act_base[i] = gb.base[workset_of(gb, i)];
+  }
+}
+
+// key = class base, then list elements depth .. depth + per_key - 1 of the
+// group (`end` past the list's end), each in elem_bits bits.
+__global__ void order_keys_kernel(const uint32_t* __restrict__ act_group,
+                                  const uint32_t* __restrict__ act_base, uint32_t n,
+                                  const uint32_t* __restrict__ lists,
+                                  const uint32_t* __restrict__ list_begin, uint32_t depth,
+                                  int per_key, int elem_bits, uint32_t end,
+                                  uint64_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const uint32_t g = act_group[i];
+    const uint32_t b = list_begin[g];
+    const uint32_t len = list_begin[g + 1] - b;
+    uint64_t key = act_base[i];
+    for (int j = 0; j < per_key; ++j) {
+      const uint32_t d = depth + uint32_t(j);
+      key = (key << elem_bits) | (d < len ? lists[b + d] : end);
+    }
+    keys[i] = key;
+    vals[i] = g;
+  }
+}
+
+// or_and[0] |= OR of the keys, or_and[1] &= AND of the keys.
+__global__ void key_span_kernel(const uint64_t* __restrict__ keys, uint32_t n,
+                                unsigned long long* __restrict__ or_and) {
+  unsigned long long o = 0ull, a = ~0ull;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    o |= keys[i];
+    a &= keys[i];
+  }
+  for (int d = 1; d < kWave; d <<= 1) {
+    o |= __shfl_xor(o, d, kWave);
+    a &= __shfl_xor(a, d, kWave);
+  }
+  if (lane_id() == 0) {
+    atomicOr(&or_and[0], o);
+    atomicAnd(&or_and[1], a);
+  }
+}
+
+// Over the sorted keys: new_head[i] = 1 where key i starts a run of equal keys,
+// old_head[i] = 1 where its class base (key >> elem_shift) starts a run.
+__global__ void order_flags_kernel(const uint64_t* __restrict__ keys, uint32_t n, int elem_shift,
+                                   uint32_t* __restrict__ new_head,
+                                   uint32_t* __restrict__ old_head) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const bool first = i == 0;
+    new_head[i] = (first || keys[i] != keys[i - 1]) ? 1u : 0u;
+    old_head[i] = (first || (keys[i] >> elem_shift) != (keys[i - 1] >> elem_shift)) ? 1u : 0u;
+  }
+}
+
+// new_at[c] / old_at[c] = sorted index where run c begins (runs numbered by the
+// exclusive scans of the head flags).
+__global__ void order_heads_kernel(uint32_t n, const uint32_t* __restrict__ new_head,
+                                   const uint32_t* __restrict__ new_rank,
+                                   const uint32_t* __restrict__ old_head,
+                                   const uint32_t* __restrict__ old_rank,
+                                   uint32_t* __restrict__ new_at, uint32_t* __restrict__ old_at) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    if (new_head[i]) new_at[new_rank[i]] = i;
+    if (old_head[i]) old_at[old_rank[i]] = i;
+  }
+}
+
+// A run of equal keys inside a class is the new class; its base = the old base
+// + the run's offset inside the class. A group is placed when its new class
+// has one member, or when the key's last element is past the list's end (the
+// members' lists are then identical and group order decides). keep[i] = 1 for
+// groups that stay tied; next_base[i] = their new class base.
+__global__ void order_resolve_kernel(const uint64_t* __restrict__ keys,
+                                     const uint32_t* __restrict__ groups, uint32_t n,
+                                     int elem_shift, int elem_bits, uint32_t end,
+                                     const uint32_t* __restrict__ new_head,
+                                     const uint32_t* __restrict__ new_rank,
+                                     const uint32_t* __restrict__ old_head,
+                                     const uint32_t* __restrict__ old_rank,
+                                     const uint32_t* __restrict__ new_at,
+                                     const uint32_t* __restrict__ old_at, GroupBase gb,
+                                     SigTable perm, uint32_t* __restrict__ keep,
+                                     uint32_t* __restrict__ next_base) {
+  const uint64_t elem_mask = (uint64_t(1) << elem_bits) - 1;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const uint64_t key = keys[i];
+    const uint32_t hn = new_at[new_rank[i] + new_head[i] - 1];
+    const uint32_t ho = old_at[old_rank[i] + old_head[i] - 1];
+    const uint32_t base = uint32_t(key >> elem_shift) + (hn - ho);
+    const bool single = new_head[i] && (i + 1 == n || new_head[i + 1]);
+    const bool done = single || uint32_t(key & elem_mask) == end;
+    if (done) {
+      const uint32_t g = groups[i];
+      const int s = workset_of(gb, g);
+      perm.p[s][base + (i - hn) - gb.base[s]] = g - gb.base[s];
+    }
+    keep[i] = done ? 0u : 1u;
+    next_base[i] = base;
+  }
+}
+
+__global__ void order_compact_kernel(uint32_t n, const uint32_t* __restrict__ keep,
+                                     const uint32_t* __restrict__ slot,
+                                     const uint32_t* __restrict__ groups,
+                                     const uint32_t* __restrict__ next_base,
+                                     uint32_t* __restrict__ act_group,
+                                     uint32_t* __restrict__ act_base) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    if (keep[i]) {
+      act_group[slot[i]] = groups[i];
+      act_base[slot[i]] = next_base[i];
+    }
   }
 }
 
@@ -348,6 +543,49 @@ int bits_for(uint64_t v) {  // bits needed to hold values 0..v
   int b = 0;
   while (b < 64 && (v >> b) != 0) ++b;
   return b;
+}
+
+// One device allocation cut into 256-byte aligned arrays, freed when the
+// object leaves scope (hipFree waits for the device, so queued work that still
+// reads the arrays completes first).
+class Scratch {
+ public:
+  static size_t bytes(size_t n, size_t elem) { return (n * elem + 255) & ~size_t(255); }
+  explicit Scratch(size_t total) : err_(hipMalloc(&base_, total ? total : 1)) {}
+  ~Scratch() {
+    if (base_) (void)hipFree(base_);
+  }
+  Scratch(const Scratch&) = delete;
+  Scratch& operator=(const Scratch&) = delete;
+  hipError_t error() const { return err_; }
+  template <typename T>
+  T* take(size_t n) {
+    T* p = reinterpret_cast<T*>(static_cast<char*>(base_) + used_);
+    used_ += bytes(n, sizeof(T));
+    return p;
+  }
+
+ private:
+  void* base_ = nullptr;
+  size_t used_ = 0;
+  hipError_t err_;
+};
+
+// Global group numbering over the worksets; false if the total overflows.
+bool make_group_base(int S, const int* group_num, GroupBase* gb) {
+  uint64_t total = 0;
+  for (int s = 0; s <= PS_MAX_WORKSETS; ++s) {
+    if (s < S) {
+      if (group_num[s] < 0) return false;
+      gb->base[s] = uint32_t(total);
+      total += uint64_t(group_num[s]);
+      if (total >= (uint64_t(1) << 31)) return false;
+    } else {
+      gb->base[s] = uint32_t(total);
+    }
+  }
+  gb->S = S;
+  return true;
 }
 
 }  // namespace
@@ -582,6 +820,173 @@ int ps_pre_gather_workset(int group_size, const uint32_t* perm, int groups,
   (void)hipFree(ws);
   if (rc != PS_OK) return rc;
   PS_HIP(e);
+  return PS_OK;
+}
+
+int ps_pre_signature_lists(const int* row_ptr, int rows, int group_type_num, int fine,
+                           const uint64_t* ranked_keys, int count_bits,
+                           const uint32_t* ranked_vals, int nnz, const int* col_ind,
+                           const int* sigbit, int signature_len, const uint32_t* prefix,
+                           const int* group_num, uint32_t* lists, uint32_t* list_begin,
+                           ps_stream_t stream) {
+  PS_CHECK_ARG(row_ptr && ranked_keys && ranked_vals && col_ind && sigbit && prefix &&
+                   group_num && lists && list_begin && rows > 0 && nnz > 0 &&
+                   group_type_num >= 1 && group_type_num <= PS_MAX_WORKSETS &&
+                   signature_len >= 1 && count_bits >= 0 && count_bits < 64 && fine >= 1,
+               "ps_pre_signature_lists: bad argument");
+  ps::GroupBase gb{};
+  PS_CHECK_ARG(ps::make_group_base(group_type_num, group_num, &gb),
+               "ps_pre_signature_lists: bad group counts");
+  const uint32_t total = gb.base[group_type_num];
+  PS_CHECK_ARG(total > 0, "ps_pre_signature_lists: no groups");
+  const int bit_bits = ps::bits_for(uint64_t(signature_len - 1)) > 0
+                           ? ps::bits_for(uint64_t(signature_len - 1))
+                           : 1;
+  const int key_bits = bit_bits + ps::bits_for(uint64_t(total - 1));
+  PS_CHECK_ARG(key_bits <= 64, "ps_pre_signature_lists: key overflow");
+  const size_t n = size_t(nnz);
+  using S = ps::Scratch;
+  S ws(2 * S::bytes(n, 8) + 2 * S::bytes(n, 4) + ps_radix_workspace_bytes(n) +
+       ps_scan_workspace_bytes(n));
+  PS_HIP(ws.error());
+  uint64_t* e = ws.take<uint64_t>(n);
+  uint64_t* e_alt = ws.take<uint64_t>(n);
+  uint32_t* flag = ws.take<uint32_t>(n);
+  uint32_t* pos = ws.take<uint32_t>(n);
+  void* radix_ws = ws.take<char>(ps_radix_workspace_bytes(n));
+  void* scan_ws = ws.take<char>(ps_scan_workspace_bytes(n));
+  hipStream_t st = ps::to_hip(stream);
+  const unsigned grid = ps::grid_for(n);
+  ps::signature_entries_kernel<<<grid, ps::kThreads, 0, st>>>(
+      row_ptr, rows, group_type_num, fine, ranked_keys, count_bits, ranked_vals, nnz, col_ind,
+      sigbit, prefix, gb, bit_bits, e);
+  PS_LAUNCHED();
+  int alt = 0;
+  int rc = ps_radix_sort_pairs_u64(e, e_alt, nullptr, nullptr, n, 0, key_bits, radix_ws, &alt,
+                                   stream);
+  if (rc != PS_OK) return rc;
+  const uint64_t* sorted = alt ? e_alt : e;
+  ps::entry_flags_kernel<<<grid, ps::kThreads, 0, st>>>(sorted, uint32_t(n), flag);
+  PS_LAUNCHED();
+  rc = ps_exclusive_scan_u32(flag, pos, n, scan_ws, stream);
+  if (rc != PS_OK) return rc;
+  ps::entry_lists_kernel<<<grid, ps::kThreads, 0, st>>>(sorted, uint32_t(n), bit_bits, flag, pos,
+                                                         total, lists, list_begin);
+  PS_LAUNCHED();
+  PS_HIP(hipStreamSynchronize(st));
+  return PS_OK;
+}
+
+int ps_pre_signature_order(const uint32_t* lists, const uint32_t* list_begin,
+                           int group_type_num, const int* group_num, int signature_len,
+                           uint32_t* const* perm, ps_stream_t stream) {
+  PS_CHECK_ARG(lists && list_begin && group_num && perm && group_type_num >= 1 &&
+                   group_type_num <= PS_MAX_WORKSETS && signature_len >= 1,
+               "ps_pre_signature_order: bad argument");
+  ps::GroupBase gb{};
+  PS_CHECK_ARG(ps::make_group_base(group_type_num, group_num, &gb),
+               "ps_pre_signature_order: bad group counts");
+  ps::SigTable out{};
+  for (int s = 0; s < group_type_num; ++s) {
+    PS_CHECK_ARG(group_num[s] == 0 || perm[s], "ps_pre_signature_order: null permutation");
+    out.p[s] = perm[s];
+    out.groups[s] = group_num[s];
+  }
+  const uint32_t total = gb.base[group_type_num];
+  if (total == 0) return PS_OK;
+  // Elements take values 0 .. signature_len - 1; signature_len marks a list's end.
+  const uint32_t end = uint32_t(signature_len);
+  const int elem_bits = ps::bits_for(end);
+  const int base_bits = ps::bits_for(uint64_t(total - 1));
+  const int per_key = (64 - base_bits) / elem_bits;
+  PS_CHECK_ARG(per_key >= 1, "ps_pre_signature_order: key overflow");
+  const int elem_shift = per_key * elem_bits;
+  const size_t n0 = total;
+  using S = ps::Scratch;
+  S ws(2 * S::bytes(n0, 8) + 13 * S::bytes(n0, 4) + S::bytes(2, 8) +
+       ps_radix_workspace_bytes(n0) + ps_scan_workspace_bytes(n0));
+  PS_HIP(ws.error());
+  uint64_t* keys = ws.take<uint64_t>(n0);
+  uint64_t* keys_alt = ws.take<uint64_t>(n0);
+  uint32_t* act_group = ws.take<uint32_t>(n0);
+  uint32_t* act_base = ws.take<uint32_t>(n0);
+  uint32_t* vals = ws.take<uint32_t>(n0);
+  uint32_t* vals_alt = ws.take<uint32_t>(n0);
+  uint32_t* new_head = ws.take<uint32_t>(n0);
+  uint32_t* old_head = ws.take<uint32_t>(n0);
+  uint32_t* new_rank = ws.take<uint32_t>(n0);
+  uint32_t* old_rank = ws.take<uint32_t>(n0);
+  uint32_t* new_at = ws.take<uint32_t>(n0);
+  uint32_t* old_at = ws.take<uint32_t>(n0);
+  uint32_t* keep = ws.take<uint32_t>(n0);
+  uint32_t* slot = ws.take<uint32_t>(n0);
+  uint32_t* next_base = ws.take<uint32_t>(n0);
+  unsigned long long* span = ws.take<unsigned long long>(2);
+  void* radix_ws = ws.take<char>(ps_radix_workspace_bytes(n0));
+  void* scan_ws = ws.take<char>(ps_scan_workspace_bytes(n0));
+  hipStream_t st = ps::to_hip(stream);
+
+  uint32_t entries = 0;  // longest possible list: bounds the refinement depth
+  PS_HIP(hipMemcpyAsync(&entries, list_begin + total, sizeof(uint32_t), hipMemcpyDeviceToHost,
+                        st));
+  ps::order_init_kernel<<<ps::grid_for(n0), ps::kThreads, 0, st>>>(total, gb, act_group,
+                                                                   act_base);
+  PS_LAUNCHED();
+  PS_HIP(hipStreamSynchronize(st));
+  uint32_t n = total;
+  for (uint64_t depth = 0; n > 0; depth += uint64_t(per_key)) {
+    if (depth > uint64_t(entries) + uint64_t(per_key))
+      return ps::fail(PS_ERR_RUNTIME, "ps_pre_signature_order: refinement did not converge");
+    const unsigned grid = ps::grid_for(n);
+    ps::order_keys_kernel<<<grid, ps::kThreads, 0, st>>>(act_group, act_base, n, lists,
+                                                         list_begin, uint32_t(depth), per_key,
+                                                         elem_bits, end, keys, vals);
+    PS_LAUNCHED();
+    static const unsigned long long span_init[2] = {0ull, ~0ull};
+    unsigned long long host_span[2] = {0ull, 0ull};
+    PS_HIP(hipMemcpyAsync(span, span_init, sizeof(span_init), hipMemcpyHostToDevice, st));
+    ps::key_span_kernel<<<grid < 1024 ? grid : 1024, ps::kThreads, 0, st>>>(keys, n, span);
+    PS_LAUNCHED();
+    PS_HIP(hipMemcpyAsync(host_span, span, sizeof(host_span), hipMemcpyDeviceToHost, st));
+    PS_HIP(hipStreamSynchronize(st));
+    const uint64_t diff = host_span[0] ^ host_span[1];
+    const uint64_t* k = keys;
+    const uint32_t* g = vals;
+    if (diff != 0) {
+      const int lo = __builtin_ctzll(diff) / 8 * 8;
+      const int hi = 64 - __builtin_clzll(diff);
+      int alt = 0;
+      const int rc = ps_radix_sort_pairs_u64(keys, keys_alt, vals, vals_alt, n, lo, hi,
+                                             radix_ws, &alt, stream);
+      if (rc != PS_OK) return rc;
+      if (alt) {
+        k = keys_alt;
+        g = vals_alt;
+      }
+    }
+    ps::order_flags_kernel<<<grid, ps::kThreads, 0, st>>>(k, n, elem_shift, new_head, old_head);
+    PS_LAUNCHED();
+    int rc = ps_exclusive_scan_u32(new_head, new_rank, n, scan_ws, stream);
+    if (rc == PS_OK) rc = ps_exclusive_scan_u32(old_head, old_rank, n, scan_ws, stream);
+    if (rc != PS_OK) return rc;
+    ps::order_heads_kernel<<<grid, ps::kThreads, 0, st>>>(n, new_head, new_rank, old_head,
+                                                          old_rank, new_at, old_at);
+    PS_LAUNCHED();
+    ps::order_resolve_kernel<<<grid, ps::kThreads, 0, st>>>(
+        k, g, n, elem_shift, elem_bits, end, new_head, new_rank, old_head, old_rank, new_at,
+        old_at, gb, out, keep, next_base);
+    PS_LAUNCHED();
+    rc = ps_exclusive_scan_u32(keep, slot, n, scan_ws, stream);
+    if (rc != PS_OK) return rc;
+    ps::order_compact_kernel<<<grid, ps::kThreads, 0, st>>>(n, keep, slot, g, next_base,
+                                                            act_group, act_base);
+    PS_LAUNCHED();
+    uint32_t tail[2] = {0u, 0u};
+    PS_HIP(hipMemcpyAsync(&tail[0], slot + (n - 1), sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    PS_HIP(hipMemcpyAsync(&tail[1], keep + (n - 1), sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    PS_HIP(hipStreamSynchronize(st));
+    n = tail[0] + tail[1];
+  }
   return PS_OK;
 }
 

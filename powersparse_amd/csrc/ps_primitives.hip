@@ -1,5 +1,6 @@
 // Device-wide primitives for the preprocessing: exclusive scan of uint32 and a
-// stable least-significant-digit radix sort of (key, uint32 value) pairs.
+// stable least-significant-digit radix sort of (key, uint32 value) pairs, or of
+// keys alone when both value buffers are null.
 //
 // Both use plain reduce-then-scan passes (no inter-workgroup waiting), 256
 // threads per workgroup and 4096 items per tile.
@@ -158,7 +159,7 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
     const size_t i = base + size_t(r) * kWave + lane;
     const bool valid = i < n;
     key[r] = valid ? keys_in[i] : K(0);
-    val[r] = valid ? vals_in[i] : 0u;
+    val[r] = (valid && vals_in) ? vals_in[i] : 0u;
     const uint32_t d = uint32_t(key[r] >> shift) & (kBins - 1);
     uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -195,7 +196,7 @@ __global__ __launch_bounds__(kThreads) void radix_scatter_kernel(
       const uint32_t d = uint32_t(key[r] >> shift) & (kBins - 1);
       const size_t pos = size_t(cnt[w][d]) + loc[r];
       keys_out[pos] = key[r];
-      vals_out[pos] = val[r];
+      if (vals_out) vals_out[pos] = val[r];
     }
   }
 }
@@ -214,7 +215,8 @@ int radix_sort(K* keys, K* keys_alt, uint32_t* vals, uint32_t* vals_alt, size_t 
   PS_CHECK_ARG(begin_bit >= 0 && end_bit <= int(8 * sizeof(K)) && begin_bit <= end_bit,
                "radix sort: bad bit range");
   if (n <= 1 || begin_bit == end_bit) return PS_OK;
-  PS_CHECK_ARG(keys && keys_alt && vals && vals_alt && workspace, "radix sort: null buffer");
+  PS_CHECK_ARG(keys && keys_alt && workspace && (vals != nullptr) == (vals_alt != nullptr),
+               "radix sort: null buffer");
   const size_t tiles = (n + kTile - 1) / kTile;
   PS_CHECK_ARG(tiles < (1u << 31) && n < (size_t(1) << 32), "radix sort: too many items");
   uint32_t* table = reinterpret_cast<uint32_t*>(workspace);

@@ -58,11 +58,22 @@ const char* psx_last_error(void) { return g_error.c_str(); }
 
 int psx_matrix_create(int rows, int cols, int nnz, const int* row_ptr, const int* col_ind,
                       const float* sp_data, int cu_count, double* timings_ms, psx_matrix** out) {
+  psx_build_options options{cu_count, PSX_ORDER_AUTO};
+  return psx_matrix_create_ex(rows, cols, nnz, row_ptr, col_ind, sp_data, &options, timings_ms,
+                              out);
+}
+
+int psx_matrix_create_ex(int rows, int cols, int nnz, const int* row_ptr, const int* col_ind,
+                         const float* sp_data, const psx_build_options* options,
+                         double* timings_ms, psx_matrix** out) {
   return Guard([&] {
     Need(out != nullptr, "psx_matrix_create: null output");
     *out = nullptr;
     PowerSparse::PartitionPolicy policy;
-    policy.cu_count = cu_count;
+    if (options) {
+      policy.cu_count = options->cu_count;
+      policy.signature_order = static_cast<PowerSparse::SignatureOrder>(options->signature_order);
+    }
     PowerSparse::PreprocessTimings t;
     auto* m = new PowerSparse::PowerSparseMatrixGPU(rows, cols, nnz, row_ptr, col_ind, sp_data,
                                                     policy, timings_ms ? &t : nullptr);
@@ -72,6 +83,13 @@ int psx_matrix_create(int rows, int cols, int nnz, const int* row_ptr, const int
                            t.signature_ms, t.order_ms, t.gather_ms, t.total_ms};
       std::memcpy(timings_ms, v, sizeof(v));
     }
+  });
+}
+
+int psx_matrix_signature_order(const psx_matrix* m, int* method) {
+  return Guard([&] {
+    Need(m && m->m && method, "psx_matrix_signature_order: null argument");
+    *method = int(m->m->SignatureOrderUsed());
   });
 }
 

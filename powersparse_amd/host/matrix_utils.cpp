@@ -155,7 +155,10 @@ PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num
     bad |= (col_ind[p] < 0 || col_ind[p] >= col_num || !std::isfinite(sp_data[p]));
   if (bad) throw std::invalid_argument("Invalid CSR column index or sparse value");
   if (policy.cu_count < 0) throw std::invalid_argument("PartitionPolicy::cu_count must be >= 0");
+  if (int(policy.signature_order) < 0 || int(policy.signature_order) > 2)
+    throw std::invalid_argument("PartitionPolicy::signature_order is not a SignatureOrder");
   _cu_count = policy.cu_count;
+  _signature_order = policy.signature_order;
   if (_cu_count == 0) {
     int dev = 0;
     ThrowOnError(ps_get_device(&dev));
@@ -260,51 +263,74 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
                                  start_ptr.data(), res_len.data(), res_atomic0.data(), st));
   clock.Mark(&PreprocessTimings::groups_ms);
 
-  // Signatures, word-major per workset.
+  // Groups in signature order: perm[s][k] = initial group at position k.
   const int words = _signature_len / 32;
+  if (_signature_order == SignatureOrder::kAuto)
+    _signature_order = words <= kBitmapMaxWords ? SignatureOrder::kBitmapWords
+                                                : SignatureOrder::kBitLists;
   DeviceArray<int> d_sigbit(static_cast<size_t>(cols));
   d_sigbit.Upload(sigbit.data(), size_t(cols));
-  std::vector<DeviceArray<uint32_t>> sig(static_cast<size_t>(S));
-  std::vector<uint32_t*> sig_ptr(static_cast<size_t>(S), nullptr);
-  for (int s = 0; s < S; ++s) {
-    sig[size_t(s)].Allocate(size_t(_group_num[s]) * words);
-    sig[size_t(s)].Zero(st);
-    sig_ptr[size_t(s)] = sig[size_t(s)].data();
-  }
-  ThrowOnError(ps_pre_signatures(d_rp.data(), rows, S, fine, keys.data(), count_bits,
-                                 vals.data(), nnz, d_ci.data(), d_sigbit.data(), prefix.data(),
-                                 _group_num, sig_ptr.data(), st));
-  keys.Reset();
-  clock.Mark(&PreprocessTimings::signature_ms);
-
-  // Stable sort of each workset's groups by signature, descending, word 0
-  // most significant: one stable pass per word from the last word to the first
-  // (matrix_utils.cu:590-592), skipping words and digits that do not vary.
   std::vector<DeviceArray<uint32_t>> perm(static_cast<size_t>(S));
+  std::vector<uint32_t*> perm_ptr(static_cast<size_t>(S), nullptr);
   for (int s = 0; s < S; ++s) {
-    const int G = _group_num[s];
-    if (G == 0) continue;
-    perm[size_t(s)].Allocate(size_t(G));
-    ThrowOnError(ps_iota_u32(perm[size_t(s)].data(), G, st));
-    if (G == 1) continue;
-    std::vector<uint32_t> w_or(static_cast<size_t>(words)), w_and(static_cast<size_t>(words));
-    ThrowOnError(ps_pre_signature_span(sig[size_t(s)].data(), G, words, w_or.data(),
-                                       w_and.data(), st));
-    DeviceArray<uint32_t> k1(static_cast<size_t>(G)), k2(static_cast<size_t>(G)), p2(static_cast<size_t>(G));
-    DeviceArray<char> ws(ps_radix_workspace_bytes(size_t(G)));
-    for (int w = words - 1; w >= 0; --w) {
-      const uint32_t diff = w_or[size_t(w)] ^ w_and[size_t(w)];
-      if (diff == 0) continue;
-      const int lo = __builtin_ctz(diff) / 8 * 8;
-      const int hi = 32 - __builtin_clz(diff);
-      ThrowOnError(ps_pre_signature_keys(sig[size_t(s)].data() + size_t(w) * G,
-                                         perm[size_t(s)].data(), G, k1.data(), st));
-      int alt = 0;
-      ThrowOnError(ps_radix_sort_pairs_u32(k1.data(), k2.data(), perm[size_t(s)].data(),
-                                           p2.data(), size_t(G), lo, hi, ws.data(), &alt, st));
-      if (alt) std::swap(perm[size_t(s)], p2);
+    if (_group_num[s] == 0) continue;
+    perm[size_t(s)].Allocate(size_t(_group_num[s]));
+    perm_ptr[size_t(s)] = perm[size_t(s)].data();
+  }
+  if (_signature_order == SignatureOrder::kBitLists) {
+    // Each group's sorted distinct signature bits, then the tie refinement.
+    size_t total = 0;
+    for (int s = 0; s < S; ++s) total += size_t(_group_num[s]);
+    DeviceArray<uint32_t> lists(static_cast<size_t>(nnz)), list_begin(total + 1);
+    ThrowOnError(ps_pre_signature_lists(d_rp.data(), rows, S, fine, keys.data(), count_bits,
+                                        vals.data(), nnz, d_ci.data(), d_sigbit.data(),
+                                        _signature_len, prefix.data(), _group_num, lists.data(),
+                                        list_begin.data(), st));
+    keys.Reset();
+    clock.Mark(&PreprocessTimings::signature_ms);
+    ThrowOnError(ps_pre_signature_order(lists.data(), list_begin.data(), S, _group_num,
+                                        _signature_len, perm_ptr.data(), st));
+  } else {
+    // Signature bitmaps, word-major per workset.
+    std::vector<DeviceArray<uint32_t>> sig(static_cast<size_t>(S));
+    std::vector<uint32_t*> sig_ptr(static_cast<size_t>(S), nullptr);
+    for (int s = 0; s < S; ++s) {
+      sig[size_t(s)].Allocate(size_t(_group_num[s]) * words);
+      sig[size_t(s)].Zero(st);
+      sig_ptr[size_t(s)] = sig[size_t(s)].data();
     }
-    sig[size_t(s)].Reset();
+    ThrowOnError(ps_pre_signatures(d_rp.data(), rows, S, fine, keys.data(), count_bits,
+                                   vals.data(), nnz, d_ci.data(), d_sigbit.data(), prefix.data(),
+                                   _group_num, sig_ptr.data(), st));
+    keys.Reset();
+    clock.Mark(&PreprocessTimings::signature_ms);
+    // Stable sort of each workset's groups by signature, descending, word 0
+    // most significant: one stable pass per word from the last word to the
+    // first (matrix_utils.cu:590-592), skipping words and digits that do not vary.
+    for (int s = 0; s < S; ++s) {
+      const int G = _group_num[s];
+      if (G == 0) continue;
+      ThrowOnError(ps_iota_u32(perm[size_t(s)].data(), G, st));
+      if (G == 1) continue;
+      std::vector<uint32_t> w_or(static_cast<size_t>(words)), w_and(static_cast<size_t>(words));
+      ThrowOnError(ps_pre_signature_span(sig[size_t(s)].data(), G, words, w_or.data(),
+                                         w_and.data(), st));
+      DeviceArray<uint32_t> k1(static_cast<size_t>(G)), k2(static_cast<size_t>(G)), p2(static_cast<size_t>(G));
+      DeviceArray<char> ws(ps_radix_workspace_bytes(size_t(G)));
+      for (int w = words - 1; w >= 0; --w) {
+        const uint32_t diff = w_or[size_t(w)] ^ w_and[size_t(w)];
+        if (diff == 0) continue;
+        const int lo = __builtin_ctz(diff) / 8 * 8;
+        const int hi = 32 - __builtin_clz(diff);
+        ThrowOnError(ps_pre_signature_keys(sig[size_t(s)].data() + size_t(w) * G,
+                                           perm[size_t(s)].data(), G, k1.data(), st));
+        int alt = 0;
+        ThrowOnError(ps_radix_sort_pairs_u32(k1.data(), k2.data(), perm[size_t(s)].data(),
+                                             p2.data(), size_t(G), lo, hi, ws.data(), &alt, st));
+        if (alt) std::swap(perm[size_t(s)], p2);
+      }
+      sig[size_t(s)].Reset();
+    }
   }
   clock.Mark(&PreprocessTimings::order_ms);
 

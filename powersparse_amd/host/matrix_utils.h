@@ -26,11 +26,22 @@ enum SigBitMode { PPL = 0, FFC = 1 };
 enum FreqSort { FreqNoSort = 0, FreqDoSort = 1 };
 enum GroupSort { GroupNoSort = 0, GroupDoSort = 1 };
 
+// How the groups of a workset are put in signature order. Both methods give
+// the order of the reference's per-word stable sorts (utils/matrix_utils.cu:
+// 588-593); they differ in cost. kBitmapWords builds the signature bitmaps
+// (groups x L/32 words) and sorts once per word that varies; kBitLists sorts
+// each group's list of distinct signature bits and refines ties a few list
+// elements at a time, in memory bounded by nnz whatever L is. kAuto takes the
+// bitmaps up to kBitmapMaxWords words, the lists beyond.
+enum class SignatureOrder { kAuto = 0, kBitmapWords = 1, kBitLists = 2 };
+constexpr int kBitmapMaxWords = 128;
+
 // Partition settings. The reference hard-codes all of them except the CU
 // count, which it reads from the current device (utils/matrix_utils.cu:31-63);
 // cu_count == 0 means "the current device's multiProcessorCount".
 struct PartitionPolicy {
   int cu_count = 0;
+  SignatureOrder signature_order = SignatureOrder::kAuto;
 };
 
 // Wall-clock milliseconds of the preprocessing stages (host timer, the stream
@@ -71,6 +82,8 @@ class PowerSparseMatrixGPU {
   // partition was computed for.
   int SignatureLen() const { return _signature_len; }
   int PartitionCuCount() const { return _cu_count; }
+  // The signature order method the build used (never kAuto).
+  SignatureOrder SignatureOrderUsed() const { return _signature_order; }
 
  private:
   void Build(const int* row_ptr, const int* col_ind, const float* sp_data,
@@ -81,6 +94,7 @@ class PowerSparseMatrixGPU {
   int _group_type_num = 0, _group_fine_size = 16;
   int _signature_len = 32;
   int _cu_count = 0;
+  SignatureOrder _signature_order = SignatureOrder::kAuto;
   int* _group_num = nullptr;
   int** _workset_col_ind = nullptr;
   float** _workset_sp_data = nullptr;

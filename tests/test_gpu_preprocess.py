@@ -11,10 +11,15 @@ from test_oracle_preprocess import csr_from_rows
 pytestmark = pytest.mark.gpu
 
 
-def compare(csr, cu):
+ORDERS = ["bitmap_words", "bit_lists"]
+
+
+def compare(csr, cu, order="auto"):
     w = oracle.preprocess(csr.rows, csr.cols, csr.row_ptr, csr.col_ind, csr.values, cu)
     say(f"  oracle S={w.S} groups={w.group_num} L={w.L}")
-    m = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=cu)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=cu, signature_order=order)
+    if order != "auto":
+        assert m.signature_order == order
     assert m.GroupTypeNum() == w.S
     assert m.GroupNum() == w.group_num
     assert m.SignatureLen() == w.L
@@ -34,18 +39,20 @@ def compare(csr, cu):
     return w
 
 
-def test_hand_cases():
+@pytest.mark.parametrize("order", ORDERS)
+def test_hand_cases(order):
     setup()
     rp, ci, va = csr_from_rows([[0, 1, 2], [0], [3, 0]])
-    compare(ps.HostCsr(3, 4, rp, ci, va), 1)
+    compare(ps.HostCsr(3, 4, rp, ci, va), 1, order)
     rows = [list(range(32))] * 40 + [list(range(33)), list(range(64)), [], list(range(64, 69))]
     rp, ci, va = csr_from_rows(rows)
-    compare(ps.HostCsr(44, 70, rp, ci, va), 1)
+    compare(ps.HostCsr(44, 70, rp, ci, va), 1, order)
 
 
+@pytest.mark.parametrize("order", ORDERS)
 @pytest.mark.parametrize("seed", range(8))
 @pytest.mark.parametrize("cu", [1, 2, 4, 64])
-def test_random_graphs(seed, cu):
+def test_random_graphs(seed, cu, order):
     setup()
     rng = np.random.default_rng(seed)
     csr = random_graph(rng, int(rng.integers(20, 400)), int(rng.integers(10, 3000)),
@@ -53,22 +60,91 @@ def test_random_graphs(seed, cu):
                        hub_deg=int(rng.integers(100, 2000)), dup=(seed % 3 == 2))
     if csr.nnz == 0:
         return
-    say(f"random seed={seed} cu={cu} rows={csr.rows} nnz={csr.nnz}")
-    compare(csr, cu)
+    say(f"random seed={seed} cu={cu} order={order} rows={csr.rows} nnz={csr.nnz}")
+    compare(csr, cu, order)
 
 
+@pytest.mark.parametrize("order", ORDERS)
 @pytest.mark.parametrize("cfg,scale,cu", [
     ("C0", 1, 256), ("C0", 1, 1), ("C1", 100, 1), ("C1", 20, 8), ("C3", 100, 2),
     ("C4", 64, 1), ("C4", 16, 4)])
-def test_configs(cfg, scale, cu):
+def test_configs(cfg, scale, cu, order):
     setup()
     csr = ps.synth(cfg, seed=7, scale=scale)
-    say(f"config {cfg}/{scale} cu={cu} rows={csr.rows} nnz={csr.nnz}")
-    compare(csr, cu)
+    say(f"config {cfg}/{scale} cu={cu} order={order} rows={csr.rows} nnz={csr.nnz}")
+    compare(csr, cu, order)
 
 
+def test_full_c4_bit_lists():
+    # L = 582720 bits: the bitmaps would take groups x 18210 words (~175 GB);
+    # the default build takes the bit lists, the oracle its comparison sort
+    setup()
+    csr = ps.synth("C4", seed=1)
+    say(f"full C4 rows={csr.rows} nnz={csr.nnz}")
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=256)
+    assert m.signature_order == "bit_lists"
+    m.close()
+    w = compare(csr, 256)
+    assert w.L == 582720 and w.signature[0] is None
+
+
+def run_order(group_sets, length):
+    """ps_pre_signature_order on worksets given as lists of bit sets."""
+    from powersparse_amd import _native
+    import ctypes
+    flat, begin = [], [0]
+    for sets in group_sets:
+        for bits in sets:
+            flat.extend(sorted(set(bits)))
+            begin.append(len(flat))
+    lists = ps.DeviceBuffer(host=np.asarray(flat or [0], np.uint32))
+    lb = ps.DeviceBuffer(host=np.asarray(begin, np.uint32))
+    S = len(group_sets)
+    counts = (ctypes.c_int * S)(*[len(x) for x in group_sets])
+    perms = [ps.DeviceBuffer(max(len(x), 1) * 4) for x in group_sets]
+    ptrs = (ctypes.c_void_p * S)(*[p.ptr for p in perms])
+    ps._hip_call(_native.hip().ps_pre_signature_order(lists.ptr, lb.ptr, S, counts, length,
+                                                      ptrs, None))
+    return [perms[s].download(np.uint32)[:len(x)] for s, x in enumerate(group_sets)]
+
+
+def test_signature_order_direct():
+    setup()
+    rng = np.random.default_rng(11)
+    length = 4000
+    common = sorted(rng.choice(length, 300, replace=False).tolist())
+    worksets = []
+    for s in range(4):
+        sets = []
+        if s == 2:
+            worksets.append(sets)  # an empty workset
+            continue
+        for g in range(int(rng.integers(50, 700))):
+            kind = rng.random()
+            if kind < 0.3:  # a long shared prefix, cut or extended at a random depth
+                cut = int(rng.integers(1, len(common) + 1))
+                extra = rng.integers(0, length, size=int(rng.integers(0, 3))).tolist()
+                sets.append(common[:cut] + extra)
+            elif kind < 0.4 and sets:  # an exact repeat
+                sets.append(list(sets[int(rng.integers(0, len(sets)))]))
+            else:
+                sets.append(rng.integers(0, length, size=int(rng.integers(1, 40))).tolist())
+        worksets.append(sets)
+    say("direct order: groups", [len(x) for x in worksets])
+    got = run_order(worksets, length)
+    for s, sets in enumerate(worksets):
+        np.testing.assert_array_equal(got[s], oracle.order_bit_lists(sets), err_msg=f"ws {s}")
+
+
+def test_signature_order_single_group():
+    setup()
+    got = run_order([[[5, 1]], []], 32)
+    assert list(got[0]) == [0]
+
+
+@pytest.mark.parametrize("order", ORDERS)
 @pytest.mark.parametrize("deg,rows", [(2048, 40), (8192, 36), (16384, 33), (20000, 34)])
-def test_large_groups(deg, rows):
+def test_large_groups(deg, rows, order):
     # P = 1: 32+ rows of `deg` nonzeros make GROUP_SIZE up to 16384, exercising
     # the LDS bitonic (<= 8192) and the radix (> 8192) within-group column sorts
     setup()
@@ -78,8 +154,8 @@ def test_large_groups(deg, rows):
     rp = np.arange(rows + 1, dtype=np.int32) * deg
     csr = ps.HostCsr(rows, cols, rp, ci.astype(np.int32),
                      rng.uniform(-1, 1, ci.size).astype(np.float32))
-    say(f"large groups deg={deg} rows={rows}")
-    w = compare(csr, 1)
+    say(f"large groups deg={deg} rows={rows} order={order}")
+    w = compare(csr, 1, order)
     assert w.S >= 2
 
 

@@ -180,8 +180,9 @@ def random_graph(rng, rows, cols, max_deg, dup=False, empty_frac=0.1):
     return np.array(rp, np.int32), np.array(ci, np.int32), va
 
 
+@pytest.mark.parametrize("order", ["bitmap_words", "bit_lists"])
 @pytest.mark.parametrize("seed", range(12))
-def test_brute_force_agreement(seed):
+def test_brute_force_agreement(seed, order):
     rng = np.random.default_rng(100 + seed)
     rows = int(rng.integers(5, 60))
     cols = int(rng.integers(3, 90))
@@ -191,7 +192,7 @@ def test_brute_force_agreement(seed):
     if ci.size == 0:
         return
     for cu in (1, 2, 4, 64):
-        w = oracle.preprocess(rows, cols, rp, ci, va, cu)
+        w = oracle.preprocess(rows, cols, rp, ci, va, cu, signature_order=order)
         S, b = brute.preprocess(rows, cols, rp.tolist(), ci.tolist(), va.tolist(), cu,
                                 w.sigbit.tolist(), w.L)
         assert w.S == S
@@ -203,6 +204,39 @@ def test_brute_force_agreement(seed):
             np.testing.assert_array_equal(w.val[s], np.array(b[s]["val"], np.float32))
         assert list(w.residue_offset) == b[0]["offsets"]
         assert [bool(x) for x in w.residue_atomic] == b[0]["atomic"]
+
+
+def bigint_order(bit_sets, length):
+    """Descending order of the L-bit signature integers (bit b weighs
+    2^(L-1-b)), ties in group order (sorted() is stable)."""
+    value = [sum(1 << (length - 1 - b) for b in set(bits)) for bits in bit_sets]
+    return sorted(range(len(bit_sets)), key=lambda g: -value[g])
+
+
+def test_order_bit_lists_hand():
+    # prefix relations, duplicates, an empty set and equal sets
+    sets = [[3], [0, 1], [1, 0, 0], [0], [], [0, 1, 2], [2, 5], [3], [0, 2]]
+    # 0,1,2 > 0,1 = 1,0,0 > 0,2 > 0 > 2,5 > 3 = 3 > empty
+    assert list(oracle.order_bit_lists(sets)) == [5, 1, 2, 8, 3, 6, 0, 7, 4]
+    assert list(oracle.order_bit_lists(sets)) == bigint_order(sets, 8)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_order_bit_lists_bigint(seed):
+    rng = np.random.default_rng(seed)
+    length = int(rng.choice([6, 32, 96]))
+    groups = int(rng.integers(1, 400))
+    sets = []
+    for _ in range(groups):
+        if sets and rng.random() < 0.2:  # repeat or extend an earlier set
+            base = list(sets[int(rng.integers(0, len(sets)))])
+            if rng.random() < 0.5:
+                base.append(int(rng.integers(0, length)))
+            sets.append(base)
+        else:
+            k = int(rng.integers(1, min(length, 12) + 1))
+            sets.append(rng.integers(0, length, size=k).tolist())
+    assert list(oracle.order_bit_lists(sets)) == bigint_order(sets, length)
 
 
 def check_structure(rows, cols, rp, ci, va, w):
@@ -234,6 +268,8 @@ def check_structure(rows, cols, rp, ci, va, w):
         for g in range(w.group_num[s]):
             seg = w.col[s][offs[g]:offs[g + 1]]
             assert (np.diff(seg) >= 0).all()
+        if w.signature[s] is None:  # ordered by bit lists
+            continue
         sig = w.signature[s][:, w.perm[s]].T  # sorted groups x words
         for k in range(1, sig.shape[0]):
             assert tuple(sig[k - 1]) >= tuple(sig[k])
@@ -254,6 +290,21 @@ def test_structure_scaled_configs(cfg, scale, cu):
     w = oracle.preprocess(csr.rows, csr.cols, csr.row_ptr, csr.col_ind, csr.values, cu)
     assert w.S >= 2
     check_structure(csr.rows, csr.cols, csr.row_ptr, csr.col_ind, csr.values, w)
+
+
+@pytest.mark.parametrize("cfg,scale,cu", [("C0", 1, 256), ("C1", 500, 1), ("C3", 800, 1),
+                                          ("C4", 64, 2), ("C4", 256, 2)])
+def test_order_methods_agree(cfg, scale, cu):
+    import powersparse_amd as ps
+    csr = ps.synth(cfg, seed=5, scale=scale)
+    args = (csr.rows, csr.cols, csr.row_ptr, csr.col_ind, csr.values, cu)
+    a = oracle.preprocess(*args, signature_order="bitmap_words")
+    b = oracle.preprocess(*args, signature_order="bit_lists")
+    assert a.S == b.S and b.signature[0] is None
+    for s in range(a.S):
+        assert (a.perm[s] == b.perm[s]).all()
+        assert (a.col[s] == b.col[s]).all() and (a.des[s] == b.des[s]).all()
+    assert (a.residue_offset == b.residue_offset).all()
 
 
 @pytest.mark.parametrize("args,msg", [
