@@ -49,6 +49,7 @@ enum { PSX_ORDER_AUTO = 0, PSX_ORDER_BITMAP_WORDS = 1, PSX_ORDER_BIT_LISTS = 2 }
 typedef struct psx_build_options {
   int cu_count;
   int signature_order;
+  int csr_positions; /* nonzero: keep each nonzero's CSR position (psx_sddmm_csr) */
 } psx_build_options;
 /* psx_matrix_create with options (NULL: all defaults). No reference counterpart. */
 int psx_matrix_create_ex(int rows, int cols, int nnz, const int* row_ptr, const int* col_ind,
@@ -82,6 +83,19 @@ int psx_sddmm(const psx_matrix* m, int N, const float* lhs, const float* rhs, fl
               int stream_count, const ps_stream_t* streams);
 int psx_sddmm_async(const psx_matrix* m, int N, const float* lhs, const float* rhs,
                     float* const* out, ps_stream_t stream);
+/* SDDMM into CSR order: out_csr holds MatrixNNZ floats, entry p for the p-th
+ * nonzero of the input CSR (no zeroing needed). One launch on `stream`. Needs a
+ * matrix built with csr_positions. Replaces: the caller-side permutation of the
+ * reference's workset-order output (PowerSparse_SDDMM.h:11-12). */
+int psx_sddmm_csr(const psx_matrix* m, int N, const float* lhs, const float* rhs,
+                  float* out_csr, ps_stream_t stream);
+/* Workset-order per-nonzero values (values[s], as SDDMM writes them) into CSR
+ * order. Needs a matrix built with csr_positions. Same replacement. */
+int psx_workset_to_csr(const psx_matrix* m, const float* const* values, float* out_csr,
+                       ps_stream_t stream);
+/* Device array of workset s: CSR position of each stored nonzero (NULL if the
+ * matrix was built without csr_positions or the workset is empty). */
+int psx_matrix_csr_position(const psx_matrix* m, int s, const int** pos);
 
 /* ------------------------------------------------------ host CSR inputs */
 /* Replaces: ReadMatrixMarket (benchmarks/matrix_market.cpp:97-134). */

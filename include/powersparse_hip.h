@@ -161,6 +161,24 @@ int ps_sddmm_workset_launch(int s, const ps_workset* workset, const int* residue
                             int rows, int cols, int N, const float* lhs, const float* rhs,
                             float* out, ps_stream_t stream);
 
+/* SDDMM with the output in the input CSR's order, in ONE launch:
+ * out_csr[csr_pos[s][p]] = sp_data[p] * dot(lhs[group_des[g], :], rhs[col_ind[p], :])
+ * for every stored nonzero p of workset s, csr_pos[s] being each slot's
+ * position in the CSR arrays the matrix was built from (ps_pre_gather_workset's
+ * out_csr_pos). Every CSR position is stored exactly once: out_csr (nnz floats)
+ * needs no zeroing. Same N and shape limits as ps_sddmm_launch.
+ * Replaces: the permutation a caller must apply to the reference's output,
+ * which "is in workset order, not original CSR order" (PowerSparse_SDDMM.h:11-12). */
+int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
+                        const int* const* csr_pos, int rows, int cols, int N, const float* lhs,
+                        const float* rhs, float* out_csr, ps_stream_t stream);
+
+/* out_csr[csr_pos[s][p]] = in[s][p] for p < lengths[s]: moves per-nonzero values
+ * from workset order (e.g. the outputs of ps_sddmm_launch) to CSR order.
+ * Replaces: the same caller-side permutation (PowerSparse_SDDMM.h:11-12). */
+int ps_workset_to_csr(int workset_count, const long long* lengths, const int* const* csr_pos,
+                      const float* const* in, float* out_csr, ps_stream_t stream);
+
 /* ---------------------------------------------------------- primitives */
 /* Device-wide exclusive prefix sum of n uint32 values (out may alias in).
  * workspace: ps_scan_workspace_bytes(n) bytes of device memory.
@@ -280,14 +298,15 @@ int ps_pre_permute_meta(const uint32_t* perm, int groups, const int* src_des, in
 /* Final nonzeros of one workset: group k (in sorted order) takes the members
  * of initial group perm[k] (ranked_vals[group_start[perm[k]] ...]) sorted by
  * column ascending, ties in ranked order, written at offset[k] (residue) or
- * k * group_size (blocks).
+ * k * group_size (blocks). out_csr_pos (optional, same length as out_col)
+ * receives each slot's position in the input CSR arrays.
  * Replaces: GetSrc{Residue,Block}Workset + thrust::sort of NNZPoint2 +
  * Get{Residue,Block}Workset (matrix_utils.cu:329-392, 596-617, 639-656). */
 int ps_pre_gather_workset(int group_size, const uint32_t* perm, int groups,
                           const int* group_start, const int* residue_offset,
                           const uint32_t* ranked_vals, const int* col_ind,
                           const float* sp_data, int* out_col, float* out_val,
-                          ps_stream_t stream);
+                          int* out_csr_pos, ps_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -336,8 +336,9 @@ class PowerSparseMatrixGPU:
     cu_count=0 partitions for the current device; a positive value reproduces
     the partition for a device with that many CUs/SMs. signature_order picks
     how groups are put in signature order ("auto", "bitmap_words" or
-    "bit_lists"; both methods give the same order). With timings=True the
-    stage times (ms) are kept in `.timings`.
+    "bit_lists"; both methods give the same order). csr_positions=True keeps
+    each stored nonzero's CSR position (SDDMMToCSR, WorksetToCSR). With
+    timings=True the stage times (ms) are kept in `.timings`.
     """
 
     TIMING_KEYS = ("upload", "analyze", "rank", "groups", "sigbit", "signature", "order",
@@ -345,7 +346,7 @@ class PowerSparseMatrixGPU:
     ORDER_METHODS = ("auto", "bitmap_words", "bit_lists")
 
     def __init__(self, row_num, col_num, nnz_num, row_ptr, col_ind, sp_data, cu_count=0,
-                 timings=False, signature_order="auto"):
+                 timings=False, signature_order="auto", csr_positions=False):
         row_ptr = np.ascontiguousarray(row_ptr, dtype=np.int32)
         col_ind = np.ascontiguousarray(col_ind, dtype=np.int32)
         sp_data = np.ascontiguousarray(sp_data, dtype=np.float32)
@@ -354,7 +355,8 @@ class PowerSparseMatrixGPU:
         h = ctypes.c_void_p()
         if signature_order not in self.ORDER_METHODS:
             raise ValueError(f"signature_order must be one of {self.ORDER_METHODS}")
-        opts = _native.BuildOptions(int(cu_count), self.ORDER_METHODS.index(signature_order))
+        opts = _native.BuildOptions(int(cu_count), self.ORDER_METHODS.index(signature_order),
+                                    int(bool(csr_positions)))
         _host_call(_native.host().psx_matrix_create_ex(
             int(row_num), int(col_num), int(nnz_num),
             row_ptr.ctypes.data if row_ptr.size else None,
@@ -377,9 +379,11 @@ class PowerSparseMatrixGPU:
         self._group_num = list(g)
 
     @classmethod
-    def from_csr(cls, csr, cu_count=0, timings=False, signature_order="auto"):
+    def from_csr(cls, csr, cu_count=0, timings=False, signature_order="auto",
+                 csr_positions=False):
         return cls(csr.rows, csr.cols, csr.nnz, csr.row_ptr, csr.col_ind, csr.values,
-                   cu_count=cu_count, timings=timings, signature_order=signature_order)
+                   cu_count=cu_count, timings=timings, signature_order=signature_order,
+                   csr_positions=csr_positions)
 
     def close(self):
         if self._h:
@@ -466,6 +470,19 @@ class PowerSparseMatrixGPU:
         return (download(c, np.int32, n), download(v, np.float32, n),
                 download(d, np.int32, self._group_num[s]))
 
+    def csr_position(self, s):
+        """Device pointer of workset s's CSR positions (0 if not kept or empty)."""
+        p = ctypes.c_void_p()
+        _host_call(_native.host().psx_matrix_csr_position(self._h, s, ctypes.byref(p)))
+        return p.value or 0
+
+    def download_csr_position(self, s):
+        """CSR position of every stored nonzero of workset s (numpy int32)."""
+        ptr = self.csr_position(s)
+        if not ptr:
+            raise ValueError("matrix built without csr_positions, or empty workset")
+        return download(ptr, np.int32, self.workset_len(s))
+
     def sddmm_output_sizes(self):
         """Floats per SDDMM output workset (benchmarks/benchmark.cu:147-155)."""
         return [self.workset_len(s) for s in range(self._S)]
@@ -515,6 +532,20 @@ def SDDMMAsync(matrix, N, lhs_gpu, rhs_gpu, sddmm_output_gpu, stream=None):
     _host_call(_native.host().psx_sddmm_async(
         matrix.handle, int(N), _ptr(lhs_gpu), _ptr(rhs_gpu),
         _out_array(sddmm_output_gpu, matrix.GroupTypeNum()), _ptr(stream)))
+
+
+def SDDMMToCSR(matrix, N, lhs_gpu, rhs_gpu, out_csr_gpu, stream=None):
+    """SDDMM with the output in the input CSR's order (MatrixNNZ floats, no
+    zeroing needed). The matrix must be built with csr_positions=True."""
+    _host_call(_native.host().psx_sddmm_csr(matrix.handle, int(N), _ptr(lhs_gpu), _ptr(rhs_gpu),
+                                            _ptr(out_csr_gpu), _ptr(stream)))
+
+
+def WorksetToCSR(matrix, values_gpu, out_csr_gpu, stream=None):
+    """Workset-order per-nonzero values (one buffer per workset) into CSR order."""
+    _host_call(_native.host().psx_workset_to_csr(
+        matrix.handle, _out_array(values_gpu, matrix.GroupTypeNum()), _ptr(out_csr_gpu),
+        _ptr(stream)))
 
 
 # ------------------------------------------------ raw launchers (C ABI)

@@ -29,7 +29,8 @@ c_void_p = ctypes.c_void_p
 
 class BuildOptions(ctypes.Structure):
     """psx_build_options (include/powersparse.h)."""
-    _fields_ = [("cu_count", ctypes.c_int), ("signature_order", ctypes.c_int)]
+    _fields_ = [("cu_count", ctypes.c_int), ("signature_order", ctypes.c_int),
+                ("csr_positions", ctypes.c_int)]
 
 
 class DeviceProps(ctypes.Structure):
@@ -105,6 +106,12 @@ HIP_API = [
     ("ps_sddmm_workset_launch", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
       c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("ps_sddmm_csr_launch", ctypes.c_int,
+     [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int,
+      ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("ps_workset_to_csr", ctypes.c_int,
+     [ctypes.c_int, ctypes.POINTER(ctypes.c_longlong), ctypes.POINTER(c_void_p),
+      ctypes.POINTER(c_void_p), c_void_p, c_void_p]),
     ("ps_scan_workspace_bytes", ctypes.c_size_t, [ctypes.c_size_t]),
     ("ps_exclusive_scan_u32", ctypes.c_int,
      [c_void_p, c_void_p, ctypes.c_size_t, c_void_p, c_void_p]),
@@ -145,7 +152,7 @@ HIP_API = [
       c_void_p]),
     ("ps_pre_gather_workset", ctypes.c_int,
      [ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-      c_void_p, c_void_p, c_void_p]),
+      c_void_p, c_void_p, c_void_p, c_void_p]),
 ]
 
 HOST_API = [
@@ -174,6 +181,11 @@ HOST_API = [
       ctypes.POINTER(c_void_p)]),
     ("psx_sddmm_async", ctypes.c_int,
      [c_void_p, ctypes.c_int, c_void_p, c_void_p, ctypes.POINTER(c_void_p), c_void_p]),
+    ("psx_sddmm_csr", ctypes.c_int,
+     [c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("psx_workset_to_csr", ctypes.c_int,
+     [c_void_p, ctypes.POINTER(c_void_p), c_void_p, c_void_p]),
+    ("psx_matrix_csr_position", ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.POINTER(c_void_p)]),
     ("psx_csr_read_mtx", ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(c_void_p)]),
     ("psx_csr_read_binary", ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(c_void_p)]),
     ("psx_csr_write_binary", ctypes.c_int, [c_void_p, ctypes.c_char_p]),

@@ -423,7 +423,7 @@ __global__ void gather_small_kernel(int gs, const uint32_t* __restrict__ perm, i
                                     const uint32_t* __restrict__ ranked_vals,
                                     const int* __restrict__ col_ind,
                                     const float* __restrict__ sp_data, int* __restrict__ out_col,
-                                    float* __restrict__ out_val) {
+                                    float* __restrict__ out_val, int* __restrict__ out_pos) {
   const int gid = blockIdx.x * blockDim.x + threadIdx.x;
   const int k = gid >> 5;
   const int t = gid & 31;
@@ -447,6 +447,7 @@ __global__ void gather_small_kernel(int gs, const uint32_t* __restrict__ perm, i
   if (has && t < len) {
     out_col[dst + rank] = col;
     out_val[dst + rank] = sp_data[p];
+    if (out_pos) out_pos[dst + rank] = p;
   }
 }
 
@@ -456,7 +457,7 @@ __global__ __launch_bounds__(kThreads) void gather_bitonic_kernel(
     int gs, int tile, const uint32_t* __restrict__ perm, int groups,
     const int* __restrict__ group_start, const uint32_t* __restrict__ ranked_vals,
     const int* __restrict__ col_ind, const float* __restrict__ sp_data, int* __restrict__ out_col,
-    float* __restrict__ out_val) {
+    float* __restrict__ out_val, int* __restrict__ out_pos) {
   extern __shared__ uint64_t smem[];
   uint64_t* keys = smem;
   uint32_t* pos = reinterpret_cast<uint32_t*>(smem + tile);
@@ -499,6 +500,7 @@ __global__ __launch_bounds__(kThreads) void gather_bitonic_kernel(
       const size_t dst = size_t(k) * gs + (e % gs);
       out_col[dst] = int(keys[e] >> 32);
       out_val[dst] = sp_data[pos[e]];
+      if (out_pos) out_pos[dst] = int(pos[e]);
     }
   }
 }
@@ -525,12 +527,14 @@ __global__ void large_group_keys_kernel(int gs, const uint32_t* __restrict__ per
 __global__ void large_group_write_kernel(size_t total, const uint64_t* __restrict__ keys,
                                          const uint32_t* __restrict__ vals, int col_bits,
                                          const float* __restrict__ sp_data,
-                                         int* __restrict__ out_col, float* __restrict__ out_val) {
+                                         int* __restrict__ out_col, float* __restrict__ out_val,
+                                         int* __restrict__ out_pos) {
   const uint64_t mask = (1ull << col_bits) - 1;
   for (size_t e = size_t(blockIdx.x) * blockDim.x + threadIdx.x; e < total;
        e += size_t(gridDim.x) * blockDim.x) {
     out_col[e] = int(keys[e] & mask);
     out_val[e] = sp_data[vals[e]];
+    if (out_pos) out_pos[e] = int(vals[e]);
   }
 }
 
@@ -751,7 +755,7 @@ int ps_pre_permute_meta(const uint32_t* perm, int groups, const int* src_des, in
 int ps_pre_gather_workset(int group_size, const uint32_t* perm, int groups,
                           const int* group_start, const int* residue_offset,
                           const uint32_t* ranked_vals, const int* col_ind, const float* sp_data,
-                          int* out_col, float* out_val, ps_stream_t stream) {
+                          int* out_col, float* out_val, int* out_csr_pos, ps_stream_t stream) {
   PS_CHECK_ARG(perm && group_start && ranked_vals && col_ind && sp_data && out_col && out_val &&
                    groups > 0,
                "ps_pre_gather_workset: bad argument");
@@ -764,7 +768,7 @@ int ps_pre_gather_workset(int group_size, const uint32_t* perm, int groups,
     ps::gather_small_kernel<<<unsigned((threads + ps::kThreads - 1) / ps::kThreads),
                               ps::kThreads, 0, st>>>(group_size, perm, groups, group_start,
                                                      residue_offset, ranked_vals, col_ind,
-                                                     sp_data, out_col, out_val);
+                                                     sp_data, out_col, out_val, out_csr_pos);
     PS_LAUNCHED();
     return PS_OK;
   }
@@ -778,7 +782,7 @@ int ps_pre_gather_workset(int group_size, const uint32_t* perm, int groups,
     const unsigned grid = unsigned((groups + per_block - 1) / per_block);
     ps::gather_bitonic_kernel<<<grid, ps::kThreads, lds, st>>>(
         group_size, tile, perm, groups, group_start, ranked_vals, col_ind, sp_data, out_col,
-        out_val);
+        out_val, out_csr_pos);
     PS_LAUNCHED();
     return PS_OK;
   }
@@ -809,7 +813,7 @@ int ps_pre_gather_workset(int group_size, const uint32_t* perm, int groups,
   if (e == hipSuccess && rc == PS_OK) {
     ps::large_group_write_kernel<<<ps::grid_for(total), ps::kThreads, 0, st>>>(
         total, alt ? keys_alt : keys, alt ? vals_alt : vals, col_bits, sp_data, out_col,
-        out_val);
+        out_val, out_csr_pos);
     e = hipGetLastError();
   }
   if (e == hipSuccess && rc == PS_OK) e = hipStreamSynchronize(st);

@@ -16,6 +16,11 @@
 // sddmm_kernel_block.cu:155-164, sddmm_kernel_residue.cu:295-305): block
 // outputs are stored, residue outputs are added atomically into out[0], the
 // output is in workset order.
+//
+// CSR-order variant (kCsr): each result goes to out_csr[csr_pos[s][p]], the
+// nonzero's position in the input CSR arrays, with a plain store (every CSR
+// position is written exactly once), so no output zeroing and no separate
+// permutation pass.
 #include "ps_common.hpp"
 
 namespace ps {
@@ -36,6 +41,8 @@ struct SddmmArgs {
   const float* rhs;
   uint64_t lhs_bytes;
   uint64_t rhs_bytes;
+  const int* csr_pos[PS_MAX_WORKSETS];  // CSR-order variant only
+  float* csr_out;
 };
 
 // Transposing reduction over the 8 lanes of a slot: in p[j] each lane holds
@@ -93,7 +100,7 @@ __device__ __forceinline__ void slot_dots(const Rows<kBuf>& Y,
   }
 }
 
-template <int KQ, bool kBuf>
+template <int KQ, bool kBuf, bool kCsr>
 __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs args) {
   constexpr int K = 32 * KQ;
   const uint32_t blk = balanced_block(blockIdx.x, gridDim.x);
@@ -104,6 +111,8 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
   while (i + 1 < args.count && task >= args.task_begin[i + 1]) ++i;
   const ps_workset ws = args.ws[i];
   float* __restrict__ out = args.out[i];
+  const int* __restrict__ csr_pos = args.csr_pos[i];
+  float* __restrict__ csr_out = args.csr_out;
   const int local = int(task - args.task_begin[i]);
 
   const int lane = lane_id();
@@ -135,7 +144,10 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     slot_dots<KQ, kBuf>(Y, yoff, x, p);
     const float dot = slot_transpose_sum(p, sub);
     const int pos = local * 64 + lane;
-    if (valid) out[pos] = dot * ws.sp_data[pos];
+    if (valid) {
+      if constexpr (kCsr) csr_out[csr_pos[pos]] = dot * ws.sp_data[pos];
+      else out[pos] = dot * ws.sp_data[pos];
+    }
   } else {
     const int rcap = args.rcap;
     const int h = lane / rcap, q = lane % rcap;
@@ -160,26 +172,46 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
       slot_dots<KQ, kBuf>(Y, yoff, x, p);
       const float dot = slot_transpose_sum(p, sub);
       const int k = c0 + q;
-      if (k < len) unsafeAtomicAdd(out + beg + k, dot * ws.sp_data[beg + k]);
+      if (k < len) {
+        if constexpr (kCsr) csr_out[csr_pos[beg + k]] = dot * ws.sp_data[beg + k];
+        else unsafeAtomicAdd(out + beg + k, dot * ws.sp_data[beg + k]);
+      }
     }
   }
 }
 
-template <int KQ>
-void launch_kq(const SddmmArgs& a, bool buf, unsigned grid, hipStream_t stream) {
-  if (buf) sddmm_kernel<KQ, true><<<grid, kWave * kWavesPerBlock, 0, stream>>>(a);
-  else sddmm_kernel<KQ, false><<<grid, kWave * kWavesPerBlock, 0, stream>>>(a);
+// out[pos[e]] = in[e]: workset-order values to CSR order.
+__global__ void to_csr_kernel(const float* __restrict__ in, const int* __restrict__ pos,
+                              size_t n, float* __restrict__ out) {
+  for (size_t e = size_t(blockIdx.x) * blockDim.x + threadIdx.x; e < n;
+       e += size_t(gridDim.x) * blockDim.x)
+    out[pos[e]] = in[e];
 }
 
+template <int KQ>
+void launch_kq(const SddmmArgs& a, bool buf, unsigned grid, hipStream_t stream) {
+  constexpr unsigned kBlock = kWave * kWavesPerBlock;
+  if (a.csr_out) {
+    if (buf) sddmm_kernel<KQ, true, true><<<grid, kBlock, 0, stream>>>(a);
+    else sddmm_kernel<KQ, false, true><<<grid, kBlock, 0, stream>>>(a);
+  } else {
+    if (buf) sddmm_kernel<KQ, true, false><<<grid, kBlock, 0, stream>>>(a);
+    else sddmm_kernel<KQ, false, false><<<grid, kBlock, 0, stream>>>(a);
+  }
+}
+
+// outs[q] (workset order) or, when csr_out is set, csr_pos[q] + csr_out.
 int launch(int count, const int* order, const ps_workset* worksets, float* const* outs,
-           const int* residue_offset, int rows, int cols, int N, const float* lhs,
-           const float* rhs, int rcap, hipStream_t stream) {
+           const int* const* csr_pos, float* csr_out, const int* residue_offset, int rows,
+           int cols, int N, const float* lhs, const float* rhs, int rcap, hipStream_t stream) {
   PS_CHECK_ARG(N > 0 && N % 32 == 0 && N <= 512,
                "SDDMM requires N to be a multiple of 32 between 32 and 512");
   PS_CHECK_ARG(int64_t(rows) * N <= INT32_MAX && int64_t(cols) * N <= INT32_MAX,
                "Dense dimensions exceed the 32-bit kernel indexing range");
-  PS_CHECK_ARG(lhs && rhs && outs, "Invalid SDDMM buffers");
+  PS_CHECK_ARG(lhs && rhs && (csr_out ? csr_pos != nullptr : outs != nullptr),
+               "Invalid SDDMM buffers");
   SddmmArgs a{};
+  a.csr_out = csr_out;
   a.N = N;
   a.rcap = rcap;
   a.lhs = lhs;
@@ -196,7 +228,8 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
   for (int q = 0; q < count; ++q) {
     const ps_workset& w = worksets[q];
     if (w.group_num <= 0) continue;
-    PS_CHECK_ARG(outs[q], "Missing SDDMM output workset");
+    if (csr_out) PS_CHECK_ARG(csr_pos[q], "Missing CSR positions of an SDDMM workset");
+    else PS_CHECK_ARG(outs[q], "Missing SDDMM output workset");
     PS_CHECK_ARG(w.col_ind && w.sp_data && w.group_des, "Invalid SDDMM workset buffers");
     const int s = order[q];
     uint64_t t;
@@ -210,7 +243,8 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
     }
     a.ws[n] = w;
     if (s == 0) a.ws[n].group_size = 0;
-    a.out[n] = outs[q];
+    if (csr_out) a.csr_pos[n] = csr_pos[q];
+    else a.out[n] = outs[q];
     a.task_begin[n] = uint32_t(tasks);
     tasks += t;
     ++n;
@@ -264,16 +298,54 @@ int ps_sddmm_launch(int workset_count, const ps_workset* worksets, const int* re
   // A single workset means fine mode (residue groups of at most 16 nonzeros,
   // utils/matrix_utils.cu:137-141); otherwise residue groups hold at most 31.
   const int rcap = workset_count == 1 ? 16 : 32;
-  return ps::launch(workset_count, order, ordered, outs, residue_offset, rows, cols, N, lhs,
-                    rhs, rcap, ps::to_hip(stream));
+  return ps::launch(workset_count, order, ordered, outs, nullptr, nullptr, residue_offset, rows,
+                    cols, N, lhs, rhs, rcap, ps::to_hip(stream));
+}
+
+int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
+                        const int* const* csr_pos, int rows, int cols, int N, const float* lhs,
+                        const float* rhs, float* out_csr, ps_stream_t stream) {
+  PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets && csr_pos &&
+                   out_csr,
+               "Invalid SDDMM workset count");
+  int order[PS_MAX_WORKSETS];
+  ps_workset ordered[PS_MAX_WORKSETS];
+  const int* pos[PS_MAX_WORKSETS];
+  for (int q = 0; q < workset_count; ++q) {
+    order[q] = workset_count - 1 - q;
+    ordered[q] = worksets[workset_count - 1 - q];
+    pos[q] = csr_pos[workset_count - 1 - q];
+  }
+  const int rcap = workset_count == 1 ? 16 : 32;
+  return ps::launch(workset_count, order, ordered, nullptr, pos, out_csr, residue_offset, rows,
+                    cols, N, lhs, rhs, rcap, ps::to_hip(stream));
+}
+
+int ps_workset_to_csr(int workset_count, const long long* lengths, const int* const* csr_pos,
+                      const float* const* in, float* out_csr, ps_stream_t stream) {
+  PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && lengths && csr_pos &&
+                   in && out_csr,
+               "ps_workset_to_csr: bad argument");
+  for (int s = 0; s < workset_count; ++s) {
+    PS_CHECK_ARG(lengths[s] >= 0, "ps_workset_to_csr: negative length");
+    if (lengths[s] == 0) continue;
+    PS_CHECK_ARG(csr_pos[s] && in[s], "ps_workset_to_csr: missing workset buffers");
+    const size_t n = size_t(lengths[s]);
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    ps::to_csr_kernel<<<unsigned(blocks), 256, 0, ps::to_hip(stream)>>>(in[s], csr_pos[s], n,
+                                                                        out_csr);
+    PS_LAUNCHED();
+  }
+  return PS_OK;
 }
 
 int ps_sddmm_workset_launch(int s, const ps_workset* workset, const int* residue_offset,
                             int rows, int cols, int N, const float* lhs, const float* rhs,
                             float* out, ps_stream_t stream) {
   PS_CHECK_ARG(s >= 0 && s < PS_MAX_WORKSETS && workset, "Invalid SDDMM workset");
-  return ps::launch(1, &s, workset, &out, residue_offset, rows, cols, N, lhs, rhs, 32,
-                    ps::to_hip(stream));
+  return ps::launch(1, &s, workset, &out, nullptr, nullptr, residue_offset, rows, cols, N, lhs,
+                    rhs, 32, ps::to_hip(stream));
 }
 
 }  // extern "C"

@@ -23,6 +23,20 @@ void SDDMM(const PowerSparseMatrixGPU& ps_matrix_gpu, int N, const float* lhs_gp
 void SDDMMAsync(const PowerSparseMatrixGPU& ps_matrix_gpu, int N, const float* lhs_gpu,
                 const float* rhs_gpu, float* const* sddmm_output_gpu, ps_stream_t stream);
 
+// Not in the reference: SDDMM with the output in the input CSR's order,
+// out_csr[p] for the p-th nonzero of the CSR arrays the matrix was built from
+// (MatrixNNZ() floats, no zeroing needed; every entry is written). One launch
+// on `stream`, no device synchronisation. The matrix must have been built with
+// PartitionPolicy::csr_positions.
+void SDDMMToCSR(const PowerSparseMatrixGPU& ps_matrix_gpu, int N, const float* lhs_gpu,
+                const float* rhs_gpu, float* out_csr_gpu, ps_stream_t stream = nullptr);
+
+// Not in the reference: moves workset-order per-nonzero values (e.g. SDDMM
+// outputs) into CSR order, out_csr[WorksetCSRPosition()[s][p]] = values[s][p].
+// Same matrix requirement as SDDMMToCSR.
+void WorksetToCSR(const PowerSparseMatrixGPU& ps_matrix_gpu, const float* const* values_gpu,
+                  float* out_csr_gpu, ps_stream_t stream = nullptr);
+
 }  // namespace PowerSparse
 
 #endif  // POWERSPARSE_SDDMM_H

@@ -58,7 +58,7 @@ const char* psx_last_error(void) { return g_error.c_str(); }
 
 int psx_matrix_create(int rows, int cols, int nnz, const int* row_ptr, const int* col_ind,
                       const float* sp_data, int cu_count, double* timings_ms, psx_matrix** out) {
-  psx_build_options options{cu_count, PSX_ORDER_AUTO};
+  psx_build_options options{cu_count, PSX_ORDER_AUTO, 0};
   return psx_matrix_create_ex(rows, cols, nnz, row_ptr, col_ind, sp_data, &options, timings_ms,
                               out);
 }
@@ -73,6 +73,7 @@ int psx_matrix_create_ex(int rows, int cols, int nnz, const int* row_ptr, const 
     if (options) {
       policy.cu_count = options->cu_count;
       policy.signature_order = static_cast<PowerSparse::SignatureOrder>(options->signature_order);
+      policy.csr_positions = options->csr_positions != 0;
     }
     PowerSparse::PreprocessTimings t;
     auto* m = new PowerSparse::PowerSparseMatrixGPU(rows, cols, nnz, row_ptr, col_ind, sp_data,
@@ -169,6 +170,30 @@ int psx_sddmm_async(const psx_matrix* m, int N, const float* lhs, const float* r
   return Guard([&] {
     Need(m && m->m, "psx_sddmm_async: null matrix");
     PowerSparse::SDDMMAsync(*m->m, N, lhs, rhs, out, stream);
+  });
+}
+
+int psx_sddmm_csr(const psx_matrix* m, int N, const float* lhs, const float* rhs,
+                  float* out_csr, ps_stream_t stream) {
+  return Guard([&] {
+    Need(m && m->m, "psx_sddmm_csr: null matrix");
+    PowerSparse::SDDMMToCSR(*m->m, N, lhs, rhs, out_csr, stream);
+  });
+}
+
+int psx_workset_to_csr(const psx_matrix* m, const float* const* values, float* out_csr,
+                       ps_stream_t stream) {
+  return Guard([&] {
+    Need(m && m->m, "psx_workset_to_csr: null matrix");
+    PowerSparse::WorksetToCSR(*m->m, values, out_csr, stream);
+  });
+}
+
+int psx_matrix_csr_position(const psx_matrix* m, int s, const int** pos) {
+  return Guard([&] {
+    Need(m && m->m && pos, "psx_matrix_csr_position: null argument");
+    Need(s >= 0 && s < m->m->GroupTypeNum(), "psx_matrix_csr_position: workset out of range");
+    *pos = m->m->WorksetCSRPosition() ? m->m->WorksetCSRPosition()[s] : nullptr;
   });
 }
 

@@ -159,6 +159,7 @@ PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num
     throw std::invalid_argument("PartitionPolicy::signature_order is not a SignatureOrder");
   _cu_count = policy.cu_count;
   _signature_order = policy.signature_order;
+  _keep_csr_pos = policy.csr_positions;
   if (_cu_count == 0) {
     int dev = 0;
     ThrowOnError(ps_get_device(&dev));
@@ -338,6 +339,7 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
   _workset_col_ind = new int*[S]();
   _workset_sp_data = new float*[S]();
   _group_des = new int*[S]();
+  if (_keep_csr_pos) _workset_csr_pos = new int*[S]();
   ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_residue_offset), sizeof(int) * (size_t(G0) + 1)));
   ThrowOnError(ps_memset_async(_residue_offset, 0, sizeof(int) * (size_t(G0) + 1), st));
   if (G0 > 0) {
@@ -371,10 +373,13 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
     }
     ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_workset_col_ind[s]), sizeof(int) * size));
     ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_workset_sp_data[s]), sizeof(float) * size));
+    if (_keep_csr_pos)
+      ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_workset_csr_pos[s]), sizeof(int) * size));
     ThrowOnError(ps_pre_gather_workset(s == 0 ? 0 : GROUP_SIZE(s), perm[size_t(s)].data(), G,
                                        start[size_t(s)].data(), s == 0 ? _residue_offset : nullptr,
                                        vals.data(), d_ci.data(), d_sv.data(), _workset_col_ind[s],
-                                       _workset_sp_data[s], st));
+                                       _workset_sp_data[s],
+                                       _keep_csr_pos ? _workset_csr_pos[s] : nullptr, st));
   }
   ThrowOnError(ps_device_synchronize());
   clock.Mark(&PreprocessTimings::gather_ms);
@@ -386,17 +391,20 @@ void PowerSparseMatrixGPU::Release() noexcept {
     if (_workset_col_ind) ps_free(_workset_col_ind[s]);
     if (_workset_sp_data) ps_free(_workset_sp_data[s]);
     if (_group_des) ps_free(_group_des[s]);
+    if (_workset_csr_pos) ps_free(_workset_csr_pos[s]);
   }
   delete[] _group_num;
   delete[] _workset_col_ind;
   delete[] _workset_sp_data;
   delete[] _group_des;
+  delete[] _workset_csr_pos;
   ps_free(_residue_offset);
   ps_free(_residue_atomic);
   _group_num = nullptr;
   _workset_col_ind = nullptr;
   _workset_sp_data = nullptr;
   _group_des = nullptr;
+  _workset_csr_pos = nullptr;
   _residue_offset = nullptr;
   _residue_atomic = nullptr;
 }

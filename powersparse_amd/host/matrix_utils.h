@@ -42,6 +42,9 @@ constexpr int kBitmapMaxWords = 128;
 struct PartitionPolicy {
   int cu_count = 0;
   SignatureOrder signature_order = SignatureOrder::kAuto;
+  // Keep, for every stored nonzero, its position in the input CSR arrays
+  // (4 bytes per nonzero on the device): needed by SDDMMToCSR / WorksetToCSR.
+  bool csr_positions = false;
 };
 
 // Wall-clock milliseconds of the preprocessing stages (host timer, the stream
@@ -84,6 +87,9 @@ class PowerSparseMatrixGPU {
   int PartitionCuCount() const { return _cu_count; }
   // The signature order method the build used (never kAuto).
   SignatureOrder SignatureOrderUsed() const { return _signature_order; }
+  // Position in the input CSR arrays of every stored nonzero, per workset
+  // (same layout as WorksetColInd); nullptr unless the policy asked for it.
+  const int* const* WorksetCSRPosition() const { return _workset_csr_pos; }
 
  private:
   void Build(const int* row_ptr, const int* col_ind, const float* sp_data,
@@ -95,10 +101,12 @@ class PowerSparseMatrixGPU {
   int _signature_len = 32;
   int _cu_count = 0;
   SignatureOrder _signature_order = SignatureOrder::kAuto;
+  bool _keep_csr_pos = false;
   int* _group_num = nullptr;
   int** _workset_col_ind = nullptr;
   float** _workset_sp_data = nullptr;
   int** _group_des = nullptr;
+  int** _workset_csr_pos = nullptr;
   int* _residue_offset = nullptr;
   bool* _residue_atomic = nullptr;
 };

@@ -74,6 +74,40 @@ void SDDMMAsync(const PowerSparseMatrixGPU& m, int N, const float* lhs, const fl
                                m.MatrixCol(), N, lhs, rhs, out, stream));
 }
 
+void SDDMMToCSR(const PowerSparseMatrixGPU& m, int N, const float* lhs, const float* rhs,
+                float* out_csr, ps_stream_t stream) {
+  CheckSddmmArgs(m, N, lhs, rhs, out_csr);
+  if (!m.WorksetCSRPosition())
+    throw std::invalid_argument(
+        "SDDMMToCSR needs a matrix built with PartitionPolicy::csr_positions");
+  const auto ws = Worksets(m);
+  ThrowOnError(ps_sddmm_csr_launch(m.GroupTypeNum(), ws.data(), m.ResidueOffset(),
+                                   m.WorksetCSRPosition(), m.MatrixRow(), m.MatrixCol(), N, lhs,
+                                   rhs, out_csr, stream));
+}
+
+void WorksetToCSR(const PowerSparseMatrixGPU& m, const float* const* values, float* out_csr,
+                  ps_stream_t stream) {
+  if (!values || !out_csr) throw std::invalid_argument("Invalid WorksetToCSR buffers");
+  if (!m.WorksetCSRPosition())
+    throw std::invalid_argument(
+        "WorksetToCSR needs a matrix built with PartitionPolicy::csr_positions");
+  const int S = m.GroupTypeNum();
+  std::vector<long long> lengths(static_cast<size_t>(S));
+  for (int s = 0; s < S; ++s) {
+    if (s == 0) {
+      int total = 0;
+      if (m.GroupNum()[0] > 0)
+        ThrowOnError(ps_memcpy_dtoh(&total, m.ResidueOffset() + m.GroupNum()[0], sizeof(int)));
+      lengths[0] = total;
+    } else {
+      lengths[size_t(s)] = (long long)m.GroupNum()[s] * GROUP_SIZE(s);
+    }
+  }
+  ThrowOnError(ps_workset_to_csr(S, lengths.data(), m.WorksetCSRPosition(), values, out_csr,
+                                 stream));
+}
+
 void SDDMM(const PowerSparseMatrixGPU& m, int N, const float* lhs, const float* rhs,
            float** out, int stream_count, const ps_stream_t* streams) {
   CheckSddmmArgs(m, N, lhs, rhs, out);
