@@ -1,0 +1,101 @@
+"""The benchmark binaries (powersparse_amd/bin/powersparse_{spmm,sddmm}) and
+the batch runner on the GPU: CSV contract, the CHECK path (preprocessing
+invariant + CPU reference, as benchmarks/benchmark.cu:45-96), and exit codes.
+The binaries run as child processes."""
+import csv
+import io
+import os
+import subprocess
+import sys
+
+import pytest
+
+from gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BUILD = os.path.join(ROOT, "powersparse_amd")
+HEADER = ("algorithm,operator,matrix,rows,cols,nnz,N,device,gpu,compute_capability,"
+          "cuda_runtime,cuda_driver,warmup,repeats,seed,check,preprocess_ms,ms,gflops")
+
+# 6 x 5 general real matrix with an empty row (row 4).
+SMALL_MTX = """%%MatrixMarket matrix coordinate real general
+% small test matrix
+6 5 9
+1 1 0.5
+1 3 -1.25
+2 2 2.0
+3 1 1.0
+3 5 3.5
+5 4 -0.75
+6 1 1.5
+6 2 0.25
+6 5 -2.0
+"""
+
+
+def dense_mtx(rows, cols, per_row):
+    lines = ["%%MatrixMarket matrix coordinate pattern general",
+             f"{rows} {cols} {rows * per_row}"]
+    for r in range(rows):
+        for k in range(per_row):
+            lines.append(f"{r + 1} {(r * 7 + k * 3) % cols + 1}")
+    return "\n".join(lines) + "\n"
+
+
+def binary(op):
+    return os.path.join(BUILD, "bin", f"powersparse_{op}")
+
+
+def call(args, **kw):
+    say("$", " ".join(str(a) for a in args))
+    r = subprocess.run([str(a) for a in args], capture_output=True, text=True, timeout=240, **kw)
+    say(r.stderr.strip()[-400:])
+    return r
+
+
+@pytest.mark.parametrize("op,N", [("spmm", 32), ("spmm", 64), ("sddmm", 128)])
+def test_cli_synth_check(op, N):
+    r = call([binary(op), "synth:C0:5", N, 0, 1, 3])
+    assert r.returncode == 0
+    row = next(csv.DictReader(io.StringIO(HEADER + "\n" + r.stdout)))
+    assert row["algorithm"] == "PowerSparse" and row["operator"] == {"spmm": "SpMM",
+                                                                      "sddmm": "SDDMM"}[op]
+    assert row["check"] == "passed" and int(row["N"]) == N and int(row["repeats"]) == 3
+    assert row["compute_capability"].startswith("gfx")
+    assert float(row["ms"]) > 0 and float(row["gflops"]) > 0
+    assert "checks passed" in r.stderr
+
+
+def test_cli_errors(tmp_path):
+    r = call([binary("spmm"), "synth:C0", 48, 0, 0, 1])
+    assert r.returncode == 2 and "N=48 was not selected in main" in r.stderr
+    r = call([binary("sddmm"), tmp_path / "missing.mtx", 32, 0, 0, 1])
+    assert r.returncode == 1 and "Error:" in r.stderr
+    r = call([binary("spmm"), "synth:C0", 32, 0, 2, 1])
+    assert r.returncode == 1 and "CHECK 0 or 1" in r.stderr
+    r = call([binary("spmm")])
+    assert r.returncode == 2 and "Usage:" in r.stderr
+    r = call([binary("spmm"), "--header"])
+    assert r.returncode == 0 and r.stdout.strip() == HEADER
+
+
+def test_runner_end_to_end(tmp_path):
+    data = tmp_path / "data"
+    data.mkdir()
+    (data / "small.mtx").write_text(SMALL_MTX)
+    (data / "rows40.mtx").write_text(dense_mtx(80, 300, 40))
+    manifest = tmp_path / "list.txt"
+    manifest.write_text("# two files and a generated graph\nsmall.mtx\nrows40.mtx\nsynth:C4:2:64\n")
+    out = tmp_path / "out" / "sddmm.csv"
+    env = dict(os.environ, DATASET_LIST=str(manifest))
+    r = call([sys.executable, "-m", "powersparse_amd.cli.run_benchmarks", BUILD, data, "sddmm",
+              0, out, "32,64", 2, 1], cwd=ROOT, env=env)
+    assert r.returncode == 0 and "Results saved to" in r.stderr
+    table = list(csv.DictReader(io.StringIO(out.read_text())))
+    assert [(os.path.basename(t["matrix"]), int(t["N"])) for t in table] == [
+        ("small.mtx", 32), ("small.mtx", 64), ("rows40.mtx", 32), ("rows40.mtx", 64),
+        ("synth:C4:2:64", 32), ("synth:C4:2:64", 64)]
+    assert all(t["check"] == "passed" for t in table)
+    assert [int(t["nnz"]) for t in table[:4]] == [9, 9, 3200, 3200]
