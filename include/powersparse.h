@@ -50,7 +50,12 @@ typedef struct psx_build_options {
   int cu_count;
   int signature_order;
   int csr_positions; /* nonzero: keep each nonzero's CSR position (psx_sddmm_csr) */
+  int task_order;    /* PSX_TASK_AUTO, PSX_TASK_SIGNATURE or PSX_TASK_ROW */
 } psx_build_options;
+/* Group order the operators run in (same results; TaskOrder in matrix_utils.h):
+ * the public signature order, or a row-ordered execution copy kept when it
+ * scores better for gather locality (AUTO) or on request (ROW). */
+enum { PSX_TASK_AUTO = 0, PSX_TASK_SIGNATURE = 1, PSX_TASK_ROW = 2 };
 /* psx_matrix_create with options (NULL: all defaults). No reference counterpart. */
 int psx_matrix_create_ex(int rows, int cols, int nnz, const int* row_ptr, const int* col_ind,
                          const float* sp_data, const psx_build_options* options,
@@ -58,6 +63,10 @@ int psx_matrix_create_ex(int rows, int cols, int nnz, const int* row_ptr, const 
 /* The signature order method the build used (PSX_ORDER_BITMAP_WORDS or
  * PSX_ORDER_BIT_LISTS). No reference counterpart. */
 int psx_matrix_signature_order(const psx_matrix* m, int* method);
+/* The task order the build chose (PSX_TASK_SIGNATURE or PSX_TASK_ROW) and the
+ * locality scores compared (0 when not computed); outputs may be NULL. */
+int psx_matrix_task_order(const psx_matrix* m, int* order, double* score_signature,
+                          double* score_row);
 /* Replaces: ~PowerSparseMatrixGPU (matrix_utils.h:24). */
 int psx_matrix_destroy(psx_matrix* m);
 /* Replaces: MatrixRow/MatrixCol/MatrixNNZ/GroupTypeNum/GroupFineSize (matrix_utils.h:30-34);

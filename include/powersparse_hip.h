@@ -173,6 +173,17 @@ int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int
                         const int* const* csr_pos, int rows, int cols, int N, const float* lhs,
                         const float* rhs, float* out_csr, ps_stream_t stream);
 
+/* SDDMM of worksets laid out in another group order than the public ones (a
+ * task-order execution copy): the result of stored nonzero p of workset s goes
+ * to out[s][out_pos[s][p]], out[s] being the public workset-order buffer; block
+ * results are stored, residue results added, exactly as ps_sddmm_launch does
+ * at the public positions. No reference counterpart (the reference runs the
+ * public layout only). */
+int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
+                            const int* residue_offset, const int* const* out_pos, int rows,
+                            int cols, int N, const float* lhs, const float* rhs,
+                            float* const* out, ps_stream_t stream);
+
 /* out_csr[csr_pos[s][p]] = in[s][p] for p < lengths[s]: moves per-nonzero values
  * from workset order (e.g. the outputs of ps_sddmm_launch) to CSR order.
  * Replaces: the same caller-side permutation (PowerSparse_SDDMM.h:11-12). */
@@ -260,6 +271,25 @@ int ps_pre_signature_keys(const uint32_t* sig_word, const uint32_t* perm, int n,
  * to skip digits that cannot reorder the groups. */
 int ps_pre_signature_span(const uint32_t* sig, int groups, int words, uint32_t* or_host,
                           uint32_t* and_host, ps_stream_t stream);
+
+/* Public workset position of every slot of a task-order execution copy: for
+ * public group k (signature order) holding initial group perm[k],
+ * out_pos[exec_offset[perm[k]] + j] = pub_offset[k] + j over the group's
+ * members. Block worksets (group_size > 0) use k * group_size for both
+ * offsets; the residue workset passes its initial-order and public offsets.
+ * No reference counterpart. */
+int ps_pre_exec_positions(int group_size, const uint32_t* perm, int groups,
+                          const int* exec_offset, const int* pub_offset, int* out_pos,
+                          ps_stream_t stream);
+
+/* Gather-locality score of a task order: the concatenated column sequence
+ * col_ind[0][0 .. lengths[0]), col_ind[1][...], ... is cut into windows of
+ * `window` nonzeros; up to max_windows of them, evenly spaced, are sampled and
+ * *score = (distinct columns per window) / window, averaged (0 when the
+ * sequence is shorter than one window). Lower = more B / Y row reuse between
+ * nearby tasks. Synchronises the stream. No reference counterpart. */
+int ps_pre_locality_score(int count, const int* const* col_ind, const long long* lengths,
+                          int window, int max_windows, double* score, ps_stream_t stream);
 
 /* Sparse form of the signatures, for long signatures where the bitmaps of
  * ps_pre_signatures would not fit: the ascending list of distinct signature

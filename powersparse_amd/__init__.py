@@ -337,16 +337,21 @@ class PowerSparseMatrixGPU:
     the partition for a device with that many CUs/SMs. signature_order picks
     how groups are put in signature order ("auto", "bitmap_words" or
     "bit_lists"; both methods give the same order). csr_positions=True keeps
-    each stored nonzero's CSR position (SDDMMToCSR, WorksetToCSR). With
-    timings=True the stage times (ms) are kept in `.timings`.
+    each stored nonzero's CSR position (SDDMMToCSR, WorksetToCSR). task_order
+    ("auto", "signature" or "row") picks the group order the operators run in
+    (same results); `.task_order` and `.locality` report the choice and the
+    scores compared. With timings=True the stage times (ms) are kept in
+    `.timings` (the task-order step counts into "gather").
     """
 
     TIMING_KEYS = ("upload", "analyze", "rank", "groups", "sigbit", "signature", "order",
                    "gather", "total")
     ORDER_METHODS = ("auto", "bitmap_words", "bit_lists")
+    TASK_ORDERS = ("auto", "signature", "row")
 
     def __init__(self, row_num, col_num, nnz_num, row_ptr, col_ind, sp_data, cu_count=0,
-                 timings=False, signature_order="auto", csr_positions=False):
+                 timings=False, signature_order="auto", csr_positions=False,
+                 task_order="auto"):
         row_ptr = np.ascontiguousarray(row_ptr, dtype=np.int32)
         col_ind = np.ascontiguousarray(col_ind, dtype=np.int32)
         sp_data = np.ascontiguousarray(sp_data, dtype=np.float32)
@@ -355,8 +360,10 @@ class PowerSparseMatrixGPU:
         h = ctypes.c_void_p()
         if signature_order not in self.ORDER_METHODS:
             raise ValueError(f"signature_order must be one of {self.ORDER_METHODS}")
+        if task_order not in self.TASK_ORDERS:
+            raise ValueError(f"task_order must be one of {self.TASK_ORDERS}")
         opts = _native.BuildOptions(int(cu_count), self.ORDER_METHODS.index(signature_order),
-                                    int(bool(csr_positions)))
+                                    int(bool(csr_positions)), self.TASK_ORDERS.index(task_order))
         _host_call(_native.host().psx_matrix_create_ex(
             int(row_num), int(col_num), int(nnz_num),
             row_ptr.ctypes.data if row_ptr.size else None,
@@ -367,6 +374,11 @@ class PowerSparseMatrixGPU:
         method = ctypes.c_int()
         _host_call(_native.host().psx_matrix_signature_order(self._h, ctypes.byref(method)))
         self.signature_order = self.ORDER_METHODS[method.value]
+        order, sig, row = ctypes.c_int(), ctypes.c_double(), ctypes.c_double()
+        _host_call(_native.host().psx_matrix_task_order(self._h, ctypes.byref(order),
+                                                        ctypes.byref(sig), ctypes.byref(row)))
+        self.task_order = self.TASK_ORDERS[order.value]
+        self.locality = {"signature": sig.value, "row": row.value}
         self.timings = dict(zip(self.TIMING_KEYS, list(t))) if timings else None
         rows, cols, nnz, S, fine, L, cu = (ctypes.c_int() for _ in range(7))
         _host_call(_native.host().psx_matrix_info(
@@ -380,10 +392,10 @@ class PowerSparseMatrixGPU:
 
     @classmethod
     def from_csr(cls, csr, cu_count=0, timings=False, signature_order="auto",
-                 csr_positions=False):
+                 csr_positions=False, task_order="auto"):
         return cls(csr.rows, csr.cols, csr.nnz, csr.row_ptr, csr.col_ind, csr.values,
                    cu_count=cu_count, timings=timings, signature_order=signature_order,
-                   csr_positions=csr_positions)
+                   csr_positions=csr_positions, task_order=task_order)
 
     def close(self):
         if self._h:

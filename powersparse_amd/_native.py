@@ -30,7 +30,7 @@ c_void_p = ctypes.c_void_p
 class BuildOptions(ctypes.Structure):
     """psx_build_options (include/powersparse.h)."""
     _fields_ = [("cu_count", ctypes.c_int), ("signature_order", ctypes.c_int),
-                ("csr_positions", ctypes.c_int)]
+                ("csr_positions", ctypes.c_int), ("task_order", ctypes.c_int)]
 
 
 class DeviceProps(ctypes.Structure):
@@ -109,6 +109,14 @@ HIP_API = [
     ("ps_sddmm_csr_launch", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int,
       ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("ps_sddmm_scatter_launch", ctypes.c_int,
+     [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int,
+      ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, ctypes.POINTER(c_void_p), c_void_p]),
+    ("ps_pre_exec_positions", ctypes.c_int,
+     [ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("ps_pre_locality_score", ctypes.c_int,
+     [ctypes.c_int, ctypes.POINTER(c_void_p), ctypes.POINTER(ctypes.c_longlong), ctypes.c_int,
+      ctypes.c_int, c_double_p, c_void_p]),
     ("ps_workset_to_csr", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(ctypes.c_longlong), ctypes.POINTER(c_void_p),
       ctypes.POINTER(c_void_p), c_void_p, c_void_p]),
@@ -164,6 +172,7 @@ HOST_API = [
      [ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, c_void_p,
       ctypes.POINTER(BuildOptions), c_double_p, ctypes.POINTER(c_void_p)]),
     ("psx_matrix_signature_order", ctypes.c_int, [c_void_p, c_int_p]),
+    ("psx_matrix_task_order", ctypes.c_int, [c_void_p, c_int_p, c_double_p, c_double_p]),
     ("psx_matrix_destroy", ctypes.c_int, [c_void_p]),
     ("psx_matrix_info", ctypes.c_int,
      [c_void_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p]),

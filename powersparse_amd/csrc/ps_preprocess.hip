@@ -538,6 +538,64 @@ __global__ void large_group_write_kernel(size_t total, const uint64_t* __restric
   }
 }
 
+// ---- task order ----
+
+// For the public group k (signature order) holding initial group g = perm[k]:
+// out_pos[exec_off(g) + j] = pub_off(k) + j. Offsets are k * gs for blocks,
+// the residue offsets (initial order / signature order) otherwise.
+__global__ void exec_positions_kernel(int gs, const uint32_t* __restrict__ perm, int groups,
+                                      const int* __restrict__ exec_offset,
+                                      const int* __restrict__ pub_offset,
+                                      int* __restrict__ out_pos) {
+  for (int k = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave; k < groups;
+       k += gridDim.x * (blockDim.x / kWave)) {
+    const uint32_t g = perm[k];
+    const int src = gs ? int(g) * gs : exec_offset[g];
+    const int dst = gs ? k * gs : pub_offset[k];
+    const int len = gs ? gs : pub_offset[k + 1] - dst;
+    for (int j = lane_id(); j < len; j += kWave) out_pos[src + j] = dst + j;
+  }
+}
+
+// Locality score: for `windows` windows of `window` consecutive elements of
+// the concatenated column sequence (sampled evenly), the number of distinct
+// columns, counted by inserting into one open-addressing hash table per
+// window (2 * window slots, 0 = empty, keys stored as column + 1).
+struct SeqTable {
+  const int* p[PS_MAX_WORKSETS];
+  uint64_t begin[PS_MAX_WORKSETS + 1];
+  int count;
+};
+
+__global__ void window_distinct_kernel(SeqTable seq, uint64_t stride, uint32_t window,
+                                       uint32_t slots_log2, uint32_t* __restrict__ tables,
+                                       unsigned long long* __restrict__ distinct) {
+  const uint32_t w = blockIdx.y;
+  uint32_t* table = tables + (size_t(w) << slots_log2);
+  const uint32_t mask = (1u << slots_log2) - 1;
+  const uint64_t first = uint64_t(w) * stride;
+  uint32_t added = 0;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < window;
+       i += gridDim.x * blockDim.x) {
+    const uint64_t e = first + i;
+    int a = 0;
+    while (a + 1 < seq.count && e >= seq.begin[a + 1]) ++a;
+    const uint32_t key = uint32_t(seq.p[a][e - seq.begin[a]]) + 1u;
+    uint32_t h = (key * 2654435761u) >> (32 - slots_log2);
+    for (;;) {  // load factor <= 1/2: a free slot or the key is always found
+      const uint32_t prev = atomicCAS(&table[h], 0u, key);
+      if (prev == 0u) {
+        ++added;
+        break;
+      }
+      if (prev == key) break;
+      h = (h + 1) & mask;
+    }
+  }
+  for (int d = 1; d < kWave; d <<= 1) added += __shfl_xor(added, d, kWave);
+  if (lane_id() == 0 && added) atomicAdd(&distinct[0], (unsigned long long)added);
+}
+
 unsigned grid_for(size_t n) {
   const size_t b = (n + kThreads - 1) / kThreads;
   return unsigned(b == 0 ? 1 : (b < 1048576 ? b : 1048576));
@@ -824,6 +882,70 @@ int ps_pre_gather_workset(int group_size, const uint32_t* perm, int groups,
   (void)hipFree(ws);
   if (rc != PS_OK) return rc;
   PS_HIP(e);
+  return PS_OK;
+}
+
+int ps_pre_exec_positions(int group_size, const uint32_t* perm, int groups,
+                          const int* exec_offset, const int* pub_offset, int* out_pos,
+                          ps_stream_t stream) {
+  PS_CHECK_ARG(perm && out_pos && groups >= 0 && group_size >= 0 &&
+                   (group_size > 0 || (exec_offset && pub_offset)),
+               "ps_pre_exec_positions: bad argument");
+  if (groups == 0) return PS_OK;
+  const unsigned waves_per_block = ps::kThreads / ps::kWave;
+  size_t blocks = (size_t(groups) + waves_per_block - 1) / waves_per_block;
+  if (blocks > 65536) blocks = 65536;
+  ps::exec_positions_kernel<<<unsigned(blocks), ps::kThreads, 0, ps::to_hip(stream)>>>(
+      group_size, perm, groups, exec_offset, pub_offset, out_pos);
+  PS_LAUNCHED();
+  return PS_OK;
+}
+
+int ps_pre_locality_score(int count, const int* const* col_ind, const long long* lengths,
+                          int window, int max_windows, double* score, ps_stream_t stream) {
+  PS_CHECK_ARG(count >= 1 && count <= PS_MAX_WORKSETS && col_ind && lengths && score &&
+                   window >= 64 && window <= (1 << 24) && max_windows >= 1 &&
+                   max_windows <= 65535,
+               "ps_pre_locality_score: bad argument");
+  ps::SeqTable seq{};
+  uint64_t total = 0;
+  int n = 0;
+  for (int a = 0; a < count; ++a) {
+    PS_CHECK_ARG(lengths[a] >= 0, "ps_pre_locality_score: negative length");
+    if (lengths[a] == 0) continue;
+    PS_CHECK_ARG(col_ind[a], "ps_pre_locality_score: null column array");
+    seq.p[n] = col_ind[a];
+    seq.begin[n] = total;
+    total += uint64_t(lengths[a]);
+    ++n;
+  }
+  seq.count = n;
+  seq.begin[n] = total;
+  *score = 0.0;
+  const uint64_t nwin = total / uint64_t(window);
+  if (nwin == 0) return PS_OK;  // shorter than one window: no evidence either way
+  const uint32_t windows = uint32_t(nwin < uint64_t(max_windows) ? nwin : uint64_t(max_windows));
+  const uint64_t stride = nwin / windows * uint64_t(window);
+  uint32_t slots_log2 = 1;
+  while ((1u << slots_log2) < 2u * uint32_t(window)) ++slots_log2;
+  const size_t table_words = size_t(windows) << slots_log2;
+  using S = ps::Scratch;
+  S ws(S::bytes(table_words, 4) + S::bytes(1, 8));
+  PS_HIP(ws.error());
+  uint32_t* tables = ws.take<uint32_t>(table_words);
+  unsigned long long* distinct = ws.take<unsigned long long>(1);
+  hipStream_t st = ps::to_hip(stream);
+  PS_HIP(hipMemsetAsync(tables, 0, table_words * 4, st));
+  PS_HIP(hipMemsetAsync(distinct, 0, 8, st));
+  unsigned gx = unsigned((uint32_t(window) + ps::kThreads - 1) / ps::kThreads);
+  if (gx > 64) gx = 64;
+  ps::window_distinct_kernel<<<dim3(gx, windows), ps::kThreads, 0, st>>>(
+      seq, stride, uint32_t(window), slots_log2, tables, distinct);
+  PS_LAUNCHED();
+  unsigned long long host = 0;
+  PS_HIP(hipMemcpyAsync(&host, distinct, 8, hipMemcpyDeviceToHost, st));
+  PS_HIP(hipStreamSynchronize(st));
+  *score = double(host) / (double(windows) * double(window));
   return PS_OK;
 }
 

@@ -17,10 +17,12 @@
 // outputs are stored, residue outputs are added atomically into out[0], the
 // output is in workset order.
 //
-// CSR-order variant (kCsr): each result goes to out_csr[csr_pos[s][p]], the
-// nonzero's position in the input CSR arrays, with a plain store (every CSR
-// position is written exactly once), so no output zeroing and no separate
-// permutation pass.
+// Scatter variant (kScatter): the result of stored nonzero p of workset s goes
+// to out[s][out_pos[s][p]]. Used (a) for CSR order (every out[s] is the one
+// CSR-order array, out_pos the CSR positions, plain stores: each position is
+// written once, no zeroing needed) and (b) to run a row-ordered execution copy
+// of the worksets while writing the public workset layout (out_pos = public
+// positions; residue results are still added atomically, as above).
 #include "ps_common.hpp"
 
 namespace ps {
@@ -41,8 +43,8 @@ struct SddmmArgs {
   const float* rhs;
   uint64_t lhs_bytes;
   uint64_t rhs_bytes;
-  const int* csr_pos[PS_MAX_WORKSETS];  // CSR-order variant only
-  float* csr_out;
+  const int* out_pos[PS_MAX_WORKSETS];  // scatter variant only
+  int32_t residue_add;                  // scatter variant: residue results added
 };
 
 // Transposing reduction over the 8 lanes of a slot: in p[j] each lane holds
@@ -100,7 +102,7 @@ __device__ __forceinline__ void slot_dots(const Rows<kBuf>& Y,
   }
 }
 
-template <int KQ, bool kBuf, bool kCsr>
+template <int KQ, bool kBuf, bool kScatter>
 __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs args) {
   constexpr int K = 32 * KQ;
   const uint32_t blk = balanced_block(blockIdx.x, gridDim.x);
@@ -111,8 +113,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
   while (i + 1 < args.count && task >= args.task_begin[i + 1]) ++i;
   const ps_workset ws = args.ws[i];
   float* __restrict__ out = args.out[i];
-  const int* __restrict__ csr_pos = args.csr_pos[i];
-  float* __restrict__ csr_out = args.csr_out;
+  const int* __restrict__ out_pos = args.out_pos[i];
   const int local = int(task - args.task_begin[i]);
 
   const int lane = lane_id();
@@ -145,7 +146,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     const float dot = slot_transpose_sum(p, sub);
     const int pos = local * 64 + lane;
     if (valid) {
-      if constexpr (kCsr) csr_out[csr_pos[pos]] = dot * ws.sp_data[pos];
+      if constexpr (kScatter) out[out_pos[pos]] = dot * ws.sp_data[pos];
       else out[pos] = dot * ws.sp_data[pos];
     }
   } else {
@@ -173,8 +174,13 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
       const float dot = slot_transpose_sum(p, sub);
       const int k = c0 + q;
       if (k < len) {
-        if constexpr (kCsr) csr_out[csr_pos[beg + k]] = dot * ws.sp_data[beg + k];
-        else unsafeAtomicAdd(out + beg + k, dot * ws.sp_data[beg + k]);
+        const float v = dot * ws.sp_data[beg + k];
+        if constexpr (kScatter) {
+          if (args.residue_add) unsafeAtomicAdd(out + out_pos[beg + k], v);
+          else out[out_pos[beg + k]] = v;
+        } else {
+          unsafeAtomicAdd(out + beg + k, v);
+        }
       }
     }
   }
@@ -189,9 +195,9 @@ __global__ void to_csr_kernel(const float* __restrict__ in, const int* __restric
 }
 
 template <int KQ>
-void launch_kq(const SddmmArgs& a, bool buf, unsigned grid, hipStream_t stream) {
+void launch_kq(const SddmmArgs& a, bool buf, bool scatter, unsigned grid, hipStream_t stream) {
   constexpr unsigned kBlock = kWave * kWavesPerBlock;
-  if (a.csr_out) {
+  if (scatter) {
     if (buf) sddmm_kernel<KQ, true, true><<<grid, kBlock, 0, stream>>>(a);
     else sddmm_kernel<KQ, false, true><<<grid, kBlock, 0, stream>>>(a);
   } else {
@@ -200,18 +206,18 @@ void launch_kq(const SddmmArgs& a, bool buf, unsigned grid, hipStream_t stream) 
   }
 }
 
-// outs[q] (workset order) or, when csr_out is set, csr_pos[q] + csr_out.
+// Workset q writes outs[q] at its own positions, or at out_pos[q][p] when
+// out_pos is given (residue results added when residue_add).
 int launch(int count, const int* order, const ps_workset* worksets, float* const* outs,
-           const int* const* csr_pos, float* csr_out, const int* residue_offset, int rows,
+           const int* const* out_pos, int residue_add, const int* residue_offset, int rows,
            int cols, int N, const float* lhs, const float* rhs, int rcap, hipStream_t stream) {
   PS_CHECK_ARG(N > 0 && N % 32 == 0 && N <= 512,
                "SDDMM requires N to be a multiple of 32 between 32 and 512");
   PS_CHECK_ARG(int64_t(rows) * N <= INT32_MAX && int64_t(cols) * N <= INT32_MAX,
                "Dense dimensions exceed the 32-bit kernel indexing range");
-  PS_CHECK_ARG(lhs && rhs && (csr_out ? csr_pos != nullptr : outs != nullptr),
-               "Invalid SDDMM buffers");
+  PS_CHECK_ARG(lhs && rhs && outs, "Invalid SDDMM buffers");
   SddmmArgs a{};
-  a.csr_out = csr_out;
+  a.residue_add = residue_add;
   a.N = N;
   a.rcap = rcap;
   a.lhs = lhs;
@@ -228,8 +234,8 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
   for (int q = 0; q < count; ++q) {
     const ps_workset& w = worksets[q];
     if (w.group_num <= 0) continue;
-    if (csr_out) PS_CHECK_ARG(csr_pos[q], "Missing CSR positions of an SDDMM workset");
-    else PS_CHECK_ARG(outs[q], "Missing SDDMM output workset");
+    PS_CHECK_ARG(outs[q], "Missing SDDMM output workset");
+    if (out_pos) PS_CHECK_ARG(out_pos[q], "Missing output positions of an SDDMM workset");
     PS_CHECK_ARG(w.col_ind && w.sp_data && w.group_des, "Invalid SDDMM workset buffers");
     const int s = order[q];
     uint64_t t;
@@ -243,8 +249,8 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
     }
     a.ws[n] = w;
     if (s == 0) a.ws[n].group_size = 0;
-    if (csr_out) a.csr_pos[n] = csr_pos[q];
-    else a.out[n] = outs[q];
+    a.out[n] = outs[q];
+    if (out_pos) a.out_pos[n] = out_pos[q];
     a.task_begin[n] = uint32_t(tasks);
     tasks += t;
     ++n;
@@ -256,22 +262,22 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
   a.total_tasks = uint32_t(tasks);
   const unsigned grid = unsigned((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
   switch (N / 32) {
-    case 1: launch_kq<1>(a, buf, grid, stream); break;
-    case 2: launch_kq<2>(a, buf, grid, stream); break;
-    case 3: launch_kq<3>(a, buf, grid, stream); break;
-    case 4: launch_kq<4>(a, buf, grid, stream); break;
-    case 5: launch_kq<5>(a, buf, grid, stream); break;
-    case 6: launch_kq<6>(a, buf, grid, stream); break;
-    case 7: launch_kq<7>(a, buf, grid, stream); break;
-    case 8: launch_kq<8>(a, buf, grid, stream); break;
-    case 9: launch_kq<9>(a, buf, grid, stream); break;
-    case 10: launch_kq<10>(a, buf, grid, stream); break;
-    case 11: launch_kq<11>(a, buf, grid, stream); break;
-    case 12: launch_kq<12>(a, buf, grid, stream); break;
-    case 13: launch_kq<13>(a, buf, grid, stream); break;
-    case 14: launch_kq<14>(a, buf, grid, stream); break;
-    case 15: launch_kq<15>(a, buf, grid, stream); break;
-    default: launch_kq<16>(a, buf, grid, stream); break;
+    case 1: launch_kq<1>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 2: launch_kq<2>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 3: launch_kq<3>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 4: launch_kq<4>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 5: launch_kq<5>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 6: launch_kq<6>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 7: launch_kq<7>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 8: launch_kq<8>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 9: launch_kq<9>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 10: launch_kq<10>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 11: launch_kq<11>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 12: launch_kq<12>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 13: launch_kq<13>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 14: launch_kq<14>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 15: launch_kq<15>(a, buf, out_pos != nullptr, grid, stream); break;
+    default: launch_kq<16>(a, buf, out_pos != nullptr, grid, stream); break;
   }
   PS_LAUNCHED();
   return PS_OK;
@@ -298,8 +304,30 @@ int ps_sddmm_launch(int workset_count, const ps_workset* worksets, const int* re
   // A single workset means fine mode (residue groups of at most 16 nonzeros,
   // utils/matrix_utils.cu:137-141); otherwise residue groups hold at most 31.
   const int rcap = workset_count == 1 ? 16 : 32;
-  return ps::launch(workset_count, order, ordered, outs, nullptr, nullptr, residue_offset, rows,
-                    cols, N, lhs, rhs, rcap, ps::to_hip(stream));
+  return ps::launch(workset_count, order, ordered, outs, nullptr, 0, residue_offset, rows, cols,
+                    N, lhs, rhs, rcap, ps::to_hip(stream));
+}
+
+int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
+                            const int* residue_offset, const int* const* out_pos, int rows,
+                            int cols, int N, const float* lhs, const float* rhs,
+                            float* const* out, ps_stream_t stream) {
+  PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets && out_pos &&
+                   out,
+               "Invalid SDDMM workset count");
+  int order[PS_MAX_WORKSETS];
+  ps_workset ordered[PS_MAX_WORKSETS];
+  const int* pos[PS_MAX_WORKSETS];
+  float* outs[PS_MAX_WORKSETS];
+  for (int q = 0; q < workset_count; ++q) {
+    order[q] = workset_count - 1 - q;
+    ordered[q] = worksets[workset_count - 1 - q];
+    pos[q] = out_pos[workset_count - 1 - q];
+    outs[q] = out[workset_count - 1 - q];
+  }
+  const int rcap = workset_count == 1 ? 16 : 32;
+  return ps::launch(workset_count, order, ordered, outs, pos, 1, residue_offset, rows, cols, N,
+                    lhs, rhs, rcap, ps::to_hip(stream));
 }
 
 int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
@@ -311,14 +339,16 @@ int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int
   int order[PS_MAX_WORKSETS];
   ps_workset ordered[PS_MAX_WORKSETS];
   const int* pos[PS_MAX_WORKSETS];
+  float* outs[PS_MAX_WORKSETS];
   for (int q = 0; q < workset_count; ++q) {
     order[q] = workset_count - 1 - q;
     ordered[q] = worksets[workset_count - 1 - q];
     pos[q] = csr_pos[workset_count - 1 - q];
+    outs[q] = out_csr;
   }
   const int rcap = workset_count == 1 ? 16 : 32;
-  return ps::launch(workset_count, order, ordered, nullptr, pos, out_csr, residue_offset, rows,
-                    cols, N, lhs, rhs, rcap, ps::to_hip(stream));
+  return ps::launch(workset_count, order, ordered, outs, pos, 0, residue_offset, rows, cols, N,
+                    lhs, rhs, rcap, ps::to_hip(stream));
 }
 
 int ps_workset_to_csr(int workset_count, const long long* lengths, const int* const* csr_pos,
@@ -344,8 +374,8 @@ int ps_sddmm_workset_launch(int s, const ps_workset* workset, const int* residue
                             int rows, int cols, int N, const float* lhs, const float* rhs,
                             float* out, ps_stream_t stream) {
   PS_CHECK_ARG(s >= 0 && s < PS_MAX_WORKSETS && workset, "Invalid SDDMM workset");
-  return ps::launch(1, &s, workset, &out, nullptr, nullptr, residue_offset, rows, cols, N, lhs,
-                    rhs, 32, ps::to_hip(stream));
+  return ps::launch(1, &s, workset, &out, nullptr, 0, residue_offset, rows, cols, N, lhs, rhs,
+                    32, ps::to_hip(stream));
 }
 
 }  // extern "C"

@@ -157,9 +157,12 @@ PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num
   if (policy.cu_count < 0) throw std::invalid_argument("PartitionPolicy::cu_count must be >= 0");
   if (int(policy.signature_order) < 0 || int(policy.signature_order) > 2)
     throw std::invalid_argument("PartitionPolicy::signature_order is not a SignatureOrder");
+  if (int(policy.task_order) < 0 || int(policy.task_order) > 2)
+    throw std::invalid_argument("PartitionPolicy::task_order is not a TaskOrder");
   _cu_count = policy.cu_count;
   _signature_order = policy.signature_order;
   _keep_csr_pos = policy.csr_positions;
+  _task_order = policy.task_order;
   if (_cu_count == 0) {
     int dev = 0;
     ThrowOnError(ps_get_device(&dev));
@@ -381,12 +384,145 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
                                        _workset_sp_data[s],
                                        _keep_csr_pos ? _workset_csr_pos[s] : nullptr, st));
   }
+
+  // Task order: the row-ordered execution copy, kept when asked for or when it
+  // scores clearly better than the signature order.
+  if (_task_order != TaskOrder::kSignature) {
+    size_t gmax = 0;
+    for (int s = 0; s < S; ++s) gmax = std::max(gmax, size_t(_group_num[s]));
+    DeviceArray<uint32_t> iota(gmax);
+    ThrowOnError(ps_iota_u32(iota.data(), int(gmax), st));
+    _exec_col_ind = new int*[S]();
+    _exec_sp_data = new float*[S]();
+    _exec_group_des = new int*[S]();
+    _exec_out_pos = new int*[S]();
+    if (_keep_csr_pos) _exec_csr_pos = new int*[S]();
+    // residue offsets in the initial (row) order
+    ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_residue_offset),
+                           sizeof(int) * (size_t(G0) + 1)));
+    ThrowOnError(ps_memset_async(_exec_residue_offset, 0, sizeof(int) * (size_t(G0) + 1), st));
+    if (G0 > 0) {
+      DeviceArray<uint32_t> len(static_cast<size_t>(G0) + 1);
+      ThrowOnError(ps_memcpy_dtod_async(len.data(), res_len.data(), sizeof(int) * size_t(G0), st));
+      ThrowOnError(ps_memset_async(len.data() + G0, 0, sizeof(uint32_t), st));
+      DeviceArray<char> ws(ps_scan_workspace_bytes(size_t(G0) + 1));
+      ThrowOnError(ps_exclusive_scan_u32(len.data(),
+                                         reinterpret_cast<uint32_t*>(_exec_residue_offset),
+                                         size_t(G0) + 1, ws.data(), st));
+      _exec_residue_atomic = reinterpret_cast<bool*>(res_atomic0.Release());
+    }
+    std::vector<long long> lengths(static_cast<size_t>(S), 0);
+    for (int s = 0; s < S; ++s) {
+      const int G = _group_num[s];
+      if (G == 0) continue;
+      _exec_group_des[s] = des0[size_t(s)].Release();
+      size_t size;
+      if (s == 0) {
+        int total = 0;
+        ThrowOnError(ps_memcpy_dtoh(&total, _residue_offset + G0, sizeof(int)));
+        size = size_t(total);
+      } else {
+        size = size_t(G) * size_t(GROUP_SIZE(s));
+      }
+      lengths[size_t(s)] = (long long)size;
+      ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_col_ind[s]), sizeof(int) * size));
+      ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_sp_data[s]), sizeof(float) * size));
+      if (_keep_csr_pos)
+        ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_csr_pos[s]), sizeof(int) * size));
+      ThrowOnError(ps_pre_gather_workset(s == 0 ? 0 : GROUP_SIZE(s), iota.data(), G,
+                                         start[size_t(s)].data(),
+                                         s == 0 ? _exec_residue_offset : nullptr, vals.data(),
+                                         d_ci.data(), d_sv.data(), _exec_col_ind[s],
+                                         _exec_sp_data[s],
+                                         _keep_csr_pos ? _exec_csr_pos[s] : nullptr, st));
+    }
+    bool keep = _task_order == TaskOrder::kRow;
+    if (_task_order == TaskOrder::kAuto) {
+      // Launch order of the worksets: largest groups first, the residue last.
+      std::vector<const int*> pub(static_cast<size_t>(S)), row(static_cast<size_t>(S));
+      std::vector<long long> len(static_cast<size_t>(S));
+      for (int q = 0; q < S; ++q) {
+        pub[size_t(q)] = _workset_col_ind[S - 1 - q];
+        row[size_t(q)] = _exec_col_ind[S - 1 - q];
+        len[size_t(q)] = lengths[size_t(S - 1 - q)];
+      }
+      ThrowOnError(ps_pre_locality_score(S, pub.data(), len.data(), kLocalityWindow,
+                                         kLocalityWindows, &_locality[0], st));
+      ThrowOnError(ps_pre_locality_score(S, row.data(), len.data(), kLocalityWindow,
+                                         kLocalityWindows, &_locality[1], st));
+      keep = _locality[1] < kRowOrderGain * _locality[0];
+    }
+    if (keep) {
+      _task_order = TaskOrder::kRow;
+      for (int s = 0; s < S; ++s) {
+        const int G = _group_num[s];
+        if (G == 0) continue;
+        ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_out_pos[s]),
+                               sizeof(int) * size_t(lengths[size_t(s)])));
+        ThrowOnError(ps_pre_exec_positions(s == 0 ? 0 : GROUP_SIZE(s), perm[size_t(s)].data(), G,
+                                           _exec_residue_offset, _residue_offset,
+                                           _exec_out_pos[s], st));
+      }
+    } else {
+      _task_order = TaskOrder::kSignature;
+      ThrowOnError(ps_device_synchronize());
+      ReleaseExecution();
+    }
+  }
   ThrowOnError(ps_device_synchronize());
   clock.Mark(&PreprocessTimings::gather_ms);
   clock.Finish();
 }
 
+ExecutionLayout PowerSparseMatrixGPU::Execution() const {
+  ExecutionLayout e;
+  if (_task_order == TaskOrder::kRow) {
+    e.col_ind = _exec_col_ind;
+    e.sp_data = _exec_sp_data;
+    e.group_des = _exec_group_des;
+    e.residue_offset = _exec_residue_offset;
+    e.residue_atomic = _exec_residue_atomic;
+    e.out_pos = _exec_out_pos;
+    e.csr_pos = _exec_csr_pos;
+  } else {
+    e.col_ind = _workset_col_ind;
+    e.sp_data = _workset_sp_data;
+    e.group_des = _group_des;
+    e.residue_offset = _residue_offset;
+    e.residue_atomic = _residue_atomic;
+    e.csr_pos = _workset_csr_pos;
+  }
+  return e;
+}
+
+PowerSparseMatrixGPU::~PowerSparseMatrixGPU() { Release(); }
+
+void PowerSparseMatrixGPU::ReleaseExecution() noexcept {
+  for (int s = 0; s < _group_type_num; ++s) {
+    if (_exec_col_ind) ps_free(_exec_col_ind[s]);
+    if (_exec_sp_data) ps_free(_exec_sp_data[s]);
+    if (_exec_group_des) ps_free(_exec_group_des[s]);
+    if (_exec_out_pos) ps_free(_exec_out_pos[s]);
+    if (_exec_csr_pos) ps_free(_exec_csr_pos[s]);
+  }
+  delete[] _exec_col_ind;
+  delete[] _exec_sp_data;
+  delete[] _exec_group_des;
+  delete[] _exec_out_pos;
+  delete[] _exec_csr_pos;
+  ps_free(_exec_residue_offset);
+  ps_free(_exec_residue_atomic);
+  _exec_col_ind = nullptr;
+  _exec_sp_data = nullptr;
+  _exec_group_des = nullptr;
+  _exec_out_pos = nullptr;
+  _exec_csr_pos = nullptr;
+  _exec_residue_offset = nullptr;
+  _exec_residue_atomic = nullptr;
+}
+
 void PowerSparseMatrixGPU::Release() noexcept {
+  ReleaseExecution();
   for (int s = 0; s < _group_type_num; ++s) {
     if (_workset_col_ind) ps_free(_workset_col_ind[s]);
     if (_workset_sp_data) ps_free(_workset_sp_data[s]);

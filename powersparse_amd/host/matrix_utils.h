@@ -36,6 +36,32 @@ enum GroupSort { GroupNoSort = 0, GroupDoSort = 1 };
 enum class SignatureOrder { kAuto = 0, kBitmapWords = 1, kBitLists = 2 };
 constexpr int kBitmapMaxWords = 128;
 
+// The order in which the operators run the groups (their results do not depend
+// on it, beyond the order of FP32 atomic additions). kSignature runs the public
+// worksets as laid out. kRow runs a row-ordered copy of them (the group
+// numbering before the signature sort; ~12 more bytes per nonzero of device
+// memory), which keeps rows with shared columns together when the row ids
+// carry the graph's locality, as in community graphs. kAuto builds the copy,
+// scores both orders by the distinct columns per window of nearby nonzeros
+// (ps_pre_locality_score) and keeps the copy only if its score is below
+// kRowOrderGain times the signature order's.
+enum class TaskOrder { kAuto = 0, kSignature = 1, kRow = 2 };
+constexpr double kRowOrderGain = 0.85;
+constexpr int kLocalityWindow = 65536, kLocalityWindows = 128;
+
+// The worksets as the operators run them: the public ones (out_pos == nullptr)
+// or the row-ordered copy, whose slot p of workset s belongs at out_pos[s][p]
+// of the public layout. csr_pos: CSR position per slot, or nullptr.
+struct ExecutionLayout {
+  const int* const* col_ind = nullptr;
+  const float* const* sp_data = nullptr;
+  const int* const* group_des = nullptr;
+  const int* residue_offset = nullptr;
+  const bool* residue_atomic = nullptr;
+  const int* const* out_pos = nullptr;
+  const int* const* csr_pos = nullptr;
+};
+
 // Partition settings. The reference hard-codes all of them except the CU
 // count, which it reads from the current device (utils/matrix_utils.cu:31-63);
 // cu_count == 0 means "the current device's multiProcessorCount".
@@ -45,6 +71,7 @@ struct PartitionPolicy {
   // Keep, for every stored nonzero, its position in the input CSR arrays
   // (4 bytes per nonzero on the device): needed by SDDMMToCSR / WorksetToCSR.
   bool csr_positions = false;
+  TaskOrder task_order = TaskOrder::kAuto;
 };
 
 // Wall-clock milliseconds of the preprocessing stages (host timer, the stream
@@ -63,7 +90,7 @@ class PowerSparseMatrixGPU {
   PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num, const int* row_ptr,
                        const int* col_ind, const float* sp_data, const PartitionPolicy& policy,
                        PreprocessTimings* timings = nullptr);
-  ~PowerSparseMatrixGPU() { Release(); }
+  ~PowerSparseMatrixGPU();
   PowerSparseMatrixGPU(const PowerSparseMatrixGPU&) = delete;
   PowerSparseMatrixGPU& operator=(const PowerSparseMatrixGPU&) = delete;
   PowerSparseMatrixGPU(PowerSparseMatrixGPU&&) = delete;
@@ -90,11 +117,20 @@ class PowerSparseMatrixGPU {
   // Position in the input CSR arrays of every stored nonzero, per workset
   // (same layout as WorksetColInd); nullptr unless the policy asked for it.
   const int* const* WorksetCSRPosition() const { return _workset_csr_pos; }
+  // The task order the build chose (never kAuto) and the locality scores it
+  // compared (signature order, row order; 0 when not computed).
+  TaskOrder TaskOrderUsed() const { return _task_order; }
+  double LocalityScore(TaskOrder order) const {
+    return order == TaskOrder::kRow ? _locality[1] : _locality[0];
+  }
+  // What the operators launch on.
+  ExecutionLayout Execution() const;
 
  private:
   void Build(const int* row_ptr, const int* col_ind, const float* sp_data,
              PreprocessTimings* timings);
   void Release() noexcept;
+  void ReleaseExecution() noexcept;
 
   int _matrix_row, _matrix_col, _matrix_nnz;
   int _group_type_num = 0, _group_fine_size = 16;
@@ -108,6 +144,16 @@ class PowerSparseMatrixGPU {
   int** _group_des = nullptr;
   int** _workset_csr_pos = nullptr;
   int* _residue_offset = nullptr;
+  TaskOrder _task_order = TaskOrder::kAuto;
+  double _locality[2] = {0.0, 0.0};
+  // row-ordered execution copy (TaskOrder::kRow)
+  int** _exec_col_ind = nullptr;
+  float** _exec_sp_data = nullptr;
+  int** _exec_group_des = nullptr;
+  int** _exec_out_pos = nullptr;
+  int** _exec_csr_pos = nullptr;
+  int* _exec_residue_offset = nullptr;
+  bool* _exec_residue_atomic = nullptr;
   bool* _residue_atomic = nullptr;
 };
 

@@ -16,12 +16,13 @@
 namespace PowerSparse {
 namespace {
 
-std::vector<ps_workset> Worksets(const PowerSparseMatrixGPU& m) {
+// The worksets the kernels run: the public ones or the row-ordered copy.
+std::vector<ps_workset> Worksets(const PowerSparseMatrixGPU& m, const ExecutionLayout& e) {
   std::vector<ps_workset> ws(static_cast<size_t>(m.GroupTypeNum()));
   for (int s = 0; s < m.GroupTypeNum(); ++s) {
-    ws[size_t(s)].col_ind = m.WorksetColInd()[s];
-    ws[size_t(s)].sp_data = m.WorksetSpData()[s];
-    ws[size_t(s)].group_des = m.GroupDestination()[s];
+    ws[size_t(s)].col_ind = e.col_ind[s];
+    ws[size_t(s)].sp_data = e.sp_data[s];
+    ws[size_t(s)].group_des = e.group_des[s];
     ws[size_t(s)].group_num = m.GroupNum()[s];
     ws[size_t(s)].group_size = s == 0 ? 0 : GROUP_SIZE(s);
   }
@@ -49,10 +50,11 @@ void CheckSddmmArgs(const PowerSparseMatrixGPU& m, int N, const float* lhs, cons
 void SpMMAsync(const PowerSparseMatrixGPU& m, int N, const float* B, float* C,
                ps_stream_t stream) {
   CheckSpmmArgs(m, N, B, C);
-  const auto ws = Worksets(m);
-  ThrowOnError(ps_spmm_launch(m.GroupTypeNum(), ws.data(), m.ResidueOffset(),
-                              reinterpret_cast<const uint8_t*>(m.ResidueAtomic()),
-                              m.MatrixRow(), m.MatrixCol(), N, B, C, stream));
+  const ExecutionLayout e = m.Execution();
+  const auto ws = Worksets(m, e);
+  ThrowOnError(ps_spmm_launch(m.GroupTypeNum(), ws.data(), e.residue_offset,
+                              reinterpret_cast<const uint8_t*>(e.residue_atomic), m.MatrixRow(),
+                              m.MatrixCol(), N, B, C, stream));
 }
 
 void SpMM(const PowerSparseMatrixGPU& m, int N, const float* B, float* C, int stream_count,
@@ -69,9 +71,15 @@ void SDDMMAsync(const PowerSparseMatrixGPU& m, int N, const float* lhs, const fl
   CheckSddmmArgs(m, N, lhs, rhs, out);
   for (int s = 0; s < m.GroupTypeNum(); ++s)
     if (m.GroupNum()[s] != 0 && !out[s]) throw std::invalid_argument("Missing SDDMM output workset");
-  const auto ws = Worksets(m);
-  ThrowOnError(ps_sddmm_launch(m.GroupTypeNum(), ws.data(), m.ResidueOffset(), m.MatrixRow(),
-                               m.MatrixCol(), N, lhs, rhs, out, stream));
+  const ExecutionLayout e = m.Execution();
+  const auto ws = Worksets(m, e);
+  if (e.out_pos)  // row-ordered copy: results scattered to the public layout
+    ThrowOnError(ps_sddmm_scatter_launch(m.GroupTypeNum(), ws.data(), e.residue_offset,
+                                         e.out_pos, m.MatrixRow(), m.MatrixCol(), N, lhs, rhs,
+                                         out, stream));
+  else
+    ThrowOnError(ps_sddmm_launch(m.GroupTypeNum(), ws.data(), e.residue_offset, m.MatrixRow(),
+                                 m.MatrixCol(), N, lhs, rhs, out, stream));
 }
 
 void SDDMMToCSR(const PowerSparseMatrixGPU& m, int N, const float* lhs, const float* rhs,
@@ -80,10 +88,10 @@ void SDDMMToCSR(const PowerSparseMatrixGPU& m, int N, const float* lhs, const fl
   if (!m.WorksetCSRPosition())
     throw std::invalid_argument(
         "SDDMMToCSR needs a matrix built with PartitionPolicy::csr_positions");
-  const auto ws = Worksets(m);
-  ThrowOnError(ps_sddmm_csr_launch(m.GroupTypeNum(), ws.data(), m.ResidueOffset(),
-                                   m.WorksetCSRPosition(), m.MatrixRow(), m.MatrixCol(), N, lhs,
-                                   rhs, out_csr, stream));
+  const ExecutionLayout e = m.Execution();
+  const auto ws = Worksets(m, e);
+  ThrowOnError(ps_sddmm_csr_launch(m.GroupTypeNum(), ws.data(), e.residue_offset, e.csr_pos,
+                                   m.MatrixRow(), m.MatrixCol(), N, lhs, rhs, out_csr, stream));
 }
 
 void WorksetToCSR(const PowerSparseMatrixGPU& m, const float* const* values, float* out_csr,
