@@ -157,3 +157,49 @@ def test_full_size_properties(cfg):
     _, M1 = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, N, np.abs(B1) + np.abs(B2),
                         with_mag=True)
     tolerance.check(Cab, Ca.astype(np.float64) + Cb, M1, f"{cfg} SpMM linearity")
+
+
+def test_operands_over_4gib():
+    # B / Y of cols x 512 floats = 4.3 GB: beyond 32-bit buffer offsets, so the
+    # kernels take their 64-bit global-load path. Only three clusters of
+    # columns (start, middle, end of the range) are used and uploaded.
+    setup()
+    from powersparse_amd import _native
+    N = 512
+    cols = (1 << 21) + 4096
+    assert cols * N * 4 > (1 << 32) and cols * N <= 2**31 - 1
+    rng = np.random.default_rng(9)
+    starts = [0, 1 << 20, cols - 1024]
+    pool = np.concatenate([np.arange(s0, s0 + 1024) for s0 in starts])
+    rows = 500
+    deg = rng.integers(0, 300, rows)
+    deg[:40] = 64  # enough 64-nonzero blocks to make block worksets at cu_count 1
+    ci = [np.sort(rng.choice(pool, d, replace=False)) for d in deg]
+    rp = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    ci = np.concatenate(ci).astype(np.int32)
+    csr = ps.HostCsr(rows, cols, rp, ci, rng.uniform(0, 1, ci.size).astype(np.float32))
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=1, csr_positions=True)
+    say(f"4 GiB operands: S={m.GroupTypeNum()} groups={m.GroupNum()} nnz={csr.nnz}")
+    assert m.GroupTypeNum() >= 2
+    compact = rng.uniform(-1, 1, (3 * 1024, N)).astype(np.float32)
+    big = ps.DeviceBuffer(cols * N * 4)
+    for k, s0 in enumerate(starts):
+        block = np.ascontiguousarray(compact[k * 1024:(k + 1) * 1024])
+        ps._hip_call(_native.hip().ps_memcpy_htod(big.ptr + s0 * N * 4, block.ctypes.data,
+                                                   block.nbytes))
+    remap = np.empty(cols, np.int32)
+    for k, s0 in enumerate(starts):
+        remap[s0:s0 + 1024] = np.arange(k * 1024, (k + 1) * 1024)
+    cc = remap[csr.col_ind]
+    C = ps.DeviceBuffer.zeros(rows * N * 4)
+    ps.SpMMAsync(m, N, big, C)
+    ps.synchronize()
+    E, M = oracle.spmm(csr.row_ptr, cc, csr.values, N, compact, with_mag=True)
+    say("  ", tolerance.check(C.download(np.float32).reshape(rows, N), E, M, "SpMM > 4 GiB"))
+    X = rng.normal(size=(rows, N)).astype(np.float32)
+    out = ps.DeviceBuffer(csr.nnz * 4)
+    ps.SDDMMToCSR(m, N, ps.DeviceBuffer(host=X), big, out)
+    ps.synchronize()
+    E, M = oracle.sddmm(np.arange(rows, dtype=np.int32), csr.row_ptr, cc, csr.values, N, X,
+                        compact, with_mag=True)
+    say("  ", tolerance.check(out.download(np.float32, csr.nnz), E, M, "SDDMM > 4 GiB"))
