@@ -40,7 +40,7 @@ def short_name(name):
 
 def kernel_op(name):
     """(op, lanes-template) of an operator kernel name, else None."""
-    m = re.search(r"(spmm|sddmm)_kernel<(\d+), (true|false)>", short_name(name))
+    m = re.search(r"(spmm|sddmm)_kernel<(\d+), (true|false)(, (true|false))?>", short_name(name))
     return (m.group(1), int(m.group(2))) if m else None
 
 
