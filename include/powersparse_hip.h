@@ -308,9 +308,11 @@ int ps_pre_signature_lists(const int* row_ptr, int rows, int group_type_num, int
 
 /* perm[s][k] = the group of workset s at position k of the stable descending
  * signature order, from the lists of ps_pre_signature_lists: the same order as
- * the per-word stable sorts, found by refining ties a few list elements at a
- * time (cost follows the tied prefixes, not the signature length). Synchronises
- * the stream.
+ * the per-word stable sorts. Ties are refined in rounds: each class of tied
+ * groups is sorted by where and which way each member's list departs from
+ * the class's first member, so nested prefixes separate in one round (cost
+ * follows the branching of the tied lists, not the signature length).
+ * Synchronises the stream.
  * Replaces: the stable_sort loop over signature words (matrix_utils.cu:588-593)
  * with CompareDescending (:394-401). */
 int ps_pre_signature_order(const uint32_t* lists, const uint32_t* list_begin,

@@ -178,7 +178,7 @@ __global__ void signatures_kernel(const int* __restrict__ row_ptr, int rows, int
   }
 }
 
-// ---- signature order from sorted bit lists (long signatures) ----
+// ---- signature order from sorted bit lists ----
 //
 // The stable per-word sort orders groups by their signature read as one
 // big-endian bit string (bit b of the string is bit 31 - b % 32 of word b / 32),
@@ -241,36 +241,106 @@ __global__ void entry_lists_kernel(const uint64_t* __restrict__ e, uint32_t n, i
   }
 }
 
-// Refinement state: the active groups (still tied with another group) in
-// class order, each with its class base = final position of the class's first
-// member. Initially every group is active and the classes are the worksets.
+// Refinement. The active groups (still tied with another group of their
+// class) are kept in class order, each with its class base (final position
+// of the class's first member) and class depth (all members have equal lists
+// before it). Initially every group is active, the classes are the worksets
+// and the depth is 0. Each round compares every member with its class's first
+// member r (the reference) from the class depth on: the first position where
+// they differ, `lcp`, and which way the member goes:
+//   EQ     identical list to r;
+//   BEFORE the member's element at lcp is smaller than r's, or r's list ends;
+//   AFTER  the member's list ends at lcp, or its element is larger.
+// Sorting each class by (side, lcp ascending for BEFORE / descending for
+// AFTER, element at lcp, list end last) puts it in final order except within
+// runs of equal keys, which become the next round's classes with depth
+// lcp + 1 (their lists agree up to and including lcp). EQ runs, runs whose
+// lists ended, and single members are placed. Every class loses at least its
+// reference each round, and in practice a whole nest of prefix-related lists
+// separates in one round.
+constexpr uint32_t kBefore = 0, kEq = 1, kAfter = 2;
+
 __global__ void order_init_kernel(uint32_t n, GroupBase gb, uint32_t* __restrict__ act_group,
-                                  uint32_t* __restrict__ act_base) {
+                                  uint32_t* __restrict__ act_base,
+                                  uint32_t* __restrict__ act_depth) {
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
     act_group[i] = i;
     act_base[i] = gb.base[workset_of(gb, i)];
+    act_depth[i] = 0;
   }
 }
 
-// key = class base, then list elements depth .. depth + per_key - 1 of the
-// group (`end` past the list's end), each in elem_bits bits.
-__global__ void order_keys_kernel(const uint32_t* __restrict__ act_group,
-                                  const uint32_t* __restrict__ act_base, uint32_t n,
-                                  const uint32_t* __restrict__ lists,
-                                  const uint32_t* __restrict__ list_begin, uint32_t depth,
-                                  int per_key, int elem_bits, uint32_t end,
-                                  uint64_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+// Longest list (bounds the divergence depth).
+__global__ void max_list_kernel(const uint32_t* __restrict__ list_begin, uint32_t groups,
+                                uint32_t* __restrict__ out) {
+  uint32_t m = 0;
+  for (uint32_t g = blockIdx.x * blockDim.x + threadIdx.x; g < groups;
+       g += gridDim.x * blockDim.x)
+    m = max(m, list_begin[g + 1] - list_begin[g]);
+  for (int d = 1; d < kWave; d <<= 1) m = max(m, uint32_t(__shfl_xor(int(m), d, kWave)));
+  if (lane_id() == 0) atomicMax(out, m);
+}
+
+// head[i] = 1 where a class starts.
+__global__ void order_class_heads_kernel(const uint32_t* __restrict__ act_base, uint32_t n,
+                                         uint32_t* __restrict__ head) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    head[i] = (i == 0 || act_base[i] != act_base[i - 1]) ? 1u : 0u;
+}
+
+// head_at[c] = index of class c's first member (its reference).
+__global__ void order_class_start_kernel(uint32_t n, const uint32_t* __restrict__ head,
+                                         const uint32_t* __restrict__ rank,
+                                         uint32_t* __restrict__ head_at) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    if (head[i]) head_at[rank[i]] = i;
+}
+
+// Sort keys of every active member: hi = class * 3 + side; lo = divergence
+// key * (end + 1) + element (end for a list that ended). lcp[i] = divergence
+// position; idx[i] = i.
+__global__ void order_diverge_kernel(const uint32_t* __restrict__ act_group,
+                                     const uint32_t* __restrict__ act_depth, uint32_t n,
+                                     const uint32_t* __restrict__ lists,
+                                     const uint32_t* __restrict__ list_begin,
+                                     const uint32_t* __restrict__ head,
+                                     const uint32_t* __restrict__ rank,
+                                     const uint32_t* __restrict__ head_at, uint32_t end,
+                                     uint32_t max_len, uint64_t* __restrict__ hi,
+                                     uint64_t* __restrict__ lo, uint32_t* __restrict__ lcp_out,
+                                     uint32_t* __restrict__ idx) {
   for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const uint32_t c = rank[i] + head[i] - 1;
     const uint32_t g = act_group[i];
-    const uint32_t b = list_begin[g];
-    const uint32_t len = list_begin[g + 1] - b;
-    uint64_t key = act_base[i];
-    for (int j = 0; j < per_key; ++j) {
-      const uint32_t d = depth + uint32_t(j);
-      key = (key << elem_bits) | (d < len ? lists[b + d] : end);
+    const uint32_t r = act_group[head_at[c]];
+    const uint32_t* m = lists + list_begin[g];
+    const uint32_t* q = lists + list_begin[r];
+    const uint32_t nm = list_begin[g + 1] - list_begin[g];
+    const uint32_t nq = list_begin[r + 1] - list_begin[r];
+    uint32_t d = act_depth[i];
+    if (g != r)
+      while (d < nm && d < nq && m[d] == q[d]) ++d;
+    uint32_t side, key = 0, elem = 0;
+    if (g == r || (d == nm && d == nq)) {
+      side = kEq;
+      d = nm;
+    } else if (d == nm) {
+      side = kAfter;
+      key = max_len - d;
+      elem = end;
+    } else if (d == nq || m[d] < q[d]) {
+      side = kBefore;
+      key = d;
+      elem = m[d];
+    } else {
+      side = kAfter;
+      key = max_len - d;
+      elem = m[d];
     }
-    keys[i] = key;
-    vals[i] = g;
+    hi[i] = uint64_t(c) * 3u + side;
+    lo[i] = uint64_t(key) * (uint64_t(end) + 1u) + elem;
+    lcp_out[i] = d;
+    idx[i] = i;
   }
 }
 
@@ -292,15 +362,37 @@ __global__ void key_span_kernel(const uint64_t* __restrict__ keys, uint32_t n,
   }
 }
 
-// Over the sorted keys: new_head[i] = 1 where key i starts a run of equal keys,
-// old_head[i] = 1 where its class base (key >> elem_shift) starts a run.
-__global__ void order_flags_kernel(const uint64_t* __restrict__ keys, uint32_t n, int elem_shift,
-                                   uint32_t* __restrict__ new_head,
-                                   uint32_t* __restrict__ old_head) {
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-    const bool first = i == 0;
-    new_head[i] = (first || keys[i] != keys[i - 1]) ? 1u : 0u;
-    old_head[i] = (first || (keys[i] >> elem_shift) != (keys[i - 1] >> elem_shift)) ? 1u : 0u;
+// Combined key when both parts fit: hi << lo_bits | lo.
+__global__ void order_combine_kernel(uint32_t n, const uint64_t* __restrict__ hi,
+                                     const uint64_t* __restrict__ lo, int lo_bits,
+                                     uint64_t* __restrict__ key) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    key[i] = (hi[i] << lo_bits) | lo[i];
+}
+
+// key[j] = part[src[j]] (the second key of a two-pass sort, in first-pass order).
+__global__ void order_permute_key_kernel(uint32_t n, const uint32_t* __restrict__ src,
+                                         const uint64_t* __restrict__ part,
+                                         uint64_t* __restrict__ key) {
+  for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < n; j += gridDim.x * blockDim.x)
+    key[j] = part[src[j]];
+}
+
+// After the sort: new_head / old_head flag the starts of runs of equal keys and
+// of classes; the members' group, base and lcp follow their sorted positions.
+__global__ void order_runs_kernel(uint32_t n, const uint32_t* __restrict__ src,
+                                  const uint64_t* __restrict__ hi, const uint64_t* __restrict__ lo,
+                                  uint32_t* __restrict__ new_head, uint32_t* __restrict__ old_head) {
+  for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < n; j += gridDim.x * blockDim.x) {
+    const uint32_t i = src[j];
+    if (j == 0) {
+      new_head[j] = 1u;
+      old_head[j] = 1u;
+      continue;
+    }
+    const uint32_t p = src[j - 1];
+    new_head[j] = (hi[i] != hi[p] || lo[i] != lo[p]) ? 1u : 0u;
+    old_head[j] = (hi[i] / 3u != hi[p] / 3u) ? 1u : 0u;
   }
 }
 
@@ -317,14 +409,15 @@ __global__ void order_heads_kernel(uint32_t n, const uint32_t* __restrict__ new_
   }
 }
 
-// A run of equal keys inside a class is the new class; its base = the old base
-// + the run's offset inside the class. A group is placed when its new class
-// has one member, or when the key's last element is past the list's end (the
-// members' lists are then identical and group order decides). keep[i] = 1 for
-// groups that stay tied; next_base[i] = their new class base.
-__global__ void order_resolve_kernel(const uint64_t* __restrict__ keys,
-                                     const uint32_t* __restrict__ groups, uint32_t n,
-                                     int elem_shift, int elem_bits, uint32_t end,
+// A run's base = its class base + the run's offset inside the class. Placed
+// members write the permutation; the others (keep = 1) carry their new class
+// base and depth lcp + 1.
+__global__ void order_resolve_kernel(uint32_t n, const uint32_t* __restrict__ src,
+                                     const uint64_t* __restrict__ hi,
+                                     const uint64_t* __restrict__ lo, uint32_t end,
+                                     const uint32_t* __restrict__ act_group,
+                                     const uint32_t* __restrict__ act_base,
+                                     const uint32_t* __restrict__ lcp,
                                      const uint32_t* __restrict__ new_head,
                                      const uint32_t* __restrict__ new_rank,
                                      const uint32_t* __restrict__ old_head,
@@ -332,35 +425,43 @@ __global__ void order_resolve_kernel(const uint64_t* __restrict__ keys,
                                      const uint32_t* __restrict__ new_at,
                                      const uint32_t* __restrict__ old_at, GroupBase gb,
                                      SigTable perm, uint32_t* __restrict__ keep,
-                                     uint32_t* __restrict__ next_base) {
-  const uint64_t elem_mask = (uint64_t(1) << elem_bits) - 1;
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-    const uint64_t key = keys[i];
-    const uint32_t hn = new_at[new_rank[i] + new_head[i] - 1];
-    const uint32_t ho = old_at[old_rank[i] + old_head[i] - 1];
-    const uint32_t base = uint32_t(key >> elem_shift) + (hn - ho);
-    const bool single = new_head[i] && (i + 1 == n || new_head[i + 1]);
-    const bool done = single || uint32_t(key & elem_mask) == end;
-    if (done) {
-      const uint32_t g = groups[i];
+                                     uint32_t* __restrict__ next_group,
+                                     uint32_t* __restrict__ next_base,
+                                     uint32_t* __restrict__ next_depth) {
+  for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < n; j += gridDim.x * blockDim.x) {
+    const uint32_t i = src[j];
+    const uint32_t hn = new_at[new_rank[j] + new_head[j] - 1];
+    const uint32_t ho = old_at[old_rank[j] + old_head[j] - 1];
+    const uint32_t base = act_base[i] + (hn - ho);
+    const bool single = new_head[j] && (j + 1 == n || new_head[j + 1]);
+    const bool ended = uint32_t(hi[i] % 3u) == kEq || lo[i] % (uint64_t(end) + 1u) == end;
+    const uint32_t g = act_group[i];
+    if (single || ended) {
       const int s = workset_of(gb, g);
-      perm.p[s][base + (i - hn) - gb.base[s]] = g - gb.base[s];
+      perm.p[s][base + (j - hn) - gb.base[s]] = g - gb.base[s];
+      keep[j] = 0u;
+    } else {
+      keep[j] = 1u;
     }
-    keep[i] = done ? 0u : 1u;
-    next_base[i] = base;
+    next_group[j] = g;
+    next_base[j] = base;
+    next_depth[j] = lcp[i] + 1u;
   }
 }
 
 __global__ void order_compact_kernel(uint32_t n, const uint32_t* __restrict__ keep,
                                      const uint32_t* __restrict__ slot,
-                                     const uint32_t* __restrict__ groups,
+                                     const uint32_t* __restrict__ next_group,
                                      const uint32_t* __restrict__ next_base,
+                                     const uint32_t* __restrict__ next_depth,
                                      uint32_t* __restrict__ act_group,
-                                     uint32_t* __restrict__ act_base) {
-  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-    if (keep[i]) {
-      act_group[slot[i]] = groups[i];
-      act_base[slot[i]] = next_base[i];
+                                     uint32_t* __restrict__ act_base,
+                                     uint32_t* __restrict__ act_depth) {
+  for (uint32_t j = blockIdx.x * blockDim.x + threadIdx.x; j < n; j += gridDim.x * blockDim.x) {
+    if (keep[j]) {
+      act_group[slot[j]] = next_group[j];
+      act_base[slot[j]] = next_base[j];
+      act_depth[slot[j]] = next_depth[j];
     }
   }
 }
@@ -1003,6 +1104,46 @@ int ps_pre_signature_lists(const int* row_ptr, int rows, int group_type_num, int
   return PS_OK;
 }
 
+}  // extern "C"
+
+namespace ps {
+namespace {
+
+// Stable radix sort of (key, index) pairs over the bits where the keys differ
+// (found by an OR/AND reduction); *k / *v point at the sorted data.
+int sort_varying(uint64_t* keys, uint64_t* keys_alt, uint32_t* vals, uint32_t* vals_alt,
+                 uint32_t n, unsigned long long* span, void* radix_ws, hipStream_t st,
+                 const uint64_t** k, const uint32_t** v) {
+  static const unsigned long long span_init[2] = {0ull, ~0ull};
+  unsigned long long host_span[2] = {0ull, 0ull};
+  *k = keys;
+  *v = vals;
+  PS_HIP(hipMemcpyAsync(span, span_init, sizeof(span_init), hipMemcpyHostToDevice, st));
+  const unsigned grid = grid_for(n);
+  key_span_kernel<<<grid < 1024 ? grid : 1024, kThreads, 0, st>>>(keys, n, span);
+  PS_LAUNCHED();
+  PS_HIP(hipMemcpyAsync(host_span, span, sizeof(host_span), hipMemcpyDeviceToHost, st));
+  PS_HIP(hipStreamSynchronize(st));
+  const uint64_t diff = host_span[0] ^ host_span[1];
+  if (diff == 0) return PS_OK;
+  const int lo = __builtin_ctzll(diff) / 8 * 8;
+  const int hi = 64 - __builtin_clzll(diff);
+  int alt = 0;
+  const int rc = ps_radix_sort_pairs_u64(keys, keys_alt, vals, vals_alt, n, lo, hi, radix_ws,
+                                         &alt, reinterpret_cast<ps_stream_t>(st));
+  if (rc != PS_OK) return rc;
+  if (alt) {
+    *k = keys_alt;
+    *v = vals_alt;
+  }
+  return PS_OK;
+}
+
+}  // namespace
+}  // namespace ps
+
+extern "C" {
+
 int ps_pre_signature_order(const uint32_t* lists, const uint32_t* list_begin,
                            int group_type_num, const int* group_num, int signature_len,
                            uint32_t* const* perm, ps_stream_t stream) {
@@ -1020,24 +1161,28 @@ int ps_pre_signature_order(const uint32_t* lists, const uint32_t* list_begin,
   }
   const uint32_t total = gb.base[group_type_num];
   if (total == 0) return PS_OK;
-  // Elements take values 0 .. signature_len - 1; signature_len marks a list's end.
+  // List elements take values 0 .. signature_len - 1; signature_len marks a list's end.
   const uint32_t end = uint32_t(signature_len);
-  const int elem_bits = ps::bits_for(end);
-  const int base_bits = ps::bits_for(uint64_t(total - 1));
-  const int per_key = (64 - base_bits) / elem_bits;
-  PS_CHECK_ARG(per_key >= 1, "ps_pre_signature_order: key overflow");
-  const int elem_shift = per_key * elem_bits;
   const size_t n0 = total;
   using S = ps::Scratch;
-  S ws(2 * S::bytes(n0, 8) + 13 * S::bytes(n0, 4) + S::bytes(2, 8) +
+  S ws(6 * S::bytes(n0, 8) + 17 * S::bytes(n0, 4) + S::bytes(2, 8) + S::bytes(1, 4) +
        ps_radix_workspace_bytes(n0) + ps_scan_workspace_bytes(n0));
   PS_HIP(ws.error());
+  uint64_t* hi = ws.take<uint64_t>(n0);
+  uint64_t* lo = ws.take<uint64_t>(n0);
   uint64_t* keys = ws.take<uint64_t>(n0);
   uint64_t* keys_alt = ws.take<uint64_t>(n0);
+  uint64_t* keys2 = ws.take<uint64_t>(n0);
+  uint64_t* keys2_alt = ws.take<uint64_t>(n0);
   uint32_t* act_group = ws.take<uint32_t>(n0);
   uint32_t* act_base = ws.take<uint32_t>(n0);
-  uint32_t* vals = ws.take<uint32_t>(n0);
-  uint32_t* vals_alt = ws.take<uint32_t>(n0);
+  uint32_t* act_depth = ws.take<uint32_t>(n0);
+  uint32_t* head = ws.take<uint32_t>(n0);
+  uint32_t* rank = ws.take<uint32_t>(n0);
+  uint32_t* head_at = ws.take<uint32_t>(n0);
+  uint32_t* lcp = ws.take<uint32_t>(n0);
+  uint32_t* idx = ws.take<uint32_t>(n0);
+  uint32_t* idx_alt = ws.take<uint32_t>(n0);
   uint32_t* new_head = ws.take<uint32_t>(n0);
   uint32_t* old_head = ws.take<uint32_t>(n0);
   uint32_t* new_rank = ws.take<uint32_t>(n0);
@@ -1046,66 +1191,85 @@ int ps_pre_signature_order(const uint32_t* lists, const uint32_t* list_begin,
   uint32_t* old_at = ws.take<uint32_t>(n0);
   uint32_t* keep = ws.take<uint32_t>(n0);
   uint32_t* slot = ws.take<uint32_t>(n0);
-  uint32_t* next_base = ws.take<uint32_t>(n0);
   unsigned long long* span = ws.take<unsigned long long>(2);
+  uint32_t* max_len_dev = ws.take<uint32_t>(1);
   void* radix_ws = ws.take<char>(ps_radix_workspace_bytes(n0));
   void* scan_ws = ws.take<char>(ps_scan_workspace_bytes(n0));
+  // next_group / next_base / next_depth reuse buffers free after the sort
+  uint32_t* next_group = head;
+  uint32_t* next_base = head_at;
+  uint32_t* next_depth = rank;
   hipStream_t st = ps::to_hip(stream);
 
-  uint32_t entries = 0;  // longest possible list: bounds the refinement depth
-  PS_HIP(hipMemcpyAsync(&entries, list_begin + total, sizeof(uint32_t), hipMemcpyDeviceToHost,
-                        st));
+  uint32_t max_len = 0;
+  PS_HIP(hipMemsetAsync(max_len_dev, 0, 4, st));
+  {
+    unsigned gx = ps::grid_for(n0);
+    ps::max_list_kernel<<<gx < 1024 ? gx : 1024, ps::kThreads, 0, st>>>(list_begin, total,
+                                                                        max_len_dev);
+    PS_LAUNCHED();
+  }
+  PS_HIP(hipMemcpyAsync(&max_len, max_len_dev, 4, hipMemcpyDeviceToHost, st));
   ps::order_init_kernel<<<ps::grid_for(n0), ps::kThreads, 0, st>>>(total, gb, act_group,
-                                                                   act_base);
+                                                                   act_base, act_depth);
   PS_LAUNCHED();
   PS_HIP(hipStreamSynchronize(st));
+  const int lo_bits = ps::bits_for(uint64_t(max_len) * (uint64_t(end) + 1u) + end);
   uint32_t n = total;
-  for (uint64_t depth = 0; n > 0; depth += uint64_t(per_key)) {
-    if (depth > uint64_t(entries) + uint64_t(per_key))
+  // Every round places at least each class's reference, so a class of k
+  // groups needs at most k rounds.
+  for (uint32_t round = 0; n > 0; ++round) {
+    if (round > total)
       return ps::fail(PS_ERR_RUNTIME, "ps_pre_signature_order: refinement did not converge");
     const unsigned grid = ps::grid_for(n);
-    ps::order_keys_kernel<<<grid, ps::kThreads, 0, st>>>(act_group, act_base, n, lists,
-                                                         list_begin, uint32_t(depth), per_key,
-                                                         elem_bits, end, keys, vals);
+    ps::order_class_heads_kernel<<<grid, ps::kThreads, 0, st>>>(act_base, n, head);
     PS_LAUNCHED();
-    static const unsigned long long span_init[2] = {0ull, ~0ull};
-    unsigned long long host_span[2] = {0ull, 0ull};
-    PS_HIP(hipMemcpyAsync(span, span_init, sizeof(span_init), hipMemcpyHostToDevice, st));
-    ps::key_span_kernel<<<grid < 1024 ? grid : 1024, ps::kThreads, 0, st>>>(keys, n, span);
+    int rc = ps_exclusive_scan_u32(head, rank, n, scan_ws, stream);
+    if (rc != PS_OK) return rc;
+    ps::order_class_start_kernel<<<grid, ps::kThreads, 0, st>>>(n, head, rank, head_at);
     PS_LAUNCHED();
-    PS_HIP(hipMemcpyAsync(host_span, span, sizeof(host_span), hipMemcpyDeviceToHost, st));
-    PS_HIP(hipStreamSynchronize(st));
-    const uint64_t diff = host_span[0] ^ host_span[1];
-    const uint64_t* k = keys;
-    const uint32_t* g = vals;
-    if (diff != 0) {
-      const int lo = __builtin_ctzll(diff) / 8 * 8;
-      const int hi = 64 - __builtin_clzll(diff);
-      int alt = 0;
-      const int rc = ps_radix_sort_pairs_u64(keys, keys_alt, vals, vals_alt, n, lo, hi,
-                                             radix_ws, &alt, stream);
+    ps::order_diverge_kernel<<<grid, ps::kThreads, 0, st>>>(
+        act_group, act_depth, n, lists, list_begin, head, rank, head_at, end, max_len, hi, lo,
+        lcp, idx);
+    PS_LAUNCHED();
+    // Sort by (hi, lo): one pass over the combined key when it fits 64 bits,
+    // else lo first and hi second (both stable).
+    const int hi_bits = ps::bits_for(3ull * n);
+    const uint64_t* k = nullptr;
+    const uint32_t* src = nullptr;
+    if (hi_bits + lo_bits <= 64) {
+      ps::order_combine_kernel<<<grid, ps::kThreads, 0, st>>>(n, hi, lo, lo_bits, keys);
+      PS_LAUNCHED();
+      rc = ps::sort_varying(keys, keys_alt, idx, idx_alt, n, span, radix_ws, st, &k, &src);
       if (rc != PS_OK) return rc;
-      if (alt) {
-        k = keys_alt;
-        g = vals_alt;
-      }
+    } else {
+      ps::order_permute_key_kernel<<<grid, ps::kThreads, 0, st>>>(n, idx, lo, keys);
+      PS_LAUNCHED();
+      rc = ps::sort_varying(keys, keys_alt, idx, idx_alt, n, span, radix_ws, st, &k, &src);
+      if (rc != PS_OK) return rc;
+      uint32_t* first = const_cast<uint32_t*>(src);
+      uint32_t* first_alt = first == idx ? idx_alt : idx;
+      ps::order_permute_key_kernel<<<grid, ps::kThreads, 0, st>>>(n, first, hi, keys2);
+      PS_LAUNCHED();
+      rc = ps::sort_varying(keys2, keys2_alt, first, first_alt, n, span, radix_ws, st, &k, &src);
+      if (rc != PS_OK) return rc;
     }
-    ps::order_flags_kernel<<<grid, ps::kThreads, 0, st>>>(k, n, elem_shift, new_head, old_head);
+    ps::order_runs_kernel<<<grid, ps::kThreads, 0, st>>>(n, src, hi, lo, new_head, old_head);
     PS_LAUNCHED();
-    int rc = ps_exclusive_scan_u32(new_head, new_rank, n, scan_ws, stream);
+    rc = ps_exclusive_scan_u32(new_head, new_rank, n, scan_ws, stream);
     if (rc == PS_OK) rc = ps_exclusive_scan_u32(old_head, old_rank, n, scan_ws, stream);
     if (rc != PS_OK) return rc;
     ps::order_heads_kernel<<<grid, ps::kThreads, 0, st>>>(n, new_head, new_rank, old_head,
                                                           old_rank, new_at, old_at);
     PS_LAUNCHED();
     ps::order_resolve_kernel<<<grid, ps::kThreads, 0, st>>>(
-        k, g, n, elem_shift, elem_bits, end, new_head, new_rank, old_head, old_rank, new_at,
-        old_at, gb, out, keep, next_base);
+        n, src, hi, lo, end, act_group, act_base, lcp, new_head, new_rank, old_head, old_rank,
+        new_at, old_at, gb, out, keep, next_group, next_base, next_depth);
     PS_LAUNCHED();
     rc = ps_exclusive_scan_u32(keep, slot, n, scan_ws, stream);
     if (rc != PS_OK) return rc;
-    ps::order_compact_kernel<<<grid, ps::kThreads, 0, st>>>(n, keep, slot, g, next_base,
-                                                            act_group, act_base);
+    ps::order_compact_kernel<<<grid, ps::kThreads, 0, st>>>(
+        n, keep, slot, next_group, next_base, next_depth, act_group, act_base, act_depth);
     PS_LAUNCHED();
     uint32_t tail[2] = {0u, 0u};
     PS_HIP(hipMemcpyAsync(&tail[0], slot + (n - 1), sizeof(uint32_t), hipMemcpyDeviceToHost, st));

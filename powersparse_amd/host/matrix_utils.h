@@ -32,9 +32,10 @@ enum GroupSort { GroupNoSort = 0, GroupDoSort = 1 };
 // (groups x L/32 words) and sorts once per word that varies; kBitLists sorts
 // each group's list of distinct signature bits and refines ties a few list
 // elements at a time, in memory bounded by nnz whatever L is. kAuto takes the
-// bitmaps up to kBitmapMaxWords words, the lists beyond.
+// bitmaps up to kBitmapMaxWords words (one or a few radix passes), the lists
+// beyond (measured faster from 22 words up: C1, C3, C4).
 enum class SignatureOrder { kAuto = 0, kBitmapWords = 1, kBitLists = 2 };
-constexpr int kBitmapMaxWords = 128;
+constexpr int kBitmapMaxWords = 4;
 
 // The order in which the operators run the groups (their results do not depend
 // on it, beyond the order of FP32 atomic additions). kSignature runs the public

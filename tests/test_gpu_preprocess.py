@@ -165,3 +165,20 @@ def test_device_cu_count_default():
     m = ps.PowerSparseMatrixGPU.from_csr(csr)
     assert m.PartitionCuCount() == ps.device_props(0)["cu_count"]
     say("device:", ps.device_props(0))
+
+
+def test_signature_order_two_pass_keys():
+    # 2^21 groups, a 2^30-bit signature and one 4096-element list: the sort key
+    # (class, side, divergence, element) needs more than 64 bits, so each round
+    # sorts in two stable passes
+    setup()
+    rng = np.random.default_rng(17)
+    length = 1 << 30
+    n = 1 << 21
+    pool = rng.integers(0, length, 64).tolist()
+    sets = [rng.choice(pool, int(rng.integers(1, 4))).tolist() for _ in range(n - 1)]
+    sets.append(sorted(set(rng.integers(0, length, 6000).tolist()))[:4096])
+    say("two-pass keys: groups", n)
+    got = run_order([sets[: n // 2], sets[n // 2:]], length)
+    np.testing.assert_array_equal(got[0], oracle.order_bit_lists(sets[: n // 2]))
+    np.testing.assert_array_equal(got[1], oracle.order_bit_lists(sets[n // 2:]))
