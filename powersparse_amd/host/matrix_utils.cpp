@@ -97,6 +97,38 @@ int WorksetCount(const unsigned long long* degree_sums, int cu_count) {
 
 namespace {
 
+// Groups per workset, as the device kernels split each row (matrix_utils.cu:
+// 132-156): S == 1 cuts rows into chunks of `fine`; otherwise the block sizes
+// are taken greedily from the largest and the rest is one residue group.
+void HostGroupCounts(const int* row_ptr, int rows, int S, int fine, int* group_num) {
+  std::vector<long long> total(static_cast<size_t>(S), 0);
+#pragma omp parallel
+  {
+    std::vector<long long> mine(static_cast<size_t>(S), 0);
+#pragma omp for schedule(static)
+    for (int r = 0; r < rows; ++r) {
+      long long d = row_ptr[r + 1] - row_ptr[r];
+      if (S == 1) {
+        mine[0] += (d + fine - 1) / fine;
+        continue;
+      }
+      for (int s = S - 1; s > 0; --s) {
+        const long long n = d / GROUP_SIZE(s);
+        mine[size_t(s)] += n;
+        d -= n * GROUP_SIZE(s);
+      }
+      mine[0] += d > 0;
+    }
+#pragma omp critical
+    for (int s = 0; s < S; ++s) total[size_t(s)] += mine[size_t(s)];
+  }
+  for (int s = 0; s < S; ++s) {
+    if (total[size_t(s)] > std::numeric_limits<int>::max())
+      throw std::runtime_error("Too many groups in one workset");
+    group_num[s] = int(total[size_t(s)]);
+  }
+}
+
 int BitsFor(uint64_t v) {
   int b = 0;
   while (b < 64 && (v >> b) != 0) ++b;
@@ -206,52 +238,50 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
   const int max_count = *std::max_element(col_nnz.begin(), col_nnz.end());
   clock.Mark(&PreprocessTimings::analyze_ms);
 
+  // Device work that does not need the column signature bits is enqueued
+  // first and the host computes the bits meanwhile: nothing in between waits
+  // for the device (the workspaces stay alive until after the host step).
+  //
   // Rank every row's nonzeros by column count (descending, ties in CSR order).
   const int count_bits = BitsFor(uint64_t(max_count));
   const int row_bits = BitsFor(uint64_t(rows - 1));
   DeviceArray<uint64_t> keys(static_cast<size_t>(nnz)), keys_alt(static_cast<size_t>(nnz));
   DeviceArray<uint32_t> vals(static_cast<size_t>(nnz)), vals_alt(static_cast<size_t>(nnz));
+  DeviceArray<char> rank_ws(ps_radix_workspace_bytes(size_t(nnz)));
+  ThrowOnError(ps_pre_rank_keys(d_rp.data(), rows, d_ci.data(), nnz, d_cn.data(), max_count,
+                                count_bits, keys.data(), vals.data(), st));
   {
-    DeviceArray<char> ws(ps_radix_workspace_bytes(size_t(nnz)));
-    ThrowOnError(ps_pre_rank_keys(d_rp.data(), rows, d_ci.data(), nnz, d_cn.data(), max_count,
-                                  count_bits, keys.data(), vals.data(), st));
     int alt = 0;
     ThrowOnError(ps_radix_sort_pairs_u64(keys.data(), keys_alt.data(), vals.data(),
                                          vals_alt.data(), size_t(nnz), 0,
-                                         count_bits + row_bits, ws.data(), &alt, st));
+                                         count_bits + row_bits, rank_ws.data(), &alt, st));
     if (alt) {
       std::swap(keys, keys_alt);
       std::swap(vals, vals_alt);
     }
-    // The workspace is released when it leaves scope; ps_free synchronises.
   }
-  keys_alt.Reset();
-  vals_alt.Reset();
   clock.Mark(&PreprocessTimings::rank_ms);
+
+  // Group counts per workset, on the host from row_ptr (the split the device
+  // kernels make), so the device arrays are sized without waiting.
+  _group_num = new int[S]();
+  HostGroupCounts(row_ptr, rows, S, fine, _group_num);
+  const int G0 = _group_num[0];
+  std::vector<long long> lengths(static_cast<size_t>(S), 0);  // nonzeros per workset
+  lengths[0] = nnz;
+  for (int s = 1; s < S; ++s) {
+    lengths[size_t(s)] = (long long)_group_num[s] * GROUP_SIZE(s);
+    lengths[0] -= lengths[size_t(s)];
+  }
 
   // Per-row group counts and their exclusive scans (group ids in row order).
   const size_t stride = size_t(rows) + 1;
   DeviceArray<uint32_t> prefix(static_cast<size_t>(S) * stride);
   ThrowOnError(ps_pre_group_counts(d_rp.data(), rows, S, fine, prefix.data(), st));
-  {
-    DeviceArray<char> ws(ps_scan_workspace_bytes(stride));
-    for (int s = 0; s < S; ++s)
-      ThrowOnError(ps_exclusive_scan_u32(prefix.data() + s * stride, prefix.data() + s * stride,
-                                         stride, ws.data(), st));
-  }
-
-  // Host: column signature bits, while the device works.
-  std::vector<int> sigbit(static_cast<size_t>(cols));
-  _signature_len = GenerateSigBitFFC(cols, col_nnz.data(), 2, sigbit.data());
-  clock.Mark(&PreprocessTimings::sigbit_ms);
-
-  _group_num = new int[S]();
-  for (int s = 0; s < S; ++s) {
-    uint32_t total = 0;
-    ThrowOnError(ps_memcpy_dtoh(&total, prefix.data() + s * stride + rows, sizeof(uint32_t)));
-    _group_num[s] = int(total);
-  }
-  const int G0 = _group_num[0];
+  DeviceArray<char> scan_ws(ps_scan_workspace_bytes(stride));
+  for (int s = 0; s < S; ++s)
+    ThrowOnError(ps_exclusive_scan_u32(prefix.data() + s * stride, prefix.data() + s * stride,
+                                       stride, scan_ws.data(), st));
 
   std::vector<DeviceArray<int>> des0(static_cast<size_t>(S)), start(static_cast<size_t>(S));
   std::vector<int*> des_ptr(static_cast<size_t>(S), nullptr), start_ptr(static_cast<size_t>(S), nullptr);
@@ -266,6 +296,59 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
   ThrowOnError(ps_pre_group_meta(d_rp.data(), rows, S, fine, prefix.data(), des_ptr.data(),
                                  start_ptr.data(), res_len.data(), res_atomic0.data(), st));
   clock.Mark(&PreprocessTimings::groups_ms);
+
+  // The row-ordered execution copy (task order) does not depend on the
+  // signature order either: build it now, decide whether to keep it later.
+  DeviceArray<uint32_t> iota, exec_len;
+  DeviceArray<char> exec_ws;
+  if (_task_order != TaskOrder::kSignature) {
+    size_t gmax = 0;
+    for (int s = 0; s < S; ++s) gmax = std::max(gmax, size_t(_group_num[s]));
+    iota.Allocate(gmax);
+    ThrowOnError(ps_iota_u32(iota.data(), int(gmax), st));
+    _exec_col_ind = new int*[S]();
+    _exec_sp_data = new float*[S]();
+    _exec_group_des = new int*[S]();
+    _exec_out_pos = new int*[S]();
+    if (_keep_csr_pos) _exec_csr_pos = new int*[S]();
+    // residue offsets in the initial (row) order
+    ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_residue_offset),
+                           sizeof(int) * (size_t(G0) + 1)));
+    ThrowOnError(ps_memset_async(_exec_residue_offset, 0, sizeof(int) * (size_t(G0) + 1), st));
+    if (G0 > 0) {
+      exec_len.Allocate(size_t(G0) + 1);
+      ThrowOnError(ps_memcpy_dtod_async(exec_len.data(), res_len.data(), sizeof(int) * size_t(G0),
+                                        st));
+      ThrowOnError(ps_memset_async(exec_len.data() + G0, 0, sizeof(uint32_t), st));
+      exec_ws.Allocate(ps_scan_workspace_bytes(size_t(G0) + 1));
+      ThrowOnError(ps_exclusive_scan_u32(exec_len.data(),
+                                         reinterpret_cast<uint32_t*>(_exec_residue_offset),
+                                         size_t(G0) + 1, exec_ws.data(), st));
+    }
+    for (int s = 0; s < S; ++s) {
+      const int G = _group_num[s];
+      if (G == 0) continue;
+      const size_t size = size_t(lengths[size_t(s)]);
+      ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_col_ind[s]), sizeof(int) * size));
+      ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_sp_data[s]), sizeof(float) * size));
+      if (_keep_csr_pos)
+        ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_csr_pos[s]), sizeof(int) * size));
+      ThrowOnError(ps_pre_gather_workset(s == 0 ? 0 : GROUP_SIZE(s), iota.data(), G,
+                                         start[size_t(s)].data(),
+                                         s == 0 ? _exec_residue_offset : nullptr, vals.data(),
+                                         d_ci.data(), d_sv.data(), _exec_col_ind[s],
+                                         _exec_sp_data[s],
+                                         _keep_csr_pos ? _exec_csr_pos[s] : nullptr, st));
+    }
+  }
+
+  // Host: column signature bits, while the device works.
+  std::vector<int> sigbit(static_cast<size_t>(cols));
+  _signature_len = GenerateSigBitFFC(cols, col_nnz.data(), 2, sigbit.data());
+  clock.Mark(&PreprocessTimings::sigbit_ms);
+  keys_alt.Reset();
+  vals_alt.Reset();
+  rank_ws.Reset();
 
   // Groups in signature order: perm[s][k] = initial group at position k.
   const int words = _signature_len / 32;
@@ -366,14 +449,7 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
   for (int s = 0; s < S; ++s) {
     const int G = _group_num[s];
     if (G == 0) continue;
-    size_t size;
-    if (s == 0) {
-      int total = 0;
-      ThrowOnError(ps_memcpy_dtoh(&total, _residue_offset + G0, sizeof(int)));
-      size = size_t(total);
-    } else {
-      size = size_t(G) * size_t(GROUP_SIZE(s));
-    }
+    const size_t size = size_t(lengths[size_t(s)]);
     ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_workset_col_ind[s]), sizeof(int) * size));
     ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_workset_sp_data[s]), sizeof(float) * size));
     if (_keep_csr_pos)
@@ -385,57 +461,12 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
                                        _keep_csr_pos ? _workset_csr_pos[s] : nullptr, st));
   }
 
-  // Task order: the row-ordered execution copy, kept when asked for or when it
-  // scores clearly better than the signature order.
+  // Task order: keep the row-ordered copy when asked for, or when it scores
+  // clearly better than the signature order.
   if (_task_order != TaskOrder::kSignature) {
-    size_t gmax = 0;
-    for (int s = 0; s < S; ++s) gmax = std::max(gmax, size_t(_group_num[s]));
-    DeviceArray<uint32_t> iota(gmax);
-    ThrowOnError(ps_iota_u32(iota.data(), int(gmax), st));
-    _exec_col_ind = new int*[S]();
-    _exec_sp_data = new float*[S]();
-    _exec_group_des = new int*[S]();
-    _exec_out_pos = new int*[S]();
-    if (_keep_csr_pos) _exec_csr_pos = new int*[S]();
-    // residue offsets in the initial (row) order
-    ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_residue_offset),
-                           sizeof(int) * (size_t(G0) + 1)));
-    ThrowOnError(ps_memset_async(_exec_residue_offset, 0, sizeof(int) * (size_t(G0) + 1), st));
-    if (G0 > 0) {
-      DeviceArray<uint32_t> len(static_cast<size_t>(G0) + 1);
-      ThrowOnError(ps_memcpy_dtod_async(len.data(), res_len.data(), sizeof(int) * size_t(G0), st));
-      ThrowOnError(ps_memset_async(len.data() + G0, 0, sizeof(uint32_t), st));
-      DeviceArray<char> ws(ps_scan_workspace_bytes(size_t(G0) + 1));
-      ThrowOnError(ps_exclusive_scan_u32(len.data(),
-                                         reinterpret_cast<uint32_t*>(_exec_residue_offset),
-                                         size_t(G0) + 1, ws.data(), st));
-      _exec_residue_atomic = reinterpret_cast<bool*>(res_atomic0.Release());
-    }
-    std::vector<long long> lengths(static_cast<size_t>(S), 0);
-    for (int s = 0; s < S; ++s) {
-      const int G = _group_num[s];
-      if (G == 0) continue;
-      _exec_group_des[s] = des0[size_t(s)].Release();
-      size_t size;
-      if (s == 0) {
-        int total = 0;
-        ThrowOnError(ps_memcpy_dtoh(&total, _residue_offset + G0, sizeof(int)));
-        size = size_t(total);
-      } else {
-        size = size_t(G) * size_t(GROUP_SIZE(s));
-      }
-      lengths[size_t(s)] = (long long)size;
-      ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_col_ind[s]), sizeof(int) * size));
-      ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_sp_data[s]), sizeof(float) * size));
-      if (_keep_csr_pos)
-        ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_csr_pos[s]), sizeof(int) * size));
-      ThrowOnError(ps_pre_gather_workset(s == 0 ? 0 : GROUP_SIZE(s), iota.data(), G,
-                                         start[size_t(s)].data(),
-                                         s == 0 ? _exec_residue_offset : nullptr, vals.data(),
-                                         d_ci.data(), d_sv.data(), _exec_col_ind[s],
-                                         _exec_sp_data[s],
-                                         _keep_csr_pos ? _exec_csr_pos[s] : nullptr, st));
-    }
+    if (G0 > 0) _exec_residue_atomic = reinterpret_cast<bool*>(res_atomic0.Release());
+    for (int s = 0; s < S; ++s)
+      if (_group_num[s] > 0) _exec_group_des[s] = des0[size_t(s)].Release();
     bool keep = _task_order == TaskOrder::kRow;
     if (_task_order == TaskOrder::kAuto) {
       // Launch order of the worksets: largest groups first, the residue last.
