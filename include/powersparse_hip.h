@@ -174,13 +174,14 @@ int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int
                         const float* rhs, float* out_csr, ps_stream_t stream);
 
 /* SDDMM of worksets laid out in another group order than the public ones (a
- * task-order execution copy): the result of stored nonzero p of workset s goes
- * to out[s][out_pos[s][p]], out[s] being the public workset-order buffer; block
- * results are stored, residue results added, exactly as ps_sddmm_launch does
- * at the public positions. No reference counterpart (the reference runs the
- * public layout only). */
+ * task-order execution copy): the result of member j of group g of workset s
+ * goes to out[s][out_base[s][g] + j], out[s] being the public workset-order
+ * buffer (ps_pre_exec_positions gives the bases); block results are stored,
+ * residue results added, exactly as ps_sddmm_launch does at the public
+ * positions. No reference counterpart (the reference runs the public layout
+ * only). */
 int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
-                            const int* residue_offset, const int* const* out_pos, int rows,
+                            const int* residue_offset, const int* const* out_base, int rows,
                             int cols, int N, const float* lhs, const float* rhs,
                             float* const* out, ps_stream_t stream);
 
@@ -272,15 +273,13 @@ int ps_pre_signature_keys(const uint32_t* sig_word, const uint32_t* perm, int n,
 int ps_pre_signature_span(const uint32_t* sig, int groups, int words, uint32_t* or_host,
                           uint32_t* and_host, ps_stream_t stream);
 
-/* Public workset position of every slot of a task-order execution copy: for
- * public group k (signature order) holding initial group perm[k],
- * out_pos[exec_offset[perm[k]] + j] = pub_offset[k] + j over the group's
- * members. Block worksets (group_size > 0) use k * group_size for both
- * offsets; the residue workset passes its initial-order and public offsets.
+/* Output base of every group of a task-order execution copy (groups in their
+ * initial order): out_base[perm[k]] = where public group k (signature order)
+ * starts in the public workset, k * group_size for blocks (group_size > 0),
+ * pub_offset[k] (the public residue offsets) for the residue workset.
  * No reference counterpart. */
 int ps_pre_exec_positions(int group_size, const uint32_t* perm, int groups,
-                          const int* exec_offset, const int* pub_offset, int* out_pos,
-                          ps_stream_t stream);
+                          const int* pub_offset, int* out_base, ps_stream_t stream);
 
 /* Gather-locality score of a task order: the concatenated column sequence
  * col_ind[0][0 .. lengths[0]), col_ind[1][...], ... is cut into windows of

@@ -113,7 +113,7 @@ HIP_API = [
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int,
       ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, ctypes.POINTER(c_void_p), c_void_p]),
     ("ps_pre_exec_positions", ctypes.c_int,
-     [ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+     [ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p]),
     ("ps_pre_locality_score", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(c_void_p), ctypes.POINTER(ctypes.c_longlong), ctypes.c_int,
       ctypes.c_int, c_double_p, c_void_p]),

@@ -641,21 +641,13 @@ __global__ void large_group_write_kernel(size_t total, const uint64_t* __restric
 
 // ---- task order ----
 
-// For the public group k (signature order) holding initial group g = perm[k]:
-// out_pos[exec_off(g) + j] = pub_off(k) + j. Offsets are k * gs for blocks,
-// the residue offsets (initial order / signature order) otherwise.
+// out_base[perm[k]] = where public group k (signature order) starts in its
+// workset: k * gs for blocks, pub_offset[k] for the residue.
 __global__ void exec_positions_kernel(int gs, const uint32_t* __restrict__ perm, int groups,
-                                      const int* __restrict__ exec_offset,
                                       const int* __restrict__ pub_offset,
-                                      int* __restrict__ out_pos) {
-  for (int k = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave; k < groups;
-       k += gridDim.x * (blockDim.x / kWave)) {
-    const uint32_t g = perm[k];
-    const int src = gs ? int(g) * gs : exec_offset[g];
-    const int dst = gs ? k * gs : pub_offset[k];
-    const int len = gs ? gs : pub_offset[k + 1] - dst;
-    for (int j = lane_id(); j < len; j += kWave) out_pos[src + j] = dst + j;
-  }
+                                      int* __restrict__ out_base) {
+  for (int k = blockIdx.x * blockDim.x + threadIdx.x; k < groups; k += gridDim.x * blockDim.x)
+    out_base[perm[k]] = gs ? k * gs : pub_offset[k];
 }
 
 // Locality score: for `windows` windows of `window` consecutive elements of
@@ -987,17 +979,14 @@ int ps_pre_gather_workset(int group_size, const uint32_t* perm, int groups,
 }
 
 int ps_pre_exec_positions(int group_size, const uint32_t* perm, int groups,
-                          const int* exec_offset, const int* pub_offset, int* out_pos,
-                          ps_stream_t stream) {
-  PS_CHECK_ARG(perm && out_pos && groups >= 0 && group_size >= 0 &&
-                   (group_size > 0 || (exec_offset && pub_offset)),
+                          const int* pub_offset, int* out_base, ps_stream_t stream) {
+  PS_CHECK_ARG(perm && out_base && groups >= 0 && group_size >= 0 &&
+                   (group_size > 0 || pub_offset),
                "ps_pre_exec_positions: bad argument");
   if (groups == 0) return PS_OK;
-  const unsigned waves_per_block = ps::kThreads / ps::kWave;
-  size_t blocks = (size_t(groups) + waves_per_block - 1) / waves_per_block;
-  if (blocks > 65536) blocks = 65536;
-  ps::exec_positions_kernel<<<unsigned(blocks), ps::kThreads, 0, ps::to_hip(stream)>>>(
-      group_size, perm, groups, exec_offset, pub_offset, out_pos);
+  ps::exec_positions_kernel<<<ps::grid_for(size_t(groups)), ps::kThreads, 0,
+                              ps::to_hip(stream)>>>(group_size, perm, groups, pub_offset,
+                                                    out_base);
   PS_LAUNCHED();
   return PS_OK;
 }

@@ -17,12 +17,12 @@
 // outputs are stored, residue outputs are added atomically into out[0], the
 // output is in workset order.
 //
-// Scatter variant (kScatter): the result of stored nonzero p of workset s goes
-// to out[s][out_pos[s][p]]. Used (a) for CSR order (every out[s] is the one
-// CSR-order array, out_pos the CSR positions, plain stores: each position is
-// written once, no zeroing needed) and (b) to run a row-ordered execution copy
-// of the worksets while writing the public workset layout (out_pos = public
-// positions; residue results are still added atomically, as above).
+// Store modes (kMode): 0 = at the nonzero's own position (as above); 1 = per
+// nonzero map, out[s][map[s][p]]: CSR order (every out[s] is the one
+// CSR-order array, map = CSR positions, plain stores: each position is
+// written once, no zeroing needed); 2 = per group base, out[s][base[s][g] + j]
+// for member j of group g: a row-ordered execution copy of the worksets
+// writing the public workset layout (residue results still added atomically).
 #include "ps_common.hpp"
 
 namespace ps {
@@ -43,8 +43,8 @@ struct SddmmArgs {
   const float* rhs;
   uint64_t lhs_bytes;
   uint64_t rhs_bytes;
-  const int* out_pos[PS_MAX_WORKSETS];  // scatter variant only
-  int32_t residue_add;                  // scatter variant: residue results added
+  const int* out_pos[PS_MAX_WORKSETS];  // mode 1: per-nonzero map; mode 2: per-group base
+  int32_t residue_add;                  // modes 1-2: residue results added, not stored
 };
 
 // Transposing reduction over the 8 lanes of a slot: in p[j] each lane holds
@@ -102,7 +102,7 @@ __device__ __forceinline__ void slot_dots(const Rows<kBuf>& Y,
   }
 }
 
-template <int KQ, bool kBuf, bool kScatter>
+template <int KQ, bool kBuf, int kMode>
 __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs args) {
   constexpr int K = 32 * KQ;
   const uint32_t blk = balanced_block(blockIdx.x, gridDim.x);
@@ -146,8 +146,15 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     const float dot = slot_transpose_sum(p, sub);
     const int pos = local * 64 + lane;
     if (valid) {
-      if constexpr (kScatter) out[out_pos[pos]] = dot * ws.sp_data[pos];
-      else out[pos] = dot * ws.sp_data[pos];
+      const float v = dot * ws.sp_data[pos];
+      if constexpr (kMode == 1) {
+        out[out_pos[pos]] = v;
+      } else if constexpr (kMode == 2) {
+        const int gl = pos / ws.group_size;
+        out[out_pos[gl] + (pos - gl * ws.group_size)] = v;
+      } else {
+        out[pos] = v;
+      }
     }
   } else {
     const int rcap = args.rcap;
@@ -175,9 +182,10 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
       const int k = c0 + q;
       if (k < len) {
         const float v = dot * ws.sp_data[beg + k];
-        if constexpr (kScatter) {
-          if (args.residue_add) unsafeAtomicAdd(out + out_pos[beg + k], v);
-          else out[out_pos[beg + k]] = v;
+        if constexpr (kMode != 0) {
+          const int at = kMode == 1 ? out_pos[beg + k] : out_pos[g] + k;
+          if (args.residue_add) unsafeAtomicAdd(out + at, v);
+          else out[at] = v;
         } else {
           unsafeAtomicAdd(out + beg + k, v);
         }
@@ -195,21 +203,26 @@ __global__ void to_csr_kernel(const float* __restrict__ in, const int* __restric
 }
 
 template <int KQ>
-void launch_kq(const SddmmArgs& a, bool buf, bool scatter, unsigned grid, hipStream_t stream) {
+void launch_kq(const SddmmArgs& a, bool buf, int mode, unsigned grid, hipStream_t stream) {
   constexpr unsigned kBlock = kWave * kWavesPerBlock;
-  if (scatter) {
-    if (buf) sddmm_kernel<KQ, true, true><<<grid, kBlock, 0, stream>>>(a);
-    else sddmm_kernel<KQ, false, true><<<grid, kBlock, 0, stream>>>(a);
+  if (mode == 1) {
+    if (buf) sddmm_kernel<KQ, true, 1><<<grid, kBlock, 0, stream>>>(a);
+    else sddmm_kernel<KQ, false, 1><<<grid, kBlock, 0, stream>>>(a);
+  } else if (mode == 2) {
+    if (buf) sddmm_kernel<KQ, true, 2><<<grid, kBlock, 0, stream>>>(a);
+    else sddmm_kernel<KQ, false, 2><<<grid, kBlock, 0, stream>>>(a);
   } else {
-    if (buf) sddmm_kernel<KQ, true, false><<<grid, kBlock, 0, stream>>>(a);
-    else sddmm_kernel<KQ, false, false><<<grid, kBlock, 0, stream>>>(a);
+    if (buf) sddmm_kernel<KQ, true, 0><<<grid, kBlock, 0, stream>>>(a);
+    else sddmm_kernel<KQ, false, 0><<<grid, kBlock, 0, stream>>>(a);
   }
 }
 
-// Workset q writes outs[q] at its own positions, or at out_pos[q][p] when
-// out_pos is given (residue results added when residue_add).
+// Workset q writes outs[q] at its own positions (mode 0), through the
+// per-nonzero map out_pos[q] (mode 1) or after the per-group bases out_pos[q]
+// (mode 2); residue results are added when residue_add (modes 1-2).
 int launch(int count, const int* order, const ps_workset* worksets, float* const* outs,
-           const int* const* out_pos, int residue_add, const int* residue_offset, int rows,
+           int mode, const int* const* out_pos, int residue_add, const int* residue_offset,
+           int rows,
            int cols, int N, const float* lhs, const float* rhs, int rcap, hipStream_t stream) {
   PS_CHECK_ARG(N > 0 && N % 32 == 0 && N <= 512,
                "SDDMM requires N to be a multiple of 32 between 32 and 512");
@@ -235,7 +248,7 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
     const ps_workset& w = worksets[q];
     if (w.group_num <= 0) continue;
     PS_CHECK_ARG(outs[q], "Missing SDDMM output workset");
-    if (out_pos) PS_CHECK_ARG(out_pos[q], "Missing output positions of an SDDMM workset");
+    if (mode != 0) PS_CHECK_ARG(out_pos && out_pos[q], "Missing output positions of an SDDMM workset");
     PS_CHECK_ARG(w.col_ind && w.sp_data && w.group_des, "Invalid SDDMM workset buffers");
     const int s = order[q];
     uint64_t t;
@@ -250,7 +263,7 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
     a.ws[n] = w;
     if (s == 0) a.ws[n].group_size = 0;
     a.out[n] = outs[q];
-    if (out_pos) a.out_pos[n] = out_pos[q];
+    if (mode != 0) a.out_pos[n] = out_pos[q];
     a.task_begin[n] = uint32_t(tasks);
     tasks += t;
     ++n;
@@ -262,22 +275,22 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
   a.total_tasks = uint32_t(tasks);
   const unsigned grid = unsigned((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
   switch (N / 32) {
-    case 1: launch_kq<1>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 2: launch_kq<2>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 3: launch_kq<3>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 4: launch_kq<4>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 5: launch_kq<5>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 6: launch_kq<6>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 7: launch_kq<7>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 8: launch_kq<8>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 9: launch_kq<9>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 10: launch_kq<10>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 11: launch_kq<11>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 12: launch_kq<12>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 13: launch_kq<13>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 14: launch_kq<14>(a, buf, out_pos != nullptr, grid, stream); break;
-    case 15: launch_kq<15>(a, buf, out_pos != nullptr, grid, stream); break;
-    default: launch_kq<16>(a, buf, out_pos != nullptr, grid, stream); break;
+    case 1: launch_kq<1>(a, buf, mode, grid, stream); break;
+    case 2: launch_kq<2>(a, buf, mode, grid, stream); break;
+    case 3: launch_kq<3>(a, buf, mode, grid, stream); break;
+    case 4: launch_kq<4>(a, buf, mode, grid, stream); break;
+    case 5: launch_kq<5>(a, buf, mode, grid, stream); break;
+    case 6: launch_kq<6>(a, buf, mode, grid, stream); break;
+    case 7: launch_kq<7>(a, buf, mode, grid, stream); break;
+    case 8: launch_kq<8>(a, buf, mode, grid, stream); break;
+    case 9: launch_kq<9>(a, buf, mode, grid, stream); break;
+    case 10: launch_kq<10>(a, buf, mode, grid, stream); break;
+    case 11: launch_kq<11>(a, buf, mode, grid, stream); break;
+    case 12: launch_kq<12>(a, buf, mode, grid, stream); break;
+    case 13: launch_kq<13>(a, buf, mode, grid, stream); break;
+    case 14: launch_kq<14>(a, buf, mode, grid, stream); break;
+    case 15: launch_kq<15>(a, buf, mode, grid, stream); break;
+    default: launch_kq<16>(a, buf, mode, grid, stream); break;
   }
   PS_LAUNCHED();
   return PS_OK;
@@ -304,15 +317,15 @@ int ps_sddmm_launch(int workset_count, const ps_workset* worksets, const int* re
   // A single workset means fine mode (residue groups of at most 16 nonzeros,
   // utils/matrix_utils.cu:137-141); otherwise residue groups hold at most 31.
   const int rcap = workset_count == 1 ? 16 : 32;
-  return ps::launch(workset_count, order, ordered, outs, nullptr, 0, residue_offset, rows, cols,
-                    N, lhs, rhs, rcap, ps::to_hip(stream));
+  return ps::launch(workset_count, order, ordered, outs, 0, nullptr, 0, residue_offset, rows,
+                    cols, N, lhs, rhs, rcap, ps::to_hip(stream));
 }
 
 int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
-                            const int* residue_offset, const int* const* out_pos, int rows,
+                            const int* residue_offset, const int* const* out_base, int rows,
                             int cols, int N, const float* lhs, const float* rhs,
                             float* const* out, ps_stream_t stream) {
-  PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets && out_pos &&
+  PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets && out_base &&
                    out,
                "Invalid SDDMM workset count");
   int order[PS_MAX_WORKSETS];
@@ -322,12 +335,12 @@ int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
   for (int q = 0; q < workset_count; ++q) {
     order[q] = workset_count - 1 - q;
     ordered[q] = worksets[workset_count - 1 - q];
-    pos[q] = out_pos[workset_count - 1 - q];
+    pos[q] = out_base[workset_count - 1 - q];
     outs[q] = out[workset_count - 1 - q];
   }
   const int rcap = workset_count == 1 ? 16 : 32;
-  return ps::launch(workset_count, order, ordered, outs, pos, 1, residue_offset, rows, cols, N,
-                    lhs, rhs, rcap, ps::to_hip(stream));
+  return ps::launch(workset_count, order, ordered, outs, 2, pos, 1, residue_offset, rows, cols,
+                    N, lhs, rhs, rcap, ps::to_hip(stream));
 }
 
 int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
@@ -347,8 +360,8 @@ int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int
     outs[q] = out_csr;
   }
   const int rcap = workset_count == 1 ? 16 : 32;
-  return ps::launch(workset_count, order, ordered, outs, pos, 0, residue_offset, rows, cols, N,
-                    lhs, rhs, rcap, ps::to_hip(stream));
+  return ps::launch(workset_count, order, ordered, outs, 1, pos, 0, residue_offset, rows, cols,
+                    N, lhs, rhs, rcap, ps::to_hip(stream));
 }
 
 int ps_workset_to_csr(int workset_count, const long long* lengths, const int* const* csr_pos,
@@ -374,8 +387,8 @@ int ps_sddmm_workset_launch(int s, const ps_workset* workset, const int* residue
                             int rows, int cols, int N, const float* lhs, const float* rhs,
                             float* out, ps_stream_t stream) {
   PS_CHECK_ARG(s >= 0 && s < PS_MAX_WORKSETS && workset, "Invalid SDDMM workset");
-  return ps::launch(1, &s, workset, &out, nullptr, 0, residue_offset, rows, cols, N, lhs, rhs,
-                    32, ps::to_hip(stream));
+  return ps::launch(1, &s, workset, &out, 0, nullptr, 0, residue_offset, rows, cols, N, lhs,
+                    rhs, 32, ps::to_hip(stream));
 }
 
 }  // extern "C"

@@ -309,7 +309,7 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
     _exec_col_ind = new int*[S]();
     _exec_sp_data = new float*[S]();
     _exec_group_des = new int*[S]();
-    _exec_out_pos = new int*[S]();
+    _exec_out_base = new int*[S]();
     if (_keep_csr_pos) _exec_csr_pos = new int*[S]();
     // residue offsets in the initial (row) order
     ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_residue_offset),
@@ -488,11 +488,10 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
       for (int s = 0; s < S; ++s) {
         const int G = _group_num[s];
         if (G == 0) continue;
-        ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_out_pos[s]),
-                               sizeof(int) * size_t(lengths[size_t(s)])));
+        ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_exec_out_base[s]),
+                               sizeof(int) * size_t(G)));
         ThrowOnError(ps_pre_exec_positions(s == 0 ? 0 : GROUP_SIZE(s), perm[size_t(s)].data(), G,
-                                           _exec_residue_offset, _residue_offset,
-                                           _exec_out_pos[s], st));
+                                           _residue_offset, _exec_out_base[s], st));
       }
     } else {
       _task_order = TaskOrder::kSignature;
@@ -513,7 +512,7 @@ ExecutionLayout PowerSparseMatrixGPU::Execution() const {
     e.group_des = _exec_group_des;
     e.residue_offset = _exec_residue_offset;
     e.residue_atomic = _exec_residue_atomic;
-    e.out_pos = _exec_out_pos;
+    e.out_base = _exec_out_base;
     e.csr_pos = _exec_csr_pos;
   } else {
     e.col_ind = _workset_col_ind;
@@ -533,20 +532,20 @@ void PowerSparseMatrixGPU::ReleaseExecution() noexcept {
     if (_exec_col_ind) ps_free(_exec_col_ind[s]);
     if (_exec_sp_data) ps_free(_exec_sp_data[s]);
     if (_exec_group_des) ps_free(_exec_group_des[s]);
-    if (_exec_out_pos) ps_free(_exec_out_pos[s]);
+    if (_exec_out_base) ps_free(_exec_out_base[s]);
     if (_exec_csr_pos) ps_free(_exec_csr_pos[s]);
   }
   delete[] _exec_col_ind;
   delete[] _exec_sp_data;
   delete[] _exec_group_des;
-  delete[] _exec_out_pos;
+  delete[] _exec_out_base;
   delete[] _exec_csr_pos;
   ps_free(_exec_residue_offset);
   ps_free(_exec_residue_atomic);
   _exec_col_ind = nullptr;
   _exec_sp_data = nullptr;
   _exec_group_des = nullptr;
-  _exec_out_pos = nullptr;
+  _exec_out_base = nullptr;
   _exec_csr_pos = nullptr;
   _exec_residue_offset = nullptr;
   _exec_residue_atomic = nullptr;

@@ -40,7 +40,7 @@ constexpr int kBitmapMaxWords = 4;
 // The order in which the operators run the groups (their results do not depend
 // on it, beyond the order of FP32 atomic additions). kSignature runs the public
 // worksets as laid out. kRow runs a row-ordered copy of them (the group
-// numbering before the signature sort; ~12 more bytes per nonzero of device
+// numbering before the signature sort; ~8 more bytes per nonzero of device
 // memory), which keeps rows with shared columns together when the row ids
 // carry the graph's locality, as in community graphs. kAuto builds the copy,
 // scores both orders by the distinct columns per window of nearby nonzeros
@@ -50,16 +50,17 @@ enum class TaskOrder { kAuto = 0, kSignature = 1, kRow = 2 };
 constexpr double kRowOrderGain = 0.85;
 constexpr int kLocalityWindow = 65536, kLocalityWindows = 128;
 
-// The worksets as the operators run them: the public ones (out_pos == nullptr)
-// or the row-ordered copy, whose slot p of workset s belongs at out_pos[s][p]
-// of the public layout. csr_pos: CSR position per slot, or nullptr.
+// The worksets as the operators run them: the public ones (out_base ==
+// nullptr) or the row-ordered copy, whose group g of workset s starts at
+// out_base[s][g] in the public layout. csr_pos: CSR position per slot, or
+// nullptr.
 struct ExecutionLayout {
   const int* const* col_ind = nullptr;
   const float* const* sp_data = nullptr;
   const int* const* group_des = nullptr;
   const int* residue_offset = nullptr;
   const bool* residue_atomic = nullptr;
-  const int* const* out_pos = nullptr;
+  const int* const* out_base = nullptr;
   const int* const* csr_pos = nullptr;
 };
 
@@ -151,7 +152,7 @@ class PowerSparseMatrixGPU {
   int** _exec_col_ind = nullptr;
   float** _exec_sp_data = nullptr;
   int** _exec_group_des = nullptr;
-  int** _exec_out_pos = nullptr;
+  int** _exec_out_base = nullptr;
   int** _exec_csr_pos = nullptr;
   int* _exec_residue_offset = nullptr;
   bool* _exec_residue_atomic = nullptr;

@@ -73,9 +73,9 @@ void SDDMMAsync(const PowerSparseMatrixGPU& m, int N, const float* lhs, const fl
     if (m.GroupNum()[s] != 0 && !out[s]) throw std::invalid_argument("Missing SDDMM output workset");
   const ExecutionLayout e = m.Execution();
   const auto ws = Worksets(m, e);
-  if (e.out_pos)  // row-ordered copy: results scattered to the public layout
+  if (e.out_base)  // row-ordered copy: results written to the public layout
     ThrowOnError(ps_sddmm_scatter_launch(m.GroupTypeNum(), ws.data(), e.residue_offset,
-                                         e.out_pos, m.MatrixRow(), m.MatrixCol(), N, lhs, rhs,
+                                         e.out_base, m.MatrixRow(), m.MatrixCol(), N, lhs, rhs,
                                          out, stream));
   else
     ThrowOnError(ps_sddmm_launch(m.GroupTypeNum(), ws.data(), e.residue_offset, m.MatrixRow(),
