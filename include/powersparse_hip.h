@@ -130,7 +130,8 @@ typedef struct ps_workset {
  * and C (rows x N) row-major. Block groups and residue groups with
  * residue_atomic[g] != 0 add atomically into C; other residue groups store
  * (overwrite) their row. N must be a positive multiple of 32; cols * N and
- * rows * N must fit in int32.
+ * rows * N must fit in int32. B, C and the block worksets' col_ind / sp_data
+ * must be 16-byte aligned (as ps_malloc returns them).
  * Replaces: the launch loop of PowerSparse::SpMM (PowerSparse_SpMM/spmm_solution.cu:16-31)
  * and the kernels spmm_kernel_block (spmm_kernel_block.cu:60-162) and
  * spmm_kernel_residue (spmm_kernel_residue.cu:5-82). */
@@ -150,7 +151,8 @@ int ps_spmm_workset_launch(int s, const ps_workset* workset, const int* residue_
  * worksets store their outputs; the residue workset adds into out[0] (the
  * reference uses atomicAdd into a caller-zeroed buffer). N must be a positive
  * multiple of 32 and at most 512 (the reference accepts 32 and 128 only,
- * sddmm_solution.cu:10-11).
+ * sddmm_solution.cu:10-11). lhs, rhs and the block worksets' col_ind must be
+ * 16-byte aligned.
  * Replaces: PowerSparse::SDDMM's launch loop (sddmm_solution.cu:23-48) and
  * sddmm_kernel_block_reduce{32,128} (sddmm_kernel_block.cu:92-240),
  * sddmm_kernel_residue_reduce{32,128} (sddmm_kernel_residue.cu:69-545). */

@@ -23,6 +23,9 @@ inline int fail(int code, const std::string& msg) {
 
 inline hipStream_t to_hip(ps_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// The kernels move dense rows and staged nonzeros with 128-bit accesses.
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 }  // namespace ps
 
 // Returns PS_ERR_RUNTIME with "file:line: call: hip error text" on failure, the

@@ -229,6 +229,7 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
   PS_CHECK_ARG(int64_t(rows) * N <= INT32_MAX && int64_t(cols) * N <= INT32_MAX,
                "Dense dimensions exceed the 32-bit kernel indexing range");
   PS_CHECK_ARG(lhs && rhs && outs, "Invalid SDDMM buffers");
+  PS_CHECK_ARG(aligned16(lhs) && aligned16(rhs), "SDDMM dense buffers must be 16-byte aligned");
   SddmmArgs a{};
   a.residue_add = residue_add;
   a.N = N;
@@ -248,11 +249,14 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
     const ps_workset& w = worksets[q];
     if (w.group_num <= 0) continue;
     PS_CHECK_ARG(outs[q], "Missing SDDMM output workset");
-    if (mode != 0) PS_CHECK_ARG(out_pos && out_pos[q], "Missing output positions of an SDDMM workset");
+    if (mode != 0) {
+      PS_CHECK_ARG(out_pos && out_pos[q], "Missing output positions of an SDDMM workset");
+    }
     PS_CHECK_ARG(w.col_ind && w.sp_data && w.group_des, "Invalid SDDMM workset buffers");
     const int s = order[q];
     uint64_t t;
     if (s > 0) {
+      PS_CHECK_ARG(aligned16(w.col_ind), "Block workset arrays must be 16-byte aligned");
       PS_CHECK_ARG(w.group_size >= 32 && (w.group_size & (w.group_size - 1)) == 0,
                    "Block workset group size must be a power of two >= 32");
       t = (uint64_t(w.group_num) * w.group_size + 63) / 64;

@@ -263,6 +263,7 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
   PS_CHECK_ARG(int64_t(rows) * N <= INT32_MAX && int64_t(cols) * N <= INT32_MAX,
                "Dense dimensions exceed the 32-bit kernel indexing range");
   PS_CHECK_ARG(B && C, "Invalid SpMM buffers");
+  PS_CHECK_ARG(aligned16(B) && aligned16(C), "SpMM dense buffers must be 16-byte aligned");
   const int lpn = pick_lpn(N);
   const int SL = 64 / lpn;
   SpmmArgs a{};
@@ -285,6 +286,8 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
     PS_CHECK_ARG(w.col_ind && w.sp_data && w.group_des, "Invalid SpMM workset buffers");
     uint64_t t;
     if (s > 0) {
+      PS_CHECK_ARG(aligned16(w.col_ind) && aligned16(w.sp_data),
+                   "Block workset arrays must be 16-byte aligned");
       PS_CHECK_ARG(w.group_size >= 32 && (w.group_size & (w.group_size - 1)) == 0,
                    "Block workset group size must be a power of two >= 32");
       const uint64_t T = uint64_t(kPer) * SL;

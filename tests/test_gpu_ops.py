@@ -203,3 +203,40 @@ def test_operands_over_4gib():
     E, M = oracle.sddmm(np.arange(rows, dtype=np.int32), csr.row_ptr, cc, csr.values, N, X,
                         compact, with_mag=True)
     say("  ", tolerance.check(out.download(np.float32, csr.nnz), E, M, "SDDMM > 4 GiB"))
+
+
+def test_misaligned_buffers_rejected():
+    # the kernels use 128-bit accesses: the raw launchers refuse buffers that
+    # are not 16-byte aligned instead of running on them
+    setup()
+    csr = ps.synth("C1", seed=13, scale=50)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=4)
+    S = m.GroupTypeNum()
+    assert S > 1
+    cps, vps, dps = m.WorksetColInd(), m.WorksetSpData(), m.GroupDestination()
+    G = m.GroupNum()
+    ws = [(cps[s], vps[s], dps[s], G[s], 0 if s == 0 else ps.GROUP_SIZE(s)) for s in range(S)]
+    N = 32
+    B = ps.DeviceBuffer(csr.cols * N * 4 + 16)
+    C = ps.DeviceBuffer(csr.rows * N * 4 + 16)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        ps.spmm_launch(ws, m.ResidueOffset(), m.ResidueAtomic(), csr.rows, csr.cols, N,
+                       B.ptr + 4, C.ptr)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        ps.spmm_launch(ws, m.ResidueOffset(), m.ResidueAtomic(), csr.rows, csr.cols, N, B.ptr,
+                       C.ptr + 8)
+    bad = list(ws)
+    bad[S - 1] = (cps[S - 1] + 4,) + tuple(ws[S - 1][1:])
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        ps.spmm_launch(bad, m.ResidueOffset(), m.ResidueAtomic(), csr.rows, csr.cols, N, B.ptr,
+                       C.ptr)
+    X = ps.DeviceBuffer(csr.rows * N * 4 + 16)
+    outs = [ps.DeviceBuffer(max(n, 1) * 4) for n in m.sddmm_output_sizes()]
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        ps.sddmm_launch(ws, m.ResidueOffset(), csr.rows, csr.cols, N, X.ptr + 4, B.ptr, outs)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        ps.sddmm_launch(bad, m.ResidueOffset(), csr.rows, csr.cols, N, X.ptr, B.ptr, outs)
+    # the same call with aligned buffers runs
+    ps.spmm_launch(ws, m.ResidueOffset(), m.ResidueAtomic(), csr.rows, csr.cols, N, B.ptr,
+                   C.ptr)
+    ps.synchronize()
