@@ -344,6 +344,245 @@ __global__ void order_diverge_kernel(const uint32_t* __restrict__ act_group,
   }
 }
 
+// ---- refinement tail in one workgroup ----
+//
+// Once at most kFinishMax groups are still tied, one 1024-thread workgroup
+// runs the remaining rounds with the whole state in LDS (no host round trip
+// per round): the same rounds as above, the sort being an LDS bitonic sort of
+// (key, slot) pairs (slots unique, so equal keys keep their class order) and
+// run / class starts coming from block max-scans.
+constexpr int kFinishMax = 2048;
+constexpr int kFinishThreads = 1024;
+constexpr int kFinishPer = kFinishMax / kFinishThreads;  // elements per thread
+// LDS of order_finish_kernel: one uint64 key and seven uint32 arrays per
+// element, plus the scan partials.
+constexpr size_t kFinishLds =
+    size_t(kFinishMax) * (sizeof(uint64_t) + 7 * sizeof(uint32_t)) +
+    (kFinishThreads / kWave) * sizeof(uint32_t);
+
+// Exclusive sum (kSum) or inclusive max over v[0 .. kFinishMax) in LDS;
+// wsum holds kFinishThreads / kWave partials. Ends with a barrier.
+template <bool kSum>
+__device__ void block_scan(uint32_t* v, uint32_t* wsum) {
+  const int t = threadIdx.x;
+  uint32_t x[kFinishPer];
+  uint32_t run = 0;
+#pragma unroll
+  for (int q = 0; q < kFinishPer; ++q) {  // thread t owns v[kFinishPer * t + q]
+    x[q] = v[kFinishPer * t + q];
+    run = kSum ? run + x[q] : max(run, x[q]);
+  }
+  uint32_t inc = run;
+  const int lane = lane_id();
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t y = uint32_t(__shfl_up(int(inc), d, kWave));
+    if (lane >= d) inc = kSum ? inc + y : max(inc, y);
+  }
+  if (lane == kWave - 1) wsum[t / kWave] = inc;
+  __syncthreads();
+  if (t < kWave) {
+    uint32_t w = t < kFinishThreads / kWave ? wsum[t] : 0u;
+    for (int d = 1; d < kWave; d <<= 1) {
+      const uint32_t y = uint32_t(__shfl_up(int(w), d, kWave));
+      if (t >= d) w = kSum ? w + y : max(w, y);
+    }
+    if (t < kFinishThreads / kWave) wsum[t] = w;
+  }
+  __syncthreads();
+  const uint32_t before_wave = t >= kWave ? wsum[t / kWave - 1] : 0u;
+  uint32_t before_me = uint32_t(__shfl_up(int(inc), 1, kWave));
+  if (lane == 0) before_me = 0u;  // identity of both sum and max (values >= 0)
+  uint32_t acc = kSum ? before_wave + before_me : max(before_wave, before_me);
+#pragma unroll
+  for (int q = 0; q < kFinishPer; ++q) {
+    if (kSum) {
+      v[kFinishPer * t + q] = acc;
+      acc += x[q];
+    } else {
+      acc = max(acc, x[q]);
+      v[kFinishPer * t + q] = acc;
+    }
+  }
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(kFinishThreads) void order_finish_kernel(
+    uint32_t n0, const uint32_t* __restrict__ act_group, const uint32_t* __restrict__ act_base,
+    const uint32_t* __restrict__ act_depth, const uint32_t* __restrict__ lists,
+    const uint32_t* __restrict__ list_begin, uint32_t end, uint32_t max_len, int lo_bits,
+    GroupBase gb, SigTable perm, uint32_t* __restrict__ status) {
+  extern __shared__ __attribute__((aligned(16))) uint64_t finish_lds[];
+  constexpr int P = kFinishMax;
+  uint64_t* key = finish_lds;                            // [P]
+  uint32_t* grp = reinterpret_cast<uint32_t*>(key + P);  // [P] state by slot
+  uint32_t* bas = grp + P;
+  uint32_t* dep = bas + P;
+  uint32_t* lcp = dep + P;                               // [P] by slot
+  uint32_t* idx = lcp + P;                               // [P] sorted -> slot
+  uint32_t* t0 = idx + P;                                // [P] scratch
+  uint32_t* t1 = t0 + P;                                 // [P] scratch
+  uint32_t* wsum = t1 + P;                               // [kFinishThreads / kWave]
+  static_assert(sizeof(uint64_t) * P + 7 * sizeof(uint32_t) * P +
+                        (kFinishThreads / kWave) * sizeof(uint32_t) == kFinishLds,
+                "LDS layout and kFinishLds disagree");
+  const int t = threadIdx.x;
+  const uint64_t lo_mask = (uint64_t(1) << lo_bits) - 1;
+  const uint64_t end1 = uint64_t(end) + 1u;
+  uint32_t n = n0;
+  for (int e = t; e < P; e += kFinishThreads) {
+    if (uint32_t(e) < n) {
+      grp[e] = act_group[e];
+      bas[e] = act_base[e];
+      dep[e] = act_depth[e];
+    }
+  }
+  __syncthreads();
+  for (uint32_t round = 0; n > 0; ++round) {
+    if (round > n0) {  // cannot happen: every round places each class's reference
+      if (t == 0) status[0] = 1u;
+      return;
+    }
+    // class starts -> class ranks (t0 = head flags, then exclusive ranks)
+    for (int e = t; e < P; e += kFinishThreads)
+      t0[e] = (uint32_t(e) < n && (e == 0 || bas[e] != bas[e - 1])) ? 1u : 0u;
+    __syncthreads();
+    block_scan<true>(t0, wsum);  // t0[e] = classes before e
+    // t1[c] = first slot of class c
+    for (int e = t; e < P; e += kFinishThreads)
+      if (uint32_t(e) < n && (e == 0 || bas[e] != bas[e - 1])) t1[t0[e]] = uint32_t(e);
+    __syncthreads();
+    // divergence from each class's first member; keys (hi << lo_bits | lo)
+    uint64_t k_reg[kFinishPer];
+    uint32_t lcp_reg[kFinishPer];
+#pragma unroll
+    for (int q = 0; q < kFinishPer; ++q) {
+      const int e = t + q * kFinishThreads;
+      k_reg[q] = ~0ull;
+      lcp_reg[q] = 0u;
+      if (uint32_t(e) >= n) continue;
+      const bool head = e == 0 || bas[e] != bas[e - 1];
+      const uint32_t c = head ? t0[e] : t0[e] - 1u;
+      const uint32_t g = grp[e];
+      const uint32_t r = grp[t1[c]];
+      const uint32_t* m = lists + list_begin[g];
+      const uint32_t* rq = lists + list_begin[r];
+      const uint32_t nm = list_begin[g + 1] - list_begin[g];
+      const uint32_t nq = list_begin[r + 1] - list_begin[r];
+      uint32_t d = dep[e];
+      if (g != r)
+        while (d < nm && d < nq && m[d] == rq[d]) ++d;
+      uint32_t side, kk = 0, el = 0;
+      if (g == r || (d == nm && d == nq)) {
+        side = kEq;
+        d = nm;
+      } else if (d == nm) {
+        side = kAfter;
+        kk = max_len - d;
+        el = end;
+      } else if (d == nq || m[d] < rq[d]) {
+        side = kBefore;
+        kk = d;
+        el = m[d];
+      } else {
+        side = kAfter;
+        kk = max_len - d;
+        el = m[d];
+      }
+      k_reg[q] = ((uint64_t(c) * 3u + side) << lo_bits) | (uint64_t(kk) * end1 + el);
+      lcp_reg[q] = d;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kFinishPer; ++q) {
+      const int e = t + q * kFinishThreads;
+      key[e] = k_reg[q];
+      idx[e] = uint32_t(e);
+      lcp[e] = lcp_reg[q];
+    }
+    __syncthreads();
+    // bitonic sort of (key, slot) over the next power of two >= n
+    uint32_t pw = 2;
+    while (pw < n) pw <<= 1;
+    for (uint32_t kb = 2; kb <= pw; kb <<= 1) {
+      for (uint32_t j = kb >> 1; j > 0; j >>= 1) {
+        for (uint32_t e = t; e < pw / 2; e += kFinishThreads) {
+          const uint32_t i = (e / j) * 2 * j + (e % j);
+          const uint32_t l = i + j;
+          const bool asc = (i & kb) == 0;
+          const uint64_t ka = key[i], kl = key[l];
+          const uint32_t ia = idx[i], il = idx[l];
+          const bool greater = ka > kl || (ka == kl && ia > il);
+          if (greater == asc) {
+            key[i] = kl;
+            key[l] = ka;
+            idx[i] = il;
+            idx[l] = ia;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    // run starts (t0) and class starts (t1) of every sorted position
+    for (int e = t; e < P; e += kFinishThreads) {
+      uint32_t rs = 0, cs = 0;
+      if (uint32_t(e) < n) {
+        rs = (e == 0 || key[e] != key[e - 1]) ? uint32_t(e) : 0u;
+        cs = (e == 0 || (key[e] >> lo_bits) / 3u != (key[e - 1] >> lo_bits) / 3u) ? uint32_t(e)
+                                                                                    : 0u;
+      }
+      t0[e] = rs;
+      t1[e] = cs;
+    }
+    __syncthreads();
+    block_scan<false>(t0, wsum);
+    block_scan<false>(t1, wsum);
+    // place or keep
+    uint32_t keep_reg[kFinishPer], ng[kFinishPer], nb[kFinishPer], nd[kFinishPer];
+#pragma unroll
+    for (int q = 0; q < kFinishPer; ++q) {
+      const int j = t + q * kFinishThreads;
+      keep_reg[q] = 0u;
+      if (uint32_t(j) >= n) continue;
+      const uint32_t i = idx[j];
+      const uint32_t hn = t0[j], ho = t1[j];
+      const uint32_t base = bas[i] + (hn - ho);
+      const uint64_t kj = key[j];
+      const bool single = hn == uint32_t(j) && (uint32_t(j) + 1 == n || key[j + 1] != kj);
+      const bool ended = uint32_t((kj >> lo_bits) % 3u) == kEq || (kj & lo_mask) % end1 == end;
+      const uint32_t g = grp[i];
+      if (single || ended) {
+        const int s = workset_of(gb, g);
+        const uint32_t at = base + (uint32_t(j) - hn) - gb.base[s];
+        if (at < uint32_t(perm.groups[s])) perm.p[s][at] = g - gb.base[s];
+        else status[0] = 2u;  // a position outside the workset: never written
+      } else {
+        keep_reg[q] = 1u;
+        ng[q] = g;
+        nb[q] = base;
+        nd[q] = lcp[i] + 1u;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kFinishPer; ++q) t0[t + q * kFinishThreads] = keep_reg[q];
+    __syncthreads();
+    const uint32_t kept_last = t0[P - 1];
+    __syncthreads();
+    block_scan<true>(t0, wsum);
+    const uint32_t next_n = t0[P - 1] + kept_last;
+#pragma unroll
+    for (int q = 0; q < kFinishPer; ++q) {
+      if (!keep_reg[q]) continue;
+      const uint32_t slot = t0[t + q * kFinishThreads];
+      grp[slot] = ng[q];
+      bas[slot] = nb[q];
+      dep[slot] = nd[q];
+    }
+    __syncthreads();
+    n = next_n;
+  }
+}
+
 // or_and[0] |= OR of the keys, or_and[1] &= AND of the keys.
 __global__ void key_span_kernel(const uint64_t* __restrict__ keys, uint32_t n,
                                 unsigned long long* __restrict__ or_and) {
@@ -438,7 +677,8 @@ __global__ void order_resolve_kernel(uint32_t n, const uint32_t* __restrict__ sr
     const uint32_t g = act_group[i];
     if (single || ended) {
       const int s = workset_of(gb, g);
-      perm.p[s][base + (j - hn) - gb.base[s]] = g - gb.base[s];
+      const uint32_t at = base + (j - hn) - gb.base[s];
+      if (at < uint32_t(perm.groups[s])) perm.p[s][at] = g - gb.base[s];  // always, if correct
       keep[j] = 0u;
     } else {
       keep[j] = 1u;
@@ -1205,11 +1445,34 @@ int ps_pre_signature_order(const uint32_t* lists, const uint32_t* list_begin,
   PS_HIP(hipStreamSynchronize(st));
   const int lo_bits = ps::bits_for(uint64_t(max_len) * (uint64_t(end) + 1u) + end);
   uint32_t n = total;
+  // The finisher holds class ranks < kFinishMax in 13 bits of its keys.
+  const bool finisher = 13 + lo_bits <= 64;
+  if (finisher) {
+    const size_t lds = ps::kFinishLds;
+    PS_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&ps::order_finish_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+  }
   // Every round places at least each class's reference, so a class of k
   // groups needs at most k rounds.
   for (uint32_t round = 0; n > 0; ++round) {
     if (round > total)
       return ps::fail(PS_ERR_RUNTIME, "ps_pre_signature_order: refinement did not converge");
+    if (finisher && n <= uint32_t(ps::kFinishMax)) {
+      uint32_t flag = 0;
+      PS_HIP(hipMemsetAsync(max_len_dev, 0, 4, st));
+      const size_t lds = ps::kFinishLds;
+      ps::order_finish_kernel<<<1, ps::kFinishThreads, lds, st>>>(
+          n, act_group, act_base, act_depth, lists, list_begin, end, max_len, lo_bits, gb, out,
+          max_len_dev);
+      PS_LAUNCHED();
+      PS_HIP(hipMemcpyAsync(&flag, max_len_dev, 4, hipMemcpyDeviceToHost, st));
+      PS_HIP(hipStreamSynchronize(st));
+      if (flag)
+        return ps::fail(PS_ERR_RUNTIME, flag == 1u
+                                            ? "ps_pre_signature_order: refinement did not converge"
+                                            : "ps_pre_signature_order: position out of range");
+      break;
+    }
     const unsigned grid = ps::grid_for(n);
     ps::order_class_heads_kernel<<<grid, ps::kThreads, 0, st>>>(act_base, n, head);
     PS_LAUNCHED();
