@@ -36,6 +36,67 @@ void ThrowOnError(int status) {
   throw std::runtime_error(msg);
 }
 
+namespace {
+
+#if defined(__GLIBCXX__) && defined(_OPENMP)
+// libstdc++'s std::sort (bits/stl_algo.h) runs an introsort loop that
+// partitions a range, sorts the part right of the cut, then continues on the
+// part left of it, and finishes with one insertion-sort pass over the whole
+// range. The two parts of a cut never interact, so sorting the right parts of
+// the upper levels as concurrent tasks makes exactly the same element moves
+// as the sequential call: the order, ties included, is std::sort's. Every
+// step is the library's own (partition, sub-range loop, heap-sort fallback,
+// final insertion pass); only the dispatch of independent sub-ranges is here.
+constexpr long kSpawnBelow = 1 << 15;  // smaller right parts stay on the thread
+constexpr int kSpawnDepth = 8;
+
+template <typename It, typename Size, typename Cmp>
+void IntrosortTasks(It first, It last, Size depth, Cmp cmp, int spawn) {
+  while (last - first > 16) {  // std::sort's insertion-sort threshold
+    if (spawn <= 0) {
+      std::__introsort_loop(first, last, depth, cmp);
+      return;
+    }
+    if (depth == 0) {
+      std::__partial_sort(first, last, last, cmp);
+      return;
+    }
+    --depth;
+    It cut = std::__unguarded_partition_pivot(first, last, cmp);
+    if (last - cut >= kSpawnBelow) {
+#pragma omp task firstprivate(cut, last, depth, cmp, spawn)
+      IntrosortTasks(cut, last, depth, cmp, spawn - 1);
+    } else {
+      std::__introsort_loop(cut, last, depth, cmp);
+    }
+    last = cut;
+    --spawn;
+  }
+}
+
+template <typename It, typename Less>
+void SameOrderAsStdSort(It first, It last, Less less) {
+  if (first == last) return;
+  auto cmp = __gnu_cxx::__ops::__iter_comp_iter(less);
+  const auto depth = std::__lg(last - first) * 2;
+  if (last - first < 4 * kSpawnBelow) {
+    std::sort(first, last, less);
+    return;
+  }
+#pragma omp parallel
+#pragma omp single
+  IntrosortTasks(first, last, depth, cmp, kSpawnDepth);
+  std::__final_insertion_sort(first, last, cmp);
+}
+#else
+template <typename It, typename Less>
+void SameOrderAsStdSort(It first, It last, Less less) {
+  std::sort(first, last, less);
+}
+#endif
+
+}  // namespace
+
 int GenerateSigBitFFC(int cols, const int* col_nnz, int ffc, int* sigbit) {
   // The reference sorts iota by col_nnz descending with libstdc++ std::sort
   // (unstable, matrix_utils.cu:70-75). Sorting (count, column) records with a
@@ -48,8 +109,8 @@ int GenerateSigBitFFC(int cols, const int* col_nnz, int ffc, int* sigbit) {
   };
   std::vector<Rec> order(static_cast<size_t>(cols));
   for (int c = 0; c < cols; ++c) order[size_t(c)] = Rec{col_nnz[c], c};
-  std::sort(order.begin(), order.end(),
-            [](const Rec& a, const Rec& b) { return a.count > b.count; });
+  SameOrderAsStdSort(order.begin(), order.end(),
+                     [](const Rec& a, const Rec& b) { return a.count > b.count; });
   // FFC buckets (matrix_utils.cu:91-118): the ffc most frequent columns take
   // bit 0 and define the bucket mass; each later bucket takes at least one
   // column and keeps taking columns while its running mass stays below it.

@@ -38,8 +38,12 @@ def test_every_declared_symbol_is_exported(header, libpath):
 
 
 def test_sigbit_matches_oracle_with_ties():
+    # With one distinct count every bucket after the head holds one column, so
+    # equal bits mean the same sorted order, ties included. Sizes from 200000
+    # up take the product's multi-threaded path, whose order must still be
+    # libstdc++ std::sort's.
     rng = np.random.default_rng(11)
-    for n in (5, 17, 100, 1000, 50000):
+    for n in (5, 17, 100, 1000, 50000, 200000, 1000000, 3000000):
         for distinct in (1, 3, 50):
             counts = rng.integers(0, distinct, size=n).astype(np.int32) * 7
             s1, l1 = ps.generate_sigbit(counts)
