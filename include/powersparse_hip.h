@@ -74,6 +74,13 @@ int ps_free(void* ptr);
 int ps_memcpy_htod(void* dst, const void* src, size_t bytes);
 int ps_memcpy_dtoh(void* dst, const void* src, size_t bytes);
 int ps_memcpy_dtod_async(void* dst, const void* src, size_t bytes, ps_stream_t stream);
+/* Page-locked host memory (hipHostMalloc) and asynchronous host-to-device
+ * copies from it: the staging path of the CSR upload (the reference copies
+ * from pageable memory with thrust, matrix_utils.cu:495-497). src of
+ * ps_memcpy_htod_async must stay untouched until the copy completes. */
+int ps_host_malloc(void** ptr, size_t bytes);
+int ps_host_free(void* ptr);
+int ps_memcpy_htod_async(void* dst, const void* src, size_t bytes, ps_stream_t stream);
 /* Replaces: cudaMemset (benchmark_utils.h:29). */
 int ps_memset_async(void* dst, int value, size_t bytes, ps_stream_t stream);
 /* Fills count floats with a counter-based hash of (seed, index): uniform in

@@ -76,6 +76,9 @@ HIP_API = [
     ("ps_free", ctypes.c_int, [c_void_p]),
     ("ps_memcpy_htod", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t]),
     ("ps_memcpy_dtoh", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t]),
+    ("ps_host_malloc", ctypes.c_int, [ctypes.POINTER(c_void_p), ctypes.c_size_t]),
+    ("ps_host_free", ctypes.c_int, [c_void_p]),
+    ("ps_memcpy_htod_async", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
     ("ps_memcpy_dtod_async", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
     ("ps_memset_async", ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_size_t, c_void_p]),
     ("ps_fill_random_async", ctypes.c_int,

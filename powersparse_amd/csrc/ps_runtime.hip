@@ -222,6 +222,26 @@ int ps_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
   return PS_OK;
 }
 
+int ps_host_malloc(void** ptr, size_t bytes) {
+  PS_CHECK_ARG(ptr, "ps_host_malloc: null output");
+  *ptr = nullptr;
+  if (bytes == 0) return PS_OK;
+  PS_HIP(hipHostMalloc(ptr, bytes, hipHostMallocDefault));
+  return PS_OK;
+}
+
+int ps_host_free(void* ptr) {
+  if (ptr) PS_HIP(hipHostFree(ptr));
+  return PS_OK;
+}
+
+int ps_memcpy_htod_async(void* dst, const void* src, size_t bytes, ps_stream_t stream) {
+  if (bytes == 0) return PS_OK;
+  PS_CHECK_ARG(dst && src, "ps_memcpy_htod_async: null pointer");
+  PS_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ps::to_hip(stream)));
+  return PS_OK;
+}
+
 int ps_memcpy_dtod_async(void* dst, const void* src, size_t bytes, ps_stream_t stream) {
   if (bytes == 0) return PS_OK;
   PS_CHECK_ARG(dst && src, "ps_memcpy_dtod_async: null pointer");

@@ -22,6 +22,7 @@
 
 #include "device_buffer.h"
 #include "preprocess_host.h"
+#include "staged_upload.h"
 
 #ifdef _OPENMP
 #include <omp.h>
@@ -280,9 +281,9 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
 
   DeviceArray<int> d_rp(static_cast<size_t>(rows) + 1), d_ci(static_cast<size_t>(nnz));
   DeviceArray<float> d_sv(static_cast<size_t>(nnz));
-  d_rp.Upload(row_ptr, size_t(rows) + 1);
-  d_ci.Upload(col_ind, size_t(nnz));
-  d_sv.Upload(sp_data, size_t(nnz));
+  StagedUpload(d_rp.data(), row_ptr, sizeof(int) * (size_t(rows) + 1));
+  StagedUpload(d_ci.data(), col_ind, sizeof(int) * size_t(nnz));
+  StagedUpload(d_sv.data(), sp_data, sizeof(float) * size_t(nnz));
   clock.Mark(&PreprocessTimings::upload_ms);
 
   // Worksets S (AnalyzeMatrix) and the column histogram.

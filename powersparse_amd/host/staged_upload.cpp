@@ -1,0 +1,90 @@
+// Pipelined host-to-device upload (see staged_upload.h).
+#include "staged_upload.h"
+
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+
+#include "matrix_utils.h"
+
+namespace PowerSparse {
+namespace {
+
+constexpr size_t kChunk = size_t(32) << 20;       // bytes per DMA
+constexpr size_t kMinStaged = size_t(64) << 20;   // smaller copies: one plain copy
+constexpr size_t kCopyBlock = size_t(1) << 20;    // host-copy work item
+
+// Two page-locked buffers shared by every upload of the process (allocated on
+// first use, kept until exit); one upload at a time uses them.
+struct StagingPool {
+  std::mutex mu;
+  void* buf[2] = {nullptr, nullptr};
+  bool tried = false;
+};
+
+StagingPool& Pool() {
+  static StagingPool* pool = new StagingPool;  // never destroyed: outlives every upload
+  return *pool;
+}
+
+void ParallelCopy(void* dst, const void* src, size_t bytes) {
+  const long long blocks = (long long)((bytes + kCopyBlock - 1) / kCopyBlock);
+#pragma omp parallel for schedule(static)
+  for (long long b = 0; b < blocks; ++b) {
+    const size_t off = size_t(b) * kCopyBlock;
+    std::memcpy(static_cast<char*>(dst) + off, static_cast<const char*>(src) + off,
+                std::min(kCopyBlock, bytes - off));
+  }
+}
+
+// Waits for the null stream on scope exit, so that no DMA still reads a
+// staging buffer when the pool is released (also on an error path).
+struct DrainOnExit {
+  ~DrainOnExit() { (void)ps_stream_synchronize(nullptr); }
+};
+
+struct Events {
+  ps_event_t e[2] = {nullptr, nullptr};
+  ~Events() {
+    for (ps_event_t x : e)
+      if (x) (void)ps_event_destroy(x);
+  }
+};
+
+}  // namespace
+
+void StagedUpload(void* dst, const void* src, size_t bytes) {
+  if (bytes < kMinStaged) {
+    ThrowOnError(ps_memcpy_htod(dst, src, bytes));
+    return;
+  }
+  StagingPool& pool = Pool();
+  std::lock_guard<std::mutex> lock(pool.mu);
+  if (!pool.tried) {
+    pool.tried = true;
+    for (void*& b : pool.buf) {
+      if (ps_host_malloc(&b, kChunk) != PS_OK) b = nullptr;
+    }
+  }
+  if (!pool.buf[0] || !pool.buf[1]) {  // no page-locked memory: plain copy
+    ThrowOnError(ps_memcpy_htod(dst, src, bytes));
+    return;
+  }
+  Events ev;
+  for (ps_event_t& x : ev.e) ThrowOnError(ps_event_create(&x));
+  DrainOnExit drain;
+  const char* s = static_cast<const char*>(src);
+  char* d = static_cast<char*>(dst);
+  size_t k = 0;
+  for (size_t off = 0; off < bytes; off += kChunk, ++k) {
+    const int b = int(k & 1);
+    const size_t len = std::min(kChunk, bytes - off);
+    if (k >= 2) ThrowOnError(ps_event_synchronize(ev.e[b]));  // buffer b's DMA is done
+    ParallelCopy(pool.buf[b], s + off, len);
+    ThrowOnError(ps_memcpy_htod_async(d + off, pool.buf[b], len, nullptr));
+    ThrowOnError(ps_event_record(ev.e[b], nullptr));
+  }
+  ThrowOnError(ps_stream_synchronize(nullptr));
+}
+
+}  // namespace PowerSparse
