@@ -36,9 +36,45 @@ __global__ void degree_sums_kernel(const int* __restrict__ row_ptr, int rows,
   if (threadIdx.x < 32 && acc[threadIdx.x]) atomicAdd(&sums[threadIdx.x], acc[threadIdx.x]);
 }
 
-__global__ void col_hist_kernel(const int* __restrict__ col_ind, int nnz, int* __restrict__ col_nnz) {
-  for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < nnz; p += gridDim.x * blockDim.x)
-    atomicAdd(&col_nnz[col_ind[p]], 1);
+// Column histogram. Each workgroup counts a chunk of kHistChunk nonzeros in
+// an LDS hash table first (keys = column + 1, bounded linear probing) and
+// adds each distinct column's count to the global histogram once: hub
+// columns, which appear in most rows, then cost one global atomic per chunk
+// instead of one per nonzero. Nonzeros that find no slot add directly.
+constexpr int kHistSlots = 4096;
+constexpr int kHistChunk = 16384;
+constexpr int kHistProbes = 8;
+
+__global__ __launch_bounds__(kThreads) void col_hist_kernel(const int* __restrict__ col_ind,
+                                                            int nnz, int* __restrict__ col_nnz) {
+  __shared__ uint32_t key[kHistSlots];
+  __shared__ uint32_t cnt[kHistSlots];
+  for (int i = threadIdx.x; i < kHistSlots; i += blockDim.x) {
+    key[i] = 0u;
+    cnt[i] = 0u;
+  }
+  __syncthreads();
+  const long long first = (long long)blockIdx.x * kHistChunk;
+  const long long last = first + kHistChunk < nnz ? first + kHistChunk : nnz;
+  for (long long p = first + threadIdx.x; p < last; p += blockDim.x) {
+    const int c = col_ind[p];
+    const uint32_t k = uint32_t(c) + 1u;
+    uint32_t h = (k * 2654435761u) >> (32 - 12);  // 12 bits: kHistSlots slots
+    bool counted = false;
+    for (int probe = 0; probe < kHistProbes; ++probe) {
+      const uint32_t prev = atomicCAS(&key[h], 0u, k);
+      if (prev == 0u || prev == k) {
+        atomicAdd(&cnt[h], 1u);
+        counted = true;
+        break;
+      }
+      h = (h + 1) & (kHistSlots - 1);
+    }
+    if (!counted) atomicAdd(&col_nnz[c], 1);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kHistSlots; i += blockDim.x)
+    if (key[i]) atomicAdd(&col_nnz[key[i] - 1u], int(cnt[i]));
 }
 
 // Row of position p: the last r with row_ptr[r] <= p (binary search).
@@ -1011,8 +1047,9 @@ int ps_pre_degree_sums(const int* row_ptr, int rows, unsigned long long* sums_ho
 
 int ps_pre_col_histogram(const int* col_ind, int nnz, int* col_nnz, ps_stream_t stream) {
   PS_CHECK_ARG(col_ind && col_nnz && nnz > 0, "ps_pre_col_histogram: bad argument");
-  ps::col_hist_kernel<<<ps::grid_for(size_t(nnz)), ps::kThreads, 0, ps::to_hip(stream)>>>(
-      col_ind, nnz, col_nnz);
+  static_assert(ps::kHistSlots == 1 << 12, "col_hist_kernel hashes to 12 bits");
+  const unsigned chunks = unsigned((size_t(nnz) + ps::kHistChunk - 1) / ps::kHistChunk);
+  ps::col_hist_kernel<<<chunks, ps::kThreads, 0, ps::to_hip(stream)>>>(col_ind, nnz, col_nnz);
   PS_LAUNCHED();
   return PS_OK;
 }
