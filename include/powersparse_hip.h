@@ -247,6 +247,17 @@ int ps_pre_rank_keys(const int* row_ptr, int rows, const int* col_ind, int nnz,
                      const int* col_nnz, int max_count, int count_bits, uint64_t* keys,
                      uint32_t* vals, ps_stream_t stream);
 
+/* The ranking itself, row by row: writes keys / vals as the stable sort of
+ * ps_pre_rank_keys' output by key would (row << count_bits | max_count -
+ * col_nnz[col], CSR position), sorting only inside rows (rows arrive in
+ * order): one wave per row up to 256 nonzeros, an LDS bitonic sort per row up
+ * to 8192, a radix sort over the elements of longer rows. count_bits <= 32.
+ * Synchronises the stream.
+ * Replaces: thrust::sort of NNZPoint (matrix_utils.cu:518-524). */
+int ps_pre_rank_sort(const int* row_ptr, int rows, const int* col_ind, int nnz,
+                     const int* col_nnz, int max_count, int count_bits, uint64_t* keys,
+                     uint32_t* vals, ps_stream_t stream);
+
 /* Per-row group counts: counts[s * rows + r] = groups of row r in workset s
  * (s = 0 residue). Replaces: GetGroupNumArray (matrix_utils.cu:132-156). */
 int ps_pre_group_counts(const int* row_ptr, int rows, int group_type_num, int fine,

@@ -139,6 +139,9 @@ HIP_API = [
     ("ps_pre_rank_keys", ctypes.c_int,
      [c_void_p, ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, ctypes.c_int, ctypes.c_int,
       c_void_p, c_void_p, c_void_p]),
+    ("ps_pre_rank_sort", ctypes.c_int,
+     [c_void_p, ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, ctypes.c_int, ctypes.c_int,
+      c_void_p, c_void_p, c_void_p]),
     ("ps_pre_group_counts", ctypes.c_int,
      [c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, c_void_p]),
     ("ps_pre_group_meta", ctypes.c_int,

@@ -99,6 +99,181 @@ __global__ void rank_keys_kernel(const int* __restrict__ row_ptr, int rows,
   }
 }
 
+// ---- ranking each row's nonzeros, row by row ----
+//
+// Rows arrive in order, so ranking only sorts inside each row: by count key
+// (max_count - col_nnz, ascending = column count descending), ties in CSR
+// order. Rows of up to 256 nonzeros: one wave per row, each element's rank
+// counted against the others. 257 .. 8192: one workgroup per row, bitonic sort of
+// (count key, index) pairs in LDS. Longer rows: their elements are compacted
+// and radix-sorted (stable) with the row's list index in the high bits.
+// Output as the stable sort of (row, count key): keys = row << count_bits |
+// count key, vals = CSR position.
+constexpr int kRankTileSmall = 1024, kRankTileLarge = 8192;
+
+__device__ __forceinline__ uint32_t count_key(const int* __restrict__ col_ind,
+                                              const int* __restrict__ col_nnz, int max_count,
+                                              int p) {
+  return uint32_t(max_count - col_nnz[col_ind[p]]);
+}
+
+constexpr int kRankWavePer = 4;  // elements per lane: one wave ranks rows up to 256
+
+__global__ void rank_small_kernel(const int* __restrict__ row_ptr, int rows,
+                                  const int* __restrict__ col_ind,
+                                  const int* __restrict__ col_nnz, int max_count, int count_bits,
+                                  uint64_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+  const int r = blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (r >= rows) return;
+  const int b = row_ptr[r];
+  const int d = row_ptr[r + 1] - b;
+  if (d == 0 || d > kWave * kRankWavePer) return;
+  const int lane = lane_id();
+  // element q * 64 + lane sits in ck[q] of this lane
+  uint32_t ck[kRankWavePer];
+  int rank[kRankWavePer];
+#pragma unroll
+  for (int q = 0; q < kRankWavePer; ++q) {
+    const int j = q * kWave + lane;
+    ck[q] = j < d ? count_key(col_ind, col_nnz, max_count, b + j) : 0xFFFFFFFFu;
+    rank[q] = 0;
+  }
+  const int used = (d + kWave - 1) / kWave;  // element rows of the wave that hold data
+  for (int qo = 0; qo < used; ++qo) {
+    const int kmax = d - qo * kWave < kWave ? d - qo * kWave : kWave;
+    for (int kl = 0; kl < kmax; ++kl) {
+      const int k = qo * kWave + kl;
+      uint32_t other = 0;
+#pragma unroll
+      for (int q = 0; q < kRankWavePer; ++q)
+        if (q == qo) other = uint32_t(__shfl(int(ck[q]), kl, kWave));
+#pragma unroll
+      for (int q = 0; q < kRankWavePer; ++q) {
+        const int j = q * kWave + lane;
+        rank[q] += (other < ck[q] || (other == ck[q] && k < j)) ? 1 : 0;
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kRankWavePer; ++q) {
+    const int j = q * kWave + lane;
+    if (j < d) {
+      keys[b + rank[q]] = (uint64_t(r) << count_bits) | ck[q];
+      vals[b + rank[q]] = uint32_t(b + j);
+    }
+  }
+}
+
+// One workgroup per listed row (degree <= tile).
+__global__ __launch_bounds__(kThreads) void rank_tile_kernel(
+    const uint32_t* __restrict__ row_list, const int* __restrict__ row_ptr,
+    const int* __restrict__ col_ind, const int* __restrict__ col_nnz, int max_count,
+    int count_bits, uint64_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+  extern __shared__ uint64_t pairs[];
+  const int r = int(row_list[blockIdx.x]);
+  const int b = row_ptr[r];
+  const int d = row_ptr[r + 1] - b;
+  int pw = 2;
+  while (pw < d) pw <<= 1;
+  for (int e = threadIdx.x; e < pw; e += blockDim.x)
+    pairs[e] = e < d ? (uint64_t(count_key(col_ind, col_nnz, max_count, b + e)) << 32) | uint32_t(e)
+                     : ~0ull;
+  __syncthreads();
+  for (int k2 = 2; k2 <= pw; k2 <<= 1) {
+    for (int j = k2 >> 1; j > 0; j >>= 1) {
+      for (int e = threadIdx.x; e < pw / 2; e += blockDim.x) {
+        const int i = (e / j) * 2 * j + (e % j);
+        const int l = i + j;
+        const bool asc = (i & k2) == 0;
+        const uint64_t x = pairs[i], y = pairs[l];
+        if ((x > y) == asc) {
+          pairs[i] = y;
+          pairs[l] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int e = threadIdx.x; e < d; e += blockDim.x) {
+    const uint64_t v = pairs[e];
+    keys[b + e] = (uint64_t(r) << count_bits) | (v >> 32);
+    vals[b + e] = uint32_t(b) + uint32_t(v & 0xFFFFFFFFu);
+  }
+}
+
+// Row classes beyond one wave, as flags flag[c * rows + r]: c = 0 up to
+// kRankTileSmall nonzeros, 1 up to kRankTileLarge, 2 longer.
+__global__ void rank_classify_kernel(const int* __restrict__ row_ptr, int rows,
+                                     uint32_t* __restrict__ flag) {
+  for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
+    const int d = row_ptr[r + 1] - row_ptr[r];
+    flag[r] = (d > kWave * kRankWavePer && d <= kRankTileSmall) ? 1u : 0u;
+    flag[size_t(rows) + r] = (d > kRankTileSmall && d <= kRankTileLarge) ? 1u : 0u;
+    flag[2 * size_t(rows) + r] = d > kRankTileLarge ? 1u : 0u;
+  }
+}
+
+// list_c[slot_c[r]] = r for the rows of each class (slots scanned per class).
+__global__ void rank_lists_kernel(int rows, const uint32_t* __restrict__ flag,
+                                  const uint32_t* __restrict__ slot,
+                                  uint32_t* __restrict__ list1, uint32_t* __restrict__ list2,
+                                  uint32_t* __restrict__ list3) {
+  for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < rows; r += gridDim.x * blockDim.x) {
+    if (flag[r]) list1[slot[r]] = uint32_t(r);
+    if (flag[size_t(rows) + r]) list2[slot[size_t(rows) + r]] = uint32_t(r);
+    if (flag[2 * size_t(rows) + r]) list3[slot[2 * size_t(rows) + r]] = uint32_t(r);
+  }
+}
+
+// long_start[i] = degree of long row list[i] (scanned into element offsets).
+__global__ void permute_long_degrees_kernel(const uint32_t* __restrict__ list, uint32_t n,
+                                            const int* __restrict__ row_ptr,
+                                            uint32_t* __restrict__ long_start) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const int r = int(list[i]);
+    long_start[i] = uint32_t(row_ptr[r + 1] - row_ptr[r]);
+  }
+}
+
+// Long rows: compacted keys (list index << count_bits | count key), values =
+// CSR positions; one workgroup per long row.
+__global__ void rank_long_keys_kernel(const uint32_t* __restrict__ list,
+                                      const uint32_t* __restrict__ seg_start,
+                                      const int* __restrict__ row_ptr,
+                                      const int* __restrict__ col_ind,
+                                      const int* __restrict__ col_nnz, int max_count,
+                                      int count_bits, uint64_t* __restrict__ ck,
+                                      uint32_t* __restrict__ cv) {
+  const uint32_t i = blockIdx.x;
+  const int r = int(list[i]);
+  const int b = row_ptr[r];
+  const int d = row_ptr[r + 1] - b;
+  const size_t o = seg_start[i];
+  for (int e = threadIdx.x; e < d; e += blockDim.x) {
+    ck[o + e] = (uint64_t(i) << count_bits) | count_key(col_ind, col_nnz, max_count, b + e);
+    cv[o + e] = uint32_t(b + e);
+  }
+}
+
+// After the stable sort the elements of long row i occupy the same compacted
+// range as before: element j of it goes to row_ptr[row] + (j - seg_start[i]).
+__global__ void rank_long_write_kernel(size_t total, const uint64_t* __restrict__ ck,
+                                       const uint32_t* __restrict__ cv,
+                                       const uint32_t* __restrict__ list,
+                                       const uint32_t* __restrict__ seg_start,
+                                       const int* __restrict__ row_ptr, int count_bits,
+                                       uint64_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+  const uint64_t mask = (uint64_t(1) << count_bits) - 1;
+  for (size_t j = size_t(blockIdx.x) * blockDim.x + threadIdx.x; j < total;
+       j += size_t(gridDim.x) * blockDim.x) {
+    const uint32_t i = uint32_t(ck[j] >> count_bits);
+    const int r = int(list[i]);
+    const size_t out = size_t(row_ptr[r]) + (j - seg_start[i]);
+    keys[out] = (uint64_t(r) << count_bits) | (ck[j] & mask);
+    vals[out] = cv[j];
+  }
+}
+
 // counts[s * (rows + 1) + r]; the extra entry per workset stays 0 so that the
 // exclusive scan leaves the workset's group total at index `rows`.
 __global__ void group_counts_kernel(const int* __restrict__ row_ptr, int rows, int S, int fine,
@@ -1064,6 +1239,104 @@ int ps_pre_rank_keys(const int* row_ptr, int rows, const int* col_ind, int nnz,
   ps::rank_keys_kernel<<<ps::grid_for(size_t(nnz)), ps::kThreads, 0, ps::to_hip(stream)>>>(
       row_ptr, rows, col_ind, nnz, col_nnz, max_count, count_bits, keys, vals);
   PS_LAUNCHED();
+  return PS_OK;
+}
+
+int ps_pre_rank_sort(const int* row_ptr, int rows, const int* col_ind, int nnz,
+                     const int* col_nnz, int max_count, int count_bits, uint64_t* keys,
+                     uint32_t* vals, ps_stream_t stream) {
+  PS_CHECK_ARG(row_ptr && col_ind && col_nnz && keys && vals && nnz > 0 && rows > 0,
+               "ps_pre_rank_sort: bad argument");
+  PS_CHECK_ARG(count_bits >= 0 && count_bits <= 32 &&
+                   count_bits + ps::bits_for(uint64_t(rows - 1)) <= 64,
+               "ps_pre_rank_sort: key does not fit 64 bits");
+  hipStream_t st = ps::to_hip(stream);
+  const size_t R = size_t(rows);
+  using S = ps::Scratch;
+  S ws(S::bytes(3 * R, 4) * 2 + S::bytes(R, 4) * 3 + S::bytes(R + 1, 4) +
+       ps_scan_workspace_bytes(R + 1));
+  PS_HIP(ws.error());
+  uint32_t* flag = ws.take<uint32_t>(3 * R);
+  uint32_t* slot = ws.take<uint32_t>(3 * R);
+  uint32_t* list1 = ws.take<uint32_t>(R);
+  uint32_t* list2 = ws.take<uint32_t>(R);
+  uint32_t* list3 = ws.take<uint32_t>(R);
+  uint32_t* long_start = ws.take<uint32_t>(R + 1);
+  void* scan_ws = ws.take<char>(ps_scan_workspace_bytes(R + 1));
+  // rows of up to 64 nonzeros
+  {
+    const unsigned waves = ps::kThreads / ps::kWave;
+    ps::rank_small_kernel<<<unsigned((R + waves - 1) / waves), ps::kThreads, 0, st>>>(
+        row_ptr, rows, col_ind, col_nnz, max_count, count_bits, keys, vals);
+    PS_LAUNCHED();
+  }
+  // lists of the longer rows, per class
+  ps::rank_classify_kernel<<<ps::grid_for(R), ps::kThreads, 0, st>>>(row_ptr, rows, flag);
+  PS_LAUNCHED();
+  for (int c = 0; c < 3; ++c) {
+    const int rc = ps_exclusive_scan_u32(flag + c * R, slot + c * R, R, scan_ws, stream);
+    if (rc != PS_OK) return rc;
+  }
+  ps::rank_lists_kernel<<<ps::grid_for(R), ps::kThreads, 0, st>>>(rows, flag, slot, list1, list2,
+                                                                   list3);
+  PS_LAUNCHED();
+  uint32_t tail_slot[3], tail_flag[3];
+  for (int c = 0; c < 3; ++c) {
+    PS_HIP(hipMemcpyAsync(&tail_slot[c], slot + (c + 1) * R - 1, 4, hipMemcpyDeviceToHost, st));
+    PS_HIP(hipMemcpyAsync(&tail_flag[c], flag + (c + 1) * R - 1, 4, hipMemcpyDeviceToHost, st));
+  }
+  PS_HIP(hipStreamSynchronize(st));
+  const uint32_t n1 = tail_slot[0] + tail_flag[0];
+  const uint32_t n2 = tail_slot[1] + tail_flag[1];
+  const uint32_t n3 = tail_slot[2] + tail_flag[2];
+  int rc = PS_OK;
+  if (n1 > 0) {
+    ps::rank_tile_kernel<<<n1, ps::kThreads, ps::kRankTileSmall * sizeof(uint64_t), st>>>(
+        list1, row_ptr, col_ind, col_nnz, max_count, count_bits, keys, vals);
+    PS_LAUNCHED();
+  }
+  if (n2 > 0) {
+    const size_t lds = size_t(ps::kRankTileLarge) * sizeof(uint64_t);
+    PS_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&ps::rank_tile_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)));
+    ps::rank_tile_kernel<<<n2, ps::kThreads, lds, st>>>(list2, row_ptr, col_ind, col_nnz,
+                                                        max_count, count_bits, keys, vals);
+    PS_LAUNCHED();
+  }
+  if (n3 > 0) {
+    // element offsets of the long rows, in list order
+    PS_HIP(hipMemsetAsync(long_start, 0, (R + 1) * 4, st));
+    ps::permute_long_degrees_kernel<<<ps::grid_for(n3), ps::kThreads, 0, st>>>(
+        list3, n3, row_ptr, long_start);
+    PS_LAUNCHED();
+    rc = ps_exclusive_scan_u32(long_start, long_start, size_t(n3) + 1, scan_ws, stream);
+    if (rc != PS_OK) return rc;
+    uint32_t total = 0;
+    PS_HIP(hipMemcpyAsync(&total, long_start + n3, 4, hipMemcpyDeviceToHost, st));
+    PS_HIP(hipStreamSynchronize(st));
+    const int list_bits = ps::bits_for(uint64_t(n3 - 1));
+    PS_CHECK_ARG(list_bits + count_bits <= 64, "ps_pre_rank_sort: key does not fit 64 bits");
+    S lw(2 * S::bytes(total, 8) + 2 * S::bytes(total, 4) + ps_radix_workspace_bytes(total));
+    PS_HIP(lw.error());
+    uint64_t* ck = lw.take<uint64_t>(total);
+    uint64_t* ck_alt = lw.take<uint64_t>(total);
+    uint32_t* cv = lw.take<uint32_t>(total);
+    uint32_t* cv_alt = lw.take<uint32_t>(total);
+    void* radix_ws = lw.take<char>(ps_radix_workspace_bytes(total));
+    ps::rank_long_keys_kernel<<<n3, ps::kThreads, 0, st>>>(list3, long_start, row_ptr, col_ind,
+                                                           col_nnz, max_count, count_bits, ck, cv);
+    PS_LAUNCHED();
+    int alt = 0;
+    rc = ps_radix_sort_pairs_u64(ck, ck_alt, cv, cv_alt, total, 0, list_bits + count_bits,
+                                 radix_ws, &alt, stream);
+    if (rc != PS_OK) return rc;
+    ps::rank_long_write_kernel<<<ps::grid_for(total), ps::kThreads, 0, st>>>(
+        total, alt ? ck_alt : ck, alt ? cv_alt : cv, list3, long_start, row_ptr, count_bits,
+        keys, vals);
+    PS_LAUNCHED();
+    PS_HIP(hipStreamSynchronize(st));
+  }
+  PS_HIP(hipStreamSynchronize(st));
   return PS_OK;
 }
 

@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <future>
 #include <cmath>
 #include <cstring>
 #include <numeric>
@@ -300,28 +301,19 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
   const int max_count = *std::max_element(col_nnz.begin(), col_nnz.end());
   clock.Mark(&PreprocessTimings::analyze_ms);
 
-  // Device work that does not need the column signature bits is enqueued
-  // first and the host computes the bits meanwhile: nothing in between waits
-  // for the device (the workspaces stay alive until after the host step).
-  //
+  // Host: the column signature bits, on a thread of their own while this
+  // thread drives the device work that does not need them (joined below).
+  std::vector<int> sigbit(static_cast<size_t>(cols));
+  std::future<int> sig_len = std::async(std::launch::async, [&sigbit, &col_nnz, cols] {
+    return GenerateSigBitFFC(cols, col_nnz.data(), 2, sigbit.data());
+  });
+
   // Rank every row's nonzeros by column count (descending, ties in CSR order).
   const int count_bits = BitsFor(uint64_t(max_count));
-  const int row_bits = BitsFor(uint64_t(rows - 1));
-  DeviceArray<uint64_t> keys(static_cast<size_t>(nnz)), keys_alt(static_cast<size_t>(nnz));
-  DeviceArray<uint32_t> vals(static_cast<size_t>(nnz)), vals_alt(static_cast<size_t>(nnz));
-  DeviceArray<char> rank_ws(ps_radix_workspace_bytes(size_t(nnz)));
-  ThrowOnError(ps_pre_rank_keys(d_rp.data(), rows, d_ci.data(), nnz, d_cn.data(), max_count,
+  DeviceArray<uint64_t> keys(static_cast<size_t>(nnz));
+  DeviceArray<uint32_t> vals(static_cast<size_t>(nnz));
+  ThrowOnError(ps_pre_rank_sort(d_rp.data(), rows, d_ci.data(), nnz, d_cn.data(), max_count,
                                 count_bits, keys.data(), vals.data(), st));
-  {
-    int alt = 0;
-    ThrowOnError(ps_radix_sort_pairs_u64(keys.data(), keys_alt.data(), vals.data(),
-                                         vals_alt.data(), size_t(nnz), 0,
-                                         count_bits + row_bits, rank_ws.data(), &alt, st));
-    if (alt) {
-      std::swap(keys, keys_alt);
-      std::swap(vals, vals_alt);
-    }
-  }
   clock.Mark(&PreprocessTimings::rank_ms);
 
   // Group counts per workset, on the host from row_ptr (the split the device
@@ -404,13 +396,9 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
     }
   }
 
-  // Host: column signature bits, while the device works.
-  std::vector<int> sigbit(static_cast<size_t>(cols));
-  _signature_len = GenerateSigBitFFC(cols, col_nnz.data(), 2, sigbit.data());
+  // Join the host thread (sigbit_ms: the time spent waiting for it here).
+  _signature_len = sig_len.get();
   clock.Mark(&PreprocessTimings::sigbit_ms);
-  keys_alt.Reset();
-  vals_alt.Reset();
-  rank_ws.Reset();
 
   // Groups in signature order: perm[s][k] = initial group at position k.
   const int words = _signature_len / 32;

@@ -182,3 +182,42 @@ def test_signature_order_two_pass_keys():
     got = run_order([sets[: n // 2], sets[n // 2:]], length)
     np.testing.assert_array_equal(got[0], oracle.order_bit_lists(sets[: n // 2]))
     np.testing.assert_array_equal(got[1], oracle.order_bit_lists(sets[n // 2:]))
+
+
+def test_rank_sort_row_classes():
+    # every row-length class of ps_pre_rank_sort (one wave up to 256, LDS tiles
+    # of 1024 and 8192, radix for longer rows) against numpy's stable sort by
+    # (row, count key); few distinct column counts, so most keys tie
+    import ctypes
+    from powersparse_amd import _native
+    setup()
+    rng = np.random.default_rng(23)
+    degrees = [0, 1, 5, 64, 65, 200, 256, 257, 300, 1024, 1025, 5000, 8192, 8193, 20000, 0, 33,
+               9000]
+    degrees += rng.integers(0, 150, 3000).tolist()
+    cols = 30000
+    pool = rng.choice(cols, 400, replace=False)  # columns concentrated on a few hundred
+    ci = []
+    for d in degrees:
+        if d <= 300:
+            row = rng.choice(pool, d, replace=False)
+        else:
+            row = rng.choice(cols, d, replace=False)
+        ci.append(np.sort(row))
+    ci = np.concatenate(ci).astype(np.int32)
+    rp = np.concatenate([[0], np.cumsum(degrees)]).astype(np.int32)
+    rows, nnz = len(degrees), ci.size
+    cn = np.bincount(ci, minlength=cols).astype(np.int32)
+    max_count = int(cn.max())
+    cb = max_count.bit_length()
+    row_of = np.repeat(np.arange(rows), np.diff(rp))
+    ckey = (max_count - cn[ci]).astype(np.uint64)
+    order = np.lexsort((np.arange(nnz), ckey, row_of))  # stable by (row, key)
+    exp_keys = (row_of[order].astype(np.uint64) << np.uint64(cb)) | ckey[order]
+    d_rp, d_ci, d_cn = (ps.DeviceBuffer(host=a) for a in (rp, ci, cn))
+    keys = ps.DeviceBuffer(nnz * 8)
+    vals = ps.DeviceBuffer(nnz * 4)
+    ps._hip_call(_native.hip().ps_pre_rank_sort(d_rp.ptr, rows, d_ci.ptr, nnz, d_cn.ptr,
+                                                max_count, cb, keys.ptr, vals.ptr, None))
+    np.testing.assert_array_equal(vals.download(np.uint32), order.astype(np.uint32))
+    np.testing.assert_array_equal(keys.download(np.uint64), exp_keys)
