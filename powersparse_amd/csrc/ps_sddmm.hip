@@ -14,17 +14,15 @@
 //
 // Reference behaviour kept (PowerSparse_SDDMM/sddmm_solution.cu:7-50,
 // sddmm_kernel_block.cu:155-164, sddmm_kernel_residue.cu:295-305): block
-// outputs are stored, residue outputs are added into out[0] (the reference
-// uses atomicAdd; every output position belongs to exactly one nonzero, so
-// here one lane adds with a plain read-modify-write, coalesced across the
-// wave, same result), the output is in workset order.
+// outputs are stored, residue outputs are added atomically into out[0], the
+// output is in workset order.
 //
 // Store modes (kMode): 0 = at the nonzero's own position (as above); 1 = per
 // nonzero map, out[s][map[s][p]]: CSR order (every out[s] is the one
 // CSR-order array, map = CSR positions, plain stores: each position is
 // written once, no zeroing needed); 2 = per group base, out[s][base[s][g] + j]
 // for member j of group g: a row-ordered execution copy of the worksets
-// writing the public workset layout (residue results still added).
+// writing the public workset layout (residue results still added atomically).
 #include "ps_common.hpp"
 
 namespace ps {
@@ -186,10 +184,10 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
         const float v = dot * ws.sp_data[beg + k];
         if constexpr (kMode != 0) {
           const int at = kMode == 1 ? out_pos[beg + k] : out_pos[g] + k;
-          if (args.residue_add) out[at] += v;
+          if (args.residue_add) unsafeAtomicAdd(out + at, v);
           else out[at] = v;
         } else {
-          out[beg + k] += v;
+          unsafeAtomicAdd(out + beg + k, v);
         }
       }
     }
