@@ -4,7 +4,8 @@
 One step = one pass of the hot path over the synthetic BASELINE graph (config
 C1 by default: Chung-Lu n = 1e6, gamma 2.1, mean degree 50, degree clip 5e4,
 values U(0,1); C2's SDDMM uses the same pattern): SpMM at N = 32, SpMM at
-N = 128 and SDDMM at N = 128, each one fused launch covering every workset,
+N = 128, SDDMM at N = 128 and SDDMM at N = 32 (C2's two widths), each one
+fused launch covering every workset,
 enqueued back to back on one stream with the operands resident in HBM. The
 outputs are not cleared between calls, as in the reference harness
 (benchmarks/benchmark.cu:179-187).
@@ -33,13 +34,13 @@ METRIC = "SpMM/SDDMM GFLOPS + achieved HBM GB/s (% of roofline), N=32/128, 1 GPU
 HBM_PEAK_GBPS = 8000.0
 WORKLOADS = {
     "C1": "C1/C2 power-law graph (Chung-Lu n=1e6, gamma 2.1, mean 50, clip 5e4): "
-          "SpMM N=32 + SpMM N=128 + SDDMM N=128",
+          "SpMM N=32 + SpMM N=128 + SDDMM N=128 + SDDMM N=32",
     "C3": "C3 power-law graph (Chung-Lu n=1.6e6, gamma 1.8, mean 165, clip 1e5): "
           "SpMM N=32 + SpMM N=128 + SDDMM N=128",
     "C4": "C4 community graph (2048 x 1024 nodes, 2% intra, +8 inter, 5% empty, 5% singleton): "
           "SpMM N=64 + SDDMM N=64",
 }
-OPS = {"C1": [("spmm", 32), ("spmm", 128), ("sddmm", 128)],
+OPS = {"C1": [("spmm", 32), ("spmm", 128), ("sddmm", 128), ("sddmm", 32)],
        "C3": [("spmm", 32), ("spmm", 128), ("sddmm", 128)],
        "C4": [("spmm", 64), ("sddmm", 64)]}
 
@@ -55,18 +56,22 @@ def algorithmic_bytes(op, nnz, rows, cols, n):
     return 12 * nnz + 4 * (rows + 1) + 4 * n * rows + 4 * n * cols  # + outputs
 
 
-def measured_traffic(config, op, n):
-    """HBM bytes per launch of the operator kernel, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary of the same workload
+def measured_counters(config, op, n):
+    """From the committed rocprofv3 summary of the same workload
     (profiles/traffic_<config>.json, made by `python -m powersparse_amd.perf
-    summarize`), or None when no summary exists."""
+    summarize`): HBM bytes per launch of the operator kernel (FETCH_SIZE +
+    WRITE_SIZE), its L2 hit rate and VALU figures (None where absent), and the
+    summary's path."""
     path = os.path.join(ROOT, "profiles", f"traffic_{config}.json")
     try:
         with open(path) as fh:
-            t = json.load(fh)["traffic"][f"{op}_N{n}"]
-        return t["traffic_bytes"], os.path.relpath(path, ROOT)
-    except (OSError, KeyError, ValueError):
-        return None, None
+            summary = json.load(fh)
+    except (OSError, ValueError):
+        return None, {}, None
+    key = f"{op}_N{n}"
+    traffic = summary.get("traffic", {}).get(key, {}).get("traffic_bytes")
+    counters = summary.get("counters", {}).get(key, {})
+    return traffic, counters, os.path.relpath(path, ROOT)
 
 
 def cpu_baseline(csr, host_ops, reps=3):
@@ -186,7 +191,7 @@ def main():
             f"{detail[-1]['alg_GBps']:.0f} GB/s ({100 * detail[-1]['roofline_frac']:.1f}% of 8 TB/s)")
     dom = max(detail, key=lambda d: d["ms"])
     kernel = "ps::spmm_kernel" if dom["op"] == "spmm" else "ps::sddmm_kernel"
-    traffic, traffic_src = measured_traffic(args.config, dom["op"], dom["N"])
+    traffic, counters, traffic_src = measured_counters(args.config, dom["op"], dom["N"])
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -222,6 +227,9 @@ def main():
         "roofline": {"bound": "hbm", "kernel": kernel, "op": f"{dom['op']} N={dom['N']}",
                      "achieved": dom["alg_GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": dom["roofline_frac"], "traffic": traffic,
+                     "l2_hit_pct": counters.get("l2_hit_pct"),
+                     "valu_busy_pct": counters.get("valu_busy_pct"),
+                     "valu_utilization_pct": counters.get("valu_utilization_pct"),
                      "traffic_source": traffic_src},
         "cpu_baseline": cpu,
     }

@@ -124,13 +124,19 @@ int ps_stream_wait_event(ps_stream_t stream, ps_event_t event);
 
 /* One workset as the kernels read it. For s == 0 (residue) group_size is 0 and
  * the group extents come from residue_offset; for s > 0 every group holds
- * group_size = 32 * 2^(s-1) nonzeros (utils/matrix_utils.h:8). */
+ * group_size = 32 * 2^(s-1) nonzeros (utils/matrix_utils.h:8).
+ * order (residue workset only, may be NULL): a permutation of its group_num
+ * groups giving the order in which the operators run them, e.g. to visit the
+ * groups of neighbouring rows together; results do not depend on it beyond the
+ * order of FP32 atomic additions. NULL runs the groups as stored.
+ * No reference counterpart. */
 typedef struct ps_workset {
   const int* col_ind;     /* WorksetColInd()[s]  (matrix_utils.h:36) */
   const float* sp_data;   /* WorksetSpData()[s]  (matrix_utils.h:37) */
   const int* group_des;   /* GroupDestination()[s] (matrix_utils.h:38) */
   int group_num;          /* GroupNum()[s] (matrix_utils.h:35) */
   int group_size;
+  const int* order;
 } ps_workset;
 
 /* SpMM C += A * B over all worksets in ONE launch on `stream`, FP32, B (cols x N)

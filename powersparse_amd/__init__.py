@@ -564,8 +564,10 @@ def WorksetToCSR(matrix, values_gpu, out_csr_gpu, stream=None):
 
 def _workset_array(worksets):
     arr = (Workset * max(len(worksets), 1))()
-    for i, (col, val, des, groups, size) in enumerate(worksets):
-        arr[i] = Workset(_ptr(col), _ptr(val), _ptr(des), int(groups), int(size))
+    for i, w in enumerate(worksets):
+        col, val, des, groups, size = w[:5]
+        order = w[5] if len(w) > 5 else None  # residue run order (optional)
+        arr[i] = Workset(_ptr(col), _ptr(val), _ptr(des), int(groups), int(size), _ptr(order))
     return arr
 
 

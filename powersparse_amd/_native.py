@@ -58,6 +58,7 @@ class Workset(ctypes.Structure):
         ("group_des", c_void_p),
         ("group_num", ctypes.c_int),
         ("group_size", ctypes.c_int),
+        ("order", c_void_p),
     ]
 
 

@@ -53,6 +53,13 @@ constexpr int kWave = 64;
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// Makes one wave's LDS writes visible to its own later LDS reads.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Cross-lane float moves inside a wave64. Masks 1 and 2 use DPP quad permutes,
 // 8 uses a DPP row rotate (xor 8 inside each 16-lane row), 4 and 16 use
 // ds_swizzle in bit mode (xor inside 32-lane halves), 32 uses ds_bpermute.

@@ -3,7 +3,10 @@
 // One launch covers every workset. Wave tasks:
 //   block workset: 64 consecutive stored nonzeros (one group when GS >= 64, two
 //     groups of 32 when GS == 32);
-//   residue workset: 64 / RCAP groups per wave, RCAP lanes per group.
+//   residue workset: 8 groups per wave, one slot per group, taken in the
+//     workset's run order (ps_workset.order: longest groups first, so the
+//     groups sharing a wave have about the same length and few lanes idle);
+//     a slot walks its group 8 nonzeros at a time, columns staged in LDS.
 // Lanes form slots of 8; slot q owns 8 consecutive nonzeros and each lane of the
 // slot holds K / 8 features of X (float4 pieces 32 floats apart, so a slot reads
 // a 128-byte line per piece). After the 8 partial dots per lane the slot does a
@@ -29,6 +32,7 @@ namespace ps {
 namespace {
 
 constexpr int kWavesPerBlock = 4;
+constexpr int kStage = 32;  // residue columns staged in LDS per slot
 
 struct SddmmArgs {
   ps_workset ws[PS_MAX_WORKSETS];
@@ -36,7 +40,6 @@ struct SddmmArgs {
   uint32_t task_begin[PS_MAX_WORKSETS + 1];
   int32_t count;
   int32_t N;
-  int32_t rcap;
   uint32_t total_tasks;
   const int* residue_offset;
   const float* lhs;
@@ -105,6 +108,7 @@ __device__ __forceinline__ void slot_dots(const Rows<kBuf>& Y,
 template <int KQ, bool kBuf, int kMode>
 __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs args) {
   constexpr int K = 32 * KQ;
+  __shared__ __attribute__((aligned(16))) int stage[kWavesPerBlock][8 * kStage];
   const uint32_t blk = balanced_block(blockIdx.x, gridDim.x);
   const uint32_t task =
       __builtin_amdgcn_readfirstlane(blk * kWavesPerBlock + threadIdx.x / kWave);
@@ -157,29 +161,51 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
       }
     }
   } else {
-    const int rcap = args.rcap;
-    const int h = lane / rcap, q = lane % rcap;
-    const int g = local * (64 / rcap) + h;
-    const bool has = g < ws.group_num;
+    // One slot per group, groups taken in the workset's run order (longest
+    // first when an order is given, so a wave's groups end together); the
+    // slot's group is walked 8 nonzeros at a time.
+    const int kq = local * 8 + slot;
+    const bool has = kq < ws.group_num;
+    const int g = has ? (ws.order ? ws.order[kq] : kq) : 0;
     const int beg = has ? args.residue_offset[g] : 0;
     const int len = has ? args.residue_offset[g + 1] - beg : 0;
     const int row = has ? ws.group_des[g] : 0;
 #pragma unroll
     for (int qq = 0; qq < KQ; ++qq)
       x[qq] = X.load(Off(uint32_t(row)) * row_bytes + piece + 128u * qq);
-    const int first = (q / 8) * 8;  // first nonzero of this lane's slot in a chunk
-#pragma unroll 1
-    for (int c0 = 0; __any(c0 < len); c0 += rcap) {
-      // nonzeros past the group's end re-read its last column and are dropped
+    // Groups of up to kStage nonzeros (all the preprocessing builds) have their
+    // columns staged in LDS, positions past the end holding the last column;
+    // longer groups read theirs directly.
+    int* const cols_lds = stage[threadIdx.x / kWave] + slot * kStage;
+    const bool staged = len <= kStage;
+    if (staged && len > 0) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int k = c0 + first + j;
-        const int kk = k < len ? k : len - 1;
-        yoff[j] = len > 0 ? Off(uint32_t(ws.col_ind[beg + kk])) * row_bytes + piece : Off(piece);
+      for (int j = sub; j < kStage; j += 8)
+        cols_lds[j] = ws.col_ind[beg + (j < len ? j : len - 1)];
+    }
+    wave_lds_sync();
+#pragma unroll 1
+    for (int c0 = 0; __any(c0 < len); c0 += 8) {
+      // nonzeros past the group's end re-read its last column and are dropped
+      int c[8];
+      if (staged && c0 < kStage) {
+        const int4 lo = *reinterpret_cast<const int4*>(cols_lds + c0);
+        const int4 hi = *reinterpret_cast<const int4*>(cols_lds + c0 + 4);
+        c[0] = lo.x; c[1] = lo.y; c[2] = lo.z; c[3] = lo.w;
+        c[4] = hi.x; c[5] = hi.y; c[6] = hi.z; c[7] = hi.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int k = c0 + j;
+          c[j] = len > 0 ? ws.col_ind[beg + (k < len ? k : len - 1)] : 0;
+        }
       }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        yoff[j] = len > 0 ? Off(uint32_t(c[j])) * row_bytes + piece : Off(piece);
       slot_dots<KQ, kBuf>(Y, yoff, x, p);
       const float dot = slot_transpose_sum(p, sub);
-      const int k = c0 + q;
+      const int k = c0 + sub;
       if (k < len) {
         const float v = dot * ws.sp_data[beg + k];
         if constexpr (kMode != 0) {
@@ -223,7 +249,7 @@ void launch_kq(const SddmmArgs& a, bool buf, int mode, unsigned grid, hipStream_
 int launch(int count, const int* order, const ps_workset* worksets, float* const* outs,
            int mode, const int* const* out_pos, int residue_add, const int* residue_offset,
            int rows,
-           int cols, int N, const float* lhs, const float* rhs, int rcap, hipStream_t stream) {
+           int cols, int N, const float* lhs, const float* rhs, hipStream_t stream) {
   PS_CHECK_ARG(N > 0 && N % 32 == 0 && N <= 512,
                "SDDMM requires N to be a multiple of 32 between 32 and 512");
   PS_CHECK_ARG(int64_t(rows) * N <= INT32_MAX && int64_t(cols) * N <= INT32_MAX,
@@ -233,7 +259,6 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
   SddmmArgs a{};
   a.residue_add = residue_add;
   a.N = N;
-  a.rcap = rcap;
   a.lhs = lhs;
   a.rhs = rhs;
   const uint64_t lhs_bytes = uint64_t(rows) * uint64_t(N) * 4u;
@@ -262,7 +287,7 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
       t = (uint64_t(w.group_num) * w.group_size + 63) / 64;
     } else {
       PS_CHECK_ARG(residue_offset, "Missing residue offsets");
-      t = (uint64_t(w.group_num) + (64 / rcap) - 1) / (64 / rcap);
+      t = (uint64_t(w.group_num) + 7) / 8;  // one slot per group
     }
     a.ws[n] = w;
     if (s == 0) a.ws[n].group_size = 0;
@@ -318,11 +343,8 @@ int ps_sddmm_launch(int workset_count, const ps_workset* worksets, const int* re
     ordered[q] = worksets[workset_count - 1 - q];
     outs[q] = out[workset_count - 1 - q];
   }
-  // A single workset means fine mode (residue groups of at most 16 nonzeros,
-  // utils/matrix_utils.cu:137-141); otherwise residue groups hold at most 31.
-  const int rcap = workset_count == 1 ? 16 : 32;
   return ps::launch(workset_count, order, ordered, outs, 0, nullptr, 0, residue_offset, rows,
-                    cols, N, lhs, rhs, rcap, ps::to_hip(stream));
+                    cols, N, lhs, rhs, ps::to_hip(stream));
 }
 
 int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
@@ -342,9 +364,8 @@ int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
     pos[q] = out_base[workset_count - 1 - q];
     outs[q] = out[workset_count - 1 - q];
   }
-  const int rcap = workset_count == 1 ? 16 : 32;
   return ps::launch(workset_count, order, ordered, outs, 2, pos, 1, residue_offset, rows, cols,
-                    N, lhs, rhs, rcap, ps::to_hip(stream));
+                    N, lhs, rhs, ps::to_hip(stream));
 }
 
 int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
@@ -363,9 +384,8 @@ int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int
     pos[q] = csr_pos[workset_count - 1 - q];
     outs[q] = out_csr;
   }
-  const int rcap = workset_count == 1 ? 16 : 32;
   return ps::launch(workset_count, order, ordered, outs, 1, pos, 0, residue_offset, rows, cols,
-                    N, lhs, rhs, rcap, ps::to_hip(stream));
+                    N, lhs, rhs, ps::to_hip(stream));
 }
 
 int ps_workset_to_csr(int workset_count, const long long* lengths, const int* const* csr_pos,
@@ -392,7 +412,7 @@ int ps_sddmm_workset_launch(int s, const ps_workset* workset, const int* residue
                             float* out, ps_stream_t stream) {
   PS_CHECK_ARG(s >= 0 && s < PS_MAX_WORKSETS && workset, "Invalid SDDMM workset");
   return ps::launch(1, &s, workset, &out, 0, nullptr, 0, residue_offset, rows, cols, N, lhs,
-                    rhs, 32, ps::to_hip(stream));
+                    rhs, ps::to_hip(stream));
 }
 
 }  // extern "C"

@@ -13,10 +13,11 @@
 //     (GS / 32 slots each), otherwise it is a piece of one group. Slots of the
 //     same group are summed with DPP / swizzle butterflies and the group's row
 //     is added to C with atomics.
-//   residue workset: a task is SL consecutive groups, one per slot; a slot
-//     walks its group (at most 31 nonzeros) alone, so no cross-slot sum is
-//     needed, and writes its row with atomics when the row has other groups,
-//     with a plain store otherwise.
+//   residue workset: a task is SL groups of the workset's run order
+//     (ps_workset.order: longest first, so the groups of a wave end together),
+//     one per slot; a slot walks its group (at most 31 nonzeros) alone, so no
+//     cross-slot sum is needed, and writes its row with atomics when the row
+//     has other groups, with a plain store otherwise.
 //
 // Each task first stages its nonzeros in LDS with coalesced loads, as
 // (byte offset of the B row, value) pairs, so the gather loop issues 16
@@ -64,12 +65,6 @@ __device__ __forceinline__ void fma4(float4& acc, float a, const float4& b) {
   acc.y = fmaf(a, b.y, acc.y);
   acc.z = fmaf(a, b.z, acc.z);
   acc.w = fmaf(a, b.w, acc.w);
-}
-
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Sums acc over the `spg` slots of each group (spg a power of two <= SL).
@@ -180,26 +175,25 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs ar
     }
   } else {
     // ------------------------------------------------------- residue groups
-    const int G = ws.group_num;
-    const int g0 = int(local) * SL;
-    const int gend = g0 + SL < G ? g0 + SL : G;
-    const int range_begin = args.residue_offset[g0];
-    const int range_len = args.residue_offset[gend] - range_begin;
-    // Residue groups built by the preprocessing hold at most 31 nonzeros, so
-    // the wave's groups fit the LDS slot area; longer ones are read directly.
-    const bool staged = range_len <= SL * kSlotWords / 2;
+    // Slot q takes group order[local * SL + q] (the workset's run order: longest
+    // groups first, so a wave's groups end together) and stages its (B-row
+    // key, value) pairs in its own LDS area; groups built by the preprocessing
+    // hold at most 31 nonzeros, longer ones are read directly.
+    const int kq = int(local) * SL + slot;
+    const bool has = kq < ws.group_num;
+    const int g = has ? (ws.order ? ws.order[kq] : kq) : 0;
+    const int start = has ? args.residue_offset[g] : 0;
+    const int len = has ? args.residue_offset[g + 1] - start : 0;
+    int* const slot_lds = my_lds + slot * kSlotWords;
+    const bool staged = len <= kSlotWords / 2;
     if (staged) {
-      for (int k = lane; k < range_len; k += kWave) {
-        const int c = ws.col_ind[range_begin + k];
-        const float v = ws.sp_data[range_begin + k];
-        *reinterpret_cast<int2*>(my_lds + 2 * k) = make_int2(stage_key(c), __float_as_int(v));
+      for (int k = sub; k < len; k += LPN) {
+        const int c = ws.col_ind[start + k];
+        const float v = ws.sp_data[start + k];
+        *reinterpret_cast<int2*>(slot_lds + 2 * k) = make_int2(stage_key(c), __float_as_int(v));
       }
     }
     wave_lds_sync();
-    const int g = g0 + slot;
-    const bool has = g < gend;
-    const int start = has ? args.residue_offset[g] - range_begin : 0;
-    const int len = has ? args.residue_offset[g + 1] - range_begin - start : 0;
 #pragma unroll 1
     for (int j0 = 0; __any(j0 < len); j0 += kBatch) {
       Off off[kBatch];
@@ -210,9 +204,9 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs ar
         const int jj = j < len ? j : (len > 0 ? len - 1 : 0);
         int2 w;
         if (staged) {
-          w = *reinterpret_cast<const int2*>(my_lds + 2 * (start + jj));
+          w = *reinterpret_cast<const int2*>(slot_lds + 2 * jj);
         } else {
-          const int p = range_begin + start + jj;
+          const int p = start + jj;
           w = make_int2(stage_key(len > 0 ? ws.col_ind[p] : 0),
                         __float_as_int(len > 0 ? ws.sp_data[p] : 0.f));
         }

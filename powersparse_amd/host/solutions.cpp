@@ -25,6 +25,7 @@ std::vector<ps_workset> Worksets(const PowerSparseMatrixGPU& m, const ExecutionL
     ws[size_t(s)].group_des = e.group_des[s];
     ws[size_t(s)].group_num = m.GroupNum()[s];
     ws[size_t(s)].group_size = s == 0 ? 0 : GROUP_SIZE(s);
+    ws[size_t(s)].order = nullptr;  // groups run as stored
   }
   return ws;
 }

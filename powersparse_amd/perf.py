@@ -12,11 +12,15 @@
       of the operators' per-nonzero B / Y row gathers.
 
   python -m powersparse_amd.perf summarize --trace KT.db [--fetch F.db --write W.db]
-        [--config C1] [--json OUT.json]
+        [--l2 L.db] [--valu V.db] [--config C1] [--json OUT.json]
       Reads rocprofv3 SQLite result databases: per kernel the dispatch count and
       mean duration (kernel trace), and per operator kernel the HBM traffic per
       dispatch = FETCH_SIZE + WRITE_SIZE (KiB), each scaled by the factor that
-      makes the calibration copy read and write exactly its size.
+      makes the calibration copy read and write exactly its size; with --l2 (a
+      `--pmc TCC_HIT_sum TCC_MISS_sum` pass) the L2 hit rate, with --valu (a `--pmc VALUBusy
+      VALUUtilization` pass) the share of time the VALUs issue and the share of
+      active lanes per VALU instruction, each averaged over the operator's
+      dispatches.
 """
 import argparse
 import collections
@@ -28,7 +32,7 @@ import sys
 CALIB_BYTES = 1 << 30
 
 # operators of each bench configuration, in launch order (kernel, N)
-CONFIG_OPS = {"C1": [("spmm", 32), ("spmm", 128), ("sddmm", 128)],
+CONFIG_OPS = {"C1": [("spmm", 32), ("spmm", 128), ("sddmm", 128), ("sddmm", 32)],
               "C3": [("spmm", 32), ("spmm", 128), ("sddmm", 128)],
               "C4": [("spmm", 64), ("sddmm", 64)]}
 
@@ -40,7 +44,8 @@ def short_name(name):
 
 def kernel_op(name):
     """(op, lanes-template) of an operator kernel name, else None."""
-    m = re.search(r"(spmm|sddmm)_kernel<(\d+), (true|false)(, (true|false))?>", short_name(name))
+    # spmm_kernel<lanes, buf>, sddmm_kernel<KQ, buf, store mode>
+    m = re.search(r"(spmm|sddmm)_kernel<(\d+), (true|false)(, \d+)?>", short_name(name))
     return (m.group(1), int(m.group(2))) if m else None
 
 
@@ -130,6 +135,23 @@ def read_counters(db, counter):
     return [(short_name(k), int(g), float(v)) for k, g, v in rows]
 
 
+def counter_means(db, counter, ops):
+    """{op_N: mean of `counter` over that operator's dispatches}, the runs of
+    operator dispatches matched to `ops` in launch order."""
+    runs = operator_runs(read_counters(db, counter))
+    return {f"{op}_N{n}": sum(v) / len(v) for (op, n), (_, v) in zip(ops, runs)}
+
+
+def l2_hit_means(db, ops):
+    """{op_N: mean L2 hit rate in percent, 100 * TCC_HIT / (TCC_HIT + TCC_MISS)
+    per dispatch} (rocprofv3 defines no L2CacheHit metric for gfx950)."""
+    hits, misses = read_counters(db, "TCC_HIT_sum"), read_counters(db, "TCC_MISS_sum")
+    rates = [(k, g, 100.0 * h / (h + m) if h + m > 0 else 0.0)
+             for (k, g, h), (_, _, m) in zip(hits, misses)]
+    runs = operator_runs(rates)
+    return {f"{op}_N{n}": sum(v) / len(v) for (op, n), (_, v) in zip(ops, runs)}
+
+
 def read_trace(db):
     """Per (kernel, grid): dispatches and mean duration in us, busiest first."""
     con = sqlite3.connect(db)
@@ -187,6 +209,21 @@ def summarize(args):
                                                 "write_bytes": wb, "traffic_bytes": fb + wb}
             lines.append(f"| {op} N={n} | `{k}` | {g} | {fb / 1e6:.1f} | {wb / 1e6:.1f} | "
                          f"{(fb + wb) / 1e6:.1f} |")
+    if args.l2 or args.valu:
+        ops = CONFIG_OPS[args.config]
+        l2 = l2_hit_means(args.l2, ops) if args.l2 else {}
+        busy = counter_means(args.valu, "VALUBusy", ops) if args.valu else {}
+        util = counter_means(args.valu, "VALUUtilization", ops) if args.valu else {}
+        lines += ["", "| operator | L2 hit rate (%) | VALU busy (%) | VALU lanes active (%) |",
+                  "|---|---|---|---|"]
+        result["counters"] = {}
+        for op, n in ops:
+            key = f"{op}_N{n}"
+            c = {"l2_hit_pct": l2.get(key), "valu_busy_pct": busy.get(key),
+                 "valu_utilization_pct": util.get(key)}
+            result["counters"][key] = c
+            lines.append(f"| {op} N={n} | " + " | ".join(
+                "-" if v is None else f"{v:.1f}" for v in c.values()) + " |")
     print("\n".join(lines))
     if args.json:
         with open(args.json, "w") as fh:
@@ -204,6 +241,8 @@ def main(argv=None):
     s.add_argument("--trace", required=True)
     s.add_argument("--fetch")
     s.add_argument("--write")
+    s.add_argument("--l2")
+    s.add_argument("--valu")
     s.add_argument("--config", default="C1", choices=sorted(CONFIG_OPS))
     s.add_argument("--json")
     args = ap.parse_args(argv)

@@ -114,3 +114,101 @@ def test_launch_argument_checks():
     with pytest.raises(ValueError, match="Missing SDDMM output"):
         ps.sddmm_launch(up.worksets, up.offset, csr.rows, csr.cols, 32, dB, dB,
                         [None] * w.S)
+
+
+def run_order(offsets, kind, seed):
+    """A residue run order: 'length' (longest first, ties in stored order) or a
+    random permutation."""
+    lens = np.diff(np.asarray(offsets, dtype=np.int64))
+    if kind == "length":
+        return np.argsort(-np.minimum(lens, 255), kind="stable").astype(np.int32)
+    return np.random.default_rng(seed).permutation(lens.size).astype(np.int32)
+
+
+@pytest.mark.parametrize("kind", ["length", "random"])
+@pytest.mark.parametrize("name", sorted(GRAPHS))
+def test_residue_run_order(name, kind):
+    """The operators given a run order for the residue groups (ps_workset.order):
+    SpMM within tolerance of the oracle, SDDMM bitwise equal to the call without
+    an order (each output is one lane's dot, whichever slot runs the group)."""
+    setup()
+    csr, w = graph(name)
+    if w.group_num[0] == 0:
+        pytest.skip("no residue groups")
+    say(f"residue run order {kind} {name} S={w.S} groups={w.group_num}")
+    up = Uploaded(w)
+    d_order = ps.DeviceBuffer(host=run_order(w.residue_offset, kind, 3))
+    ordered = [up.worksets[0] + (d_order,)] + list(up.worksets[1:])
+    rng = np.random.default_rng(17)
+    for N in (32, 64, 128):
+        B = rng.uniform(-1, 1, (csr.cols, N)).astype(np.float32)
+        dB = ps.DeviceBuffer(host=B)
+        dC = ps.DeviceBuffer.zeros(csr.rows * N * 4)
+        ps.spmm_launch(ordered, up.offset, up.atomic, csr.rows, csr.cols, N, dB, dC)
+        ps.synchronize()
+        E, M = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, N, B, with_mag=True)
+        tolerance.check(dC.download(np.float32).reshape(csr.rows, N), E, M,
+                        f"spmm {name} N={N} order {kind}")
+        X = rng.normal(size=(csr.rows, N)).astype(np.float32)
+        Y = rng.normal(size=(csr.cols, N)).astype(np.float32)
+        dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
+        plain = [ps.DeviceBuffer.zeros(max(w.col[s].size, 1) * 4) for s in range(w.S)]
+        runs = [ps.DeviceBuffer.zeros(max(w.col[s].size, 1) * 4) for s in range(w.S)]
+        ps.sddmm_launch(up.worksets, up.offset, csr.rows, csr.cols, N, dX, dY, plain)
+        ps.sddmm_launch(ordered, up.offset, csr.rows, csr.cols, N, dX, dY, runs)
+        ps.synchronize()
+        for s in range(w.S):
+            np.testing.assert_array_equal(runs[s].download(np.float32, w.col[s].size),
+                                          plain[s].download(np.float32, w.col[s].size))
+        E, M = oracle.sddmm(w.des[0], w.offsets(0), w.col[0], w.val[0], N, X, Y, with_mag=True)
+        tolerance.check(runs[0].download(np.float32, w.col[0].size), E, M,
+                        f"sddmm {name} N={N} order {kind} residue")
+
+
+@pytest.mark.parametrize("kind", [None, "length", "random"])
+def test_long_residue_groups(kind):
+    """Residue groups longer than the kernels stage in LDS (up to 150 nonzeros)
+    and empty ones, which the preprocessing never builds but the C ABI accepts:
+    one group per row, each row's whole CSR row, so SpMM stores every row."""
+    setup()
+    rng = np.random.default_rng(21)
+    rows, cols = 700, 3000
+    lens = rng.integers(0, 151, rows)
+    lens[::7] = rng.integers(0, 33, lens[::7].size)  # short ones mixed in
+    lens[::50] = 0
+    offsets = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    nnz = int(offsets[-1])
+    col = rng.integers(0, cols, nnz).astype(np.int32)
+    val = rng.uniform(-1, 1, nnz).astype(np.float32)
+    rows_of = np.repeat(np.arange(rows), lens)
+    bufs = [ps.DeviceBuffer(host=col), ps.DeviceBuffer(host=val),
+            ps.DeviceBuffer(host=np.arange(rows, dtype=np.int32))]
+    order = None if kind is None else ps.DeviceBuffer(host=run_order(offsets, kind, 5))
+    ws = [(bufs[0], bufs[1], bufs[2], rows, 0, order)]
+    d_off = ps.DeviceBuffer(host=offsets)
+    d_atomic = ps.DeviceBuffer.zeros(rows)
+    say(f"long residue groups order={kind} rows={rows} nnz={nnz} max={lens.max()}")
+    for N in (32, 64, 96):
+        B = rng.uniform(-1, 1, (cols, N)).astype(np.float32)
+        dB = ps.DeviceBuffer(host=B)
+        dC = ps.DeviceBuffer.zeros(rows * N * 4)
+        ps.spmm_launch(ws, d_off, d_atomic, rows, cols, N, dB, dC)
+        ps.synchronize()
+        terms = val[:, None].astype(np.float64) * B[col].astype(np.float64)
+        E = np.zeros((rows, N))
+        M = np.zeros((rows, N))
+        np.add.at(E, rows_of, terms)
+        np.add.at(M, rows_of, np.abs(terms))
+        tolerance.check(dC.download(np.float32).reshape(rows, N), E, M,
+                        f"spmm long groups N={N} order={kind}")
+        X = rng.normal(size=(rows, N)).astype(np.float32)
+        Y = rng.normal(size=(cols, N)).astype(np.float32)
+        dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
+        out = ps.DeviceBuffer.zeros(nnz * 4)
+        ps.sddmm_launch(ws, d_off, rows, cols, N, dX, dY, [out])
+        ps.synchronize()
+        prod = X[rows_of].astype(np.float64) * Y[col].astype(np.float64)
+        E = val * prod.sum(1)
+        M = np.abs(val) * np.abs(prod).sum(1)
+        tolerance.check(out.download(np.float32, nnz), E, M,
+                        f"sddmm long groups N={N} order={kind}")

@@ -1,0 +1,128 @@
+"""Host logic of the measurement tooling, on the CPU: the rocprofv3 summary
+(`python -m powersparse_amd.perf summarize`) on small SQLite databases shaped
+like rocprofv3's, the counters bench.py reads back from it, and bench.py's
+refusal of more than one GPU."""
+import json
+import os
+import sqlite3
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+from powersparse_amd import perf  # noqa: E402
+
+KIB = 1024.0
+SPMM32 = "void ps::spmm_kernel<8, true>(ps::(anonymous namespace)::SpmmArgs)"
+SPMM128 = "void ps::spmm_kernel<8, true>(ps::(anonymous namespace)::SpmmArgs)"
+SDDMM128 = "void ps::(anonymous namespace)::sddmm_kernel<4, true, 0>(ps::SddmmArgs)"
+SDDMM32 = "void ps::(anonymous namespace)::sddmm_kernel<1, true, 0>(ps::SddmmArgs)"
+COPY = "void ps::copy_f32_kernel(float*, float const*, unsigned long)"
+PRE = "void ps::rank_small_kernel(int const*, int, int const*)"
+
+
+def counter_db(path, counter, dispatches):
+    """dispatches: [(kernel, grid, value)] in dispatch order."""
+    con = sqlite3.connect(path)
+    con.execute("create table counters_collection (dispatch_id integer, kernel_name text, "
+                "grid_size integer, counter_name text, value real)")
+    con.executemany("insert into counters_collection values (?, ?, ?, ?, ?)",
+                    [(i, k, g, counter, v) for i, (k, g, v) in enumerate(dispatches)])
+    con.commit()
+    con.close()
+    return str(path)
+
+
+def workload(values):
+    """The perf workload's dispatch order: a warm-up and a timed copy, a
+    preprocessing kernel, then each C1 operator 1 + 3 times (values[i] for
+    operator i; the copy gets values['copy'])."""
+    out = [(COPY, 1 << 20, values["copy"])] * 2 + [(PRE, 4096, 7.0)]
+    # SpMM N=32 and N=128 share a kernel and differ in grid (32-column slices)
+    launches = [(SPMM32, 1000), (SPMM128, 4000), (SDDMM128, 3000), (SDDMM32, 3000)]
+    for (kernel, grid), v in zip(launches, values["ops"]):
+        out += [(kernel, grid, v)] * 4
+    return out
+
+
+@pytest.fixture
+def dbs(tmp_path):
+    trace = tmp_path / "kt.db"
+    con = sqlite3.connect(trace)
+    con.execute("create table kernels (name text, grid_x integer, grid_y integer, "
+                "grid_z integer, duration real)")
+    con.executemany("insert into kernels values (?, ?, 1, 1, ?)",
+                    [(SPMM32, 1000, 640e3), (SPMM32, 1000, 650e3), (SDDMM128, 3000, 2.77e6),
+                     (PRE, 4096, 10e3)])
+    con.commit()
+    con.close()
+    # FETCH reads the 1 GiB copy as 2 GiB (factor 0.5), WRITE as 1 GiB (factor 1)
+    fetch = counter_db(tmp_path / "f.db", "FETCH_SIZE",
+                       workload({"copy": 2 * (1 << 30) / KIB, "ops": [1000, 2000, 3000, 4000]}))
+    write = counter_db(tmp_path / "w.db", "WRITE_SIZE",
+                       workload({"copy": (1 << 30) / KIB, "ops": [10, 20, 30, 40]}))
+    # hit rates 45, 30, 25, 40 % from TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)
+    l2 = counter_db(tmp_path / "l2.db", "TCC_HIT_sum",
+                    workload({"copy": 1.0, "ops": [450.0, 300.0, 250.0, 40.0]}))
+    con = sqlite3.connect(l2)
+    con.executemany("insert into counters_collection values (?, ?, ?, ?, ?)",
+                    [(100 + i, k, g, "TCC_MISS_sum", v) for i, (k, g, v) in enumerate(
+                        workload({"copy": 1.0, "ops": [550.0, 700.0, 750.0, 60.0]}))])
+    con.commit()
+    con.close()
+    valu = tmp_path / "v.db"
+    counter_db(valu, "VALUBusy", workload({"copy": 5.0, "ops": [11.0, 12.0, 13.0, 14.0]}))
+    con = sqlite3.connect(valu)
+    con.executemany("insert into counters_collection values (?, ?, ?, ?, ?)",
+                    [(100 + i, k, g, "VALUUtilization", v) for i, (k, g, v) in enumerate(
+                        workload({"copy": 99.0, "ops": [90.0, 91.0, 92.0, 93.0]}))])
+    con.commit()
+    con.close()
+    return dict(trace=str(trace), fetch=fetch, write=write, l2=l2, valu=str(valu))
+
+
+def test_summary_traffic_and_counters(dbs, tmp_path, capsys):
+    out = tmp_path / "traffic.json"
+    perf.main(["summarize", "--config", "C1", "--trace", dbs["trace"], "--fetch", dbs["fetch"],
+               "--write", dbs["write"], "--l2", dbs["l2"], "--valu", dbs["valu"],
+               "--json", str(out)])
+    summary = json.loads(out.read_text())
+    assert summary["calibration"] == {"fetch": 0.5, "write": 1.0}
+    t = summary["traffic"]
+    assert list(t) == ["spmm_N32", "spmm_N128", "sddmm_N128", "sddmm_N32"]
+    # bytes = KiB * 1024 * calibration factor
+    assert t["spmm_N32"]["fetch_bytes"] == 1000 * KIB * 0.5
+    assert t["sddmm_N32"]["write_bytes"] == 40 * KIB
+    assert t["sddmm_N128"]["traffic_bytes"] == 3000 * KIB * 0.5 + 30 * KIB
+    c = summary["counters"]
+    assert c["spmm_N128"] == {"l2_hit_pct": 30.0, "valu_busy_pct": 12.0,
+                              "valu_utilization_pct": 91.0}
+    assert c["sddmm_N32"]["l2_hit_pct"] == 40.0
+    # kernel table: busiest first (dispatches x mean duration)
+    table = summary["kernels"]
+    assert table[0]["kernel"].startswith("ps::") and "sddmm_kernel<4" in table[0]["kernel"]
+    assert table[1]["dispatches"] == 2 and table[1]["mean_us"] == pytest.approx(645.0)
+    assert "| sddmm N=32 | 40.0 | 14.0 | 93.0 |" in capsys.readouterr().out
+
+
+def test_bench_reads_counters(dbs, tmp_path, monkeypatch):
+    import bench
+    profiles = tmp_path / "profiles"
+    profiles.mkdir()
+    perf.main(["summarize", "--config", "C1", "--trace", dbs["trace"], "--fetch", dbs["fetch"],
+               "--write", dbs["write"], "--l2", dbs["l2"], "--valu", dbs["valu"],
+               "--json", str(profiles / "traffic_C1.json")])
+    monkeypatch.setattr(bench, "ROOT", str(tmp_path))
+    traffic, counters, src = bench.measured_counters("C1", "sddmm", 128)
+    assert traffic == 3000 * KIB * 0.5 + 30 * KIB
+    assert counters["valu_busy_pct"] == 13.0 and src == os.path.join("profiles", "traffic_C1.json")
+    assert bench.measured_counters("C4", "spmm", 64) == (None, {}, None)
+
+
+def test_bench_one_gpu_only():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU only" in r.stderr
