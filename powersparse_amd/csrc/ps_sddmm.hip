@@ -3,10 +3,10 @@
 // One launch covers every workset. Wave tasks:
 //   block workset: 64 consecutive stored nonzeros (one group when GS >= 64, two
 //     groups of 32 when GS == 32);
-//   residue workset: 8 groups per wave, one slot per group, taken in the
-//     workset's run order (ps_workset.order: longest groups first, so the
-//     groups sharing a wave have about the same length and few lanes idle);
-//     a slot walks its group 8 nonzeros at a time, columns staged in LDS.
+//   residue workset: 8 groups per wave, one slot per group, as stored or in
+//     the workset's run order (ps_workset.order); a slot loads its group's X
+//     row once, stages the group's columns in LDS and walks it 8 nonzeros at a
+//     time.
 // Lanes form slots of 8; slot q owns 8 consecutive nonzeros and each lane of the
 // slot holds K / 8 features of X (float4 pieces 32 floats apart, so a slot reads
 // a 128-byte line per piece). After the 8 partial dots per lane the slot does a
@@ -161,9 +161,9 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
       }
     }
   } else {
-    // One slot per group, groups taken in the workset's run order (longest
-    // first when an order is given, so a wave's groups end together); the
-    // slot's group is walked 8 nonzeros at a time.
+    // One slot per group (the run order's entry local * 8 + slot: order[]
+    // when given, else as stored); the slot's group is walked 8 nonzeros at a
+    // time.
     const int kq = local * 8 + slot;
     const bool has = kq < ws.group_num;
     const int g = has ? (ws.order ? ws.order[kq] : kq) : 0;
