@@ -128,7 +128,8 @@ int ps_stream_wait_event(ps_stream_t stream, ps_event_t event);
  * order (residue workset only, may be NULL): a permutation of its group_num
  * groups giving the order in which the operators run them, e.g. to visit the
  * groups of neighbouring rows together; results do not depend on it beyond the
- * order of FP32 atomic additions. NULL runs the groups as stored.
+ * order of FP32 atomic additions. Entries outside [0, group_num) are skipped
+ * (their groups are not computed). NULL runs the groups as stored.
  * No reference counterpart. */
 typedef struct ps_workset {
   const int* col_ind;     /* WorksetColInd()[s]  (matrix_utils.h:36) */

@@ -165,8 +165,9 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     // when given, else as stored); the slot's group is walked 8 nonzeros at a
     // time.
     const int kq = local * 8 + slot;
-    const bool has = kq < ws.group_num;
-    const int g = has ? (ws.order ? ws.order[kq] : kq) : 0;
+    int g = kq < ws.group_num ? (ws.order ? ws.order[kq] : kq) : -1;
+    const bool has = g >= 0 && g < ws.group_num;  // order entries out of range are skipped
+    if (!has) g = 0;
     const int beg = has ? args.residue_offset[g] : 0;
     const int len = has ? args.residue_offset[g + 1] - beg : 0;
     const int row = has ? ws.group_des[g] : 0;

@@ -20,9 +20,9 @@
 //     plain store otherwise.
 //
 // Each task first stages its nonzeros in LDS with coalesced loads, as
-// (byte offset of the B row, value) pairs, so the gather loop issues 16 (block
-// tiles) or 8 (residue groups) independent 128-bit B loads per lane with no
-// dependent index load in between. B is addressed through a buffer resource with 32-bit offsets when
+// (byte offset of the B row, value) pairs, so the gather loop issues batches of
+// 8 independent 128-bit B loads per lane with no dependent index load in
+// between. B is addressed through a buffer resource with 32-bit offsets when
 // cols * N * 4 fits in 32 bits.
 //
 // Workgroup -> task mapping: the hardware deals workgroups round-robin over
@@ -44,10 +44,11 @@ namespace {
 constexpr int kWavesPerBlock = 4;
 constexpr int kPer = 32;          // nonzeros per slot per block tile
 constexpr int kSlotWords = 2 * kPer + 4;  // LDS words per slot (pairs + pad)
-constexpr int kBatch = 16;        // B loads in flight per lane (block tiles)
-// Residue groups are walked 8 nonzeros at a time: they hold 1..31 nonzeros and
-// a wave runs as long as its longest group, so shorter steps waste fewer lanes
-// on padding (C1 SpMM N=32 643 -> 625 us, C4 N=64 1595 -> 1541 us).
+// B loads in flight per lane. 8 keeps the kernel at 62 VGPRs, i.e. 8 waves per
+// SIMD; 16 needs 110 VGPRs (4 waves) and ran 4-9% slower on C1, C3 and C4.
+constexpr int kBatch = 8;
+// Residue groups are walked 8 nonzeros at a time too: they hold 1..31 nonzeros
+// and a wave runs as long as its longest group (16 cost 3% more).
 constexpr int kRBatch = 8;
 
 struct SpmmArgs {
@@ -184,8 +185,9 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs ar
     // area; groups built by the preprocessing hold at most 31 nonzeros, longer
     // ones are read directly.
     const int kq = int(local) * SL + slot;
-    const bool has = kq < ws.group_num;
-    const int g = has ? (ws.order ? ws.order[kq] : kq) : 0;
+    int g = kq < ws.group_num ? (ws.order ? ws.order[kq] : kq) : -1;
+    const bool has = g >= 0 && g < ws.group_num;  // order entries out of range are skipped
+    if (!has) g = 0;
     const int start = has ? args.residue_offset[g] : 0;
     const int len = has ? args.residue_offset[g + 1] - start : 0;
     int* const slot_lds = my_lds + slot * kSlotWords;

@@ -212,3 +212,32 @@ def test_long_residue_groups(kind):
         M = np.abs(val) * np.abs(prod).sum(1)
         tolerance.check(out.download(np.float32, nnz), E, M,
                         f"sddmm long groups N={N} order={kind}")
+
+
+def test_residue_order_out_of_range_entries_skipped():
+    """Run-order entries outside [0, group_num) are skipped: their slots
+    compute nothing and every other group is computed as without an order."""
+    setup()
+    csr, w = graph("c1_small")
+    up = Uploaded(w)
+    G = w.group_num[0]
+    order = np.arange(G, dtype=np.int32)
+    dropped = np.array([0, 5, G // 2, G - 1])
+    order[dropped] = np.array([-1, G, G + 1000, -(1 << 30)], dtype=np.int32)
+    d_order = ps.DeviceBuffer(host=order)
+    ordered = [up.worksets[0] + (d_order,)] + list(up.worksets[1:])
+    N = 32
+    rng = np.random.default_rng(29)
+    X = rng.normal(size=(csr.rows, N)).astype(np.float32)
+    Y = rng.normal(size=(csr.cols, N)).astype(np.float32)
+    dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
+    n0 = w.col[0].size
+    plain, runs = ps.DeviceBuffer.zeros(n0 * 4), ps.DeviceBuffer.zeros(n0 * 4)
+    ps.sddmm_launch(up.worksets[:1], up.offset, csr.rows, csr.cols, N, dX, dY, [plain])
+    ps.sddmm_launch(ordered[:1], up.offset, csr.rows, csr.cols, N, dX, dY, [runs])
+    ps.synchronize()
+    expect = plain.download(np.float32, n0)
+    off = w.residue_offset
+    for g in dropped:
+        expect[off[g]:off[g + 1]] = 0.0
+    np.testing.assert_array_equal(runs.download(np.float32, n0), expect)
