@@ -146,15 +146,22 @@ typedef struct ps_workset {
  * (overwrite) their row. N must be a positive multiple of 32; cols * N and
  * rows * N must fit in int32. B, C and the block worksets' col_ind / sp_data
  * must be 16-byte aligned (as ps_malloc returns them).
+ * task_chunk (0 or a power of two up to 256; 0 and 1 mean the hardware's
+ * round robin of workgroups over the 8 XCDs): consecutive tasks dealt to one
+ * XCD (one L2) in runs of task_chunk. Results do not depend on it. Worksets
+ * whose neighbouring groups share columns (a row-ordered copy of a graph with
+ * locality) run faster with long runs (64); in signature order 1 was as fast
+ * or faster. No reference counterpart.
  * Replaces: the launch loop of PowerSparse::SpMM (PowerSparse_SpMM/spmm_solution.cu:16-31)
  * and the kernels spmm_kernel_block (spmm_kernel_block.cu:60-162) and
  * spmm_kernel_residue (spmm_kernel_residue.cu:5-82). */
 int ps_spmm_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
                    const uint8_t* residue_atomic, int rows, int cols, int N, const float* B,
-                   float* C, ps_stream_t stream);
+                   float* C, int task_chunk, ps_stream_t stream);
 
 /* Same operator for a single workset s (s == 0: residue), so callers may keep
- * the reference's one-stream-per-workset schedule (spmm_solution.cu:16-31). */
+ * the reference's one-stream-per-workset schedule (spmm_solution.cu:16-31);
+ * workgroups in the hardware's order (task_chunk 1). */
 int ps_spmm_workset_launch(int s, const ps_workset* workset, const int* residue_offset,
                            const uint8_t* residue_atomic, int rows, int cols, int N,
                            const float* B, float* C, ps_stream_t stream);
@@ -166,13 +173,14 @@ int ps_spmm_workset_launch(int s, const ps_workset* workset, const int* residue_
  * reference uses atomicAdd into a caller-zeroed buffer). N must be a positive
  * multiple of 32 and at most 512 (the reference accepts 32 and 128 only,
  * sddmm_solution.cu:10-11). lhs, rhs and the block worksets' col_ind must be
- * 16-byte aligned.
+ * 16-byte aligned. task_chunk as for ps_spmm_launch (ps_sddmm_workset_launch:
+ * 1).
  * Replaces: PowerSparse::SDDMM's launch loop (sddmm_solution.cu:23-48) and
  * sddmm_kernel_block_reduce{32,128} (sddmm_kernel_block.cu:92-240),
  * sddmm_kernel_residue_reduce{32,128} (sddmm_kernel_residue.cu:69-545). */
 int ps_sddmm_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
                     int rows, int cols, int N, const float* lhs, const float* rhs,
-                    float* const* out, ps_stream_t stream);
+                    float* const* out, int task_chunk, ps_stream_t stream);
 int ps_sddmm_workset_launch(int s, const ps_workset* workset, const int* residue_offset,
                             int rows, int cols, int N, const float* lhs, const float* rhs,
                             float* out, ps_stream_t stream);
@@ -182,24 +190,25 @@ int ps_sddmm_workset_launch(int s, const ps_workset* workset, const int* residue
  * for every stored nonzero p of workset s, csr_pos[s] being each slot's
  * position in the CSR arrays the matrix was built from (ps_pre_gather_workset's
  * out_csr_pos). Every CSR position is stored exactly once: out_csr (nnz floats)
- * needs no zeroing. Same N and shape limits as ps_sddmm_launch.
+ * needs no zeroing. Same N and shape limits, and task_chunk, as ps_sddmm_launch.
  * Replaces: the permutation a caller must apply to the reference's output,
  * which "is in workset order, not original CSR order" (PowerSparse_SDDMM.h:11-12). */
 int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
                         const int* const* csr_pos, int rows, int cols, int N, const float* lhs,
-                        const float* rhs, float* out_csr, ps_stream_t stream);
+                        const float* rhs, float* out_csr, int task_chunk,
+                        ps_stream_t stream);
 
 /* SDDMM of worksets laid out in another group order than the public ones (a
  * task-order execution copy): the result of member j of group g of workset s
  * goes to out[s][out_base[s][g] + j], out[s] being the public workset-order
  * buffer (ps_pre_exec_positions gives the bases); block results are stored,
  * residue results added, exactly as ps_sddmm_launch does at the public
- * positions. No reference counterpart (the reference runs the public layout
- * only). */
+ * positions; task_chunk as for ps_sddmm_launch. No reference counterpart (the
+ * reference runs the public layout only). */
 int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
                             const int* residue_offset, const int* const* out_base, int rows,
                             int cols, int N, const float* lhs, const float* rhs,
-                            float* const* out, ps_stream_t stream);
+                            float* const* out, int task_chunk, ps_stream_t stream);
 
 /* out_csr[csr_pos[s][p]] = in[s][p] for p < lengths[s]: moves per-nonzero values
  * from workset order (e.g. the outputs of ps_sddmm_launch) to CSR order.

@@ -571,16 +571,19 @@ def _workset_array(worksets):
     return arr
 
 
-def spmm_launch(worksets, residue_offset, residue_atomic, rows, cols, N, B, C, stream=None):
-    """ps_spmm_launch over (col, val, des, group_num, group_size) tuples, s = 0..S-1."""
+def spmm_launch(worksets, residue_offset, residue_atomic, rows, cols, N, B, C, stream=None,
+                task_chunk=1):
+    """ps_spmm_launch over (col, val, des, group_num, group_size[, order]) tuples,
+    s = 0..S-1."""
     _hip_call(_native.hip().ps_spmm_launch(len(worksets), _workset_array(worksets),
                                            _ptr(residue_offset), _ptr(residue_atomic), rows, cols,
-                                           N, _ptr(B), _ptr(C), _ptr(stream)))
+                                           N, _ptr(B), _ptr(C), int(task_chunk), _ptr(stream)))
 
 
-def sddmm_launch(worksets, residue_offset, rows, cols, N, lhs, rhs, outputs, stream=None):
+def sddmm_launch(worksets, residue_offset, rows, cols, N, lhs, rhs, outputs, stream=None,
+                 task_chunk=1):
     """ps_sddmm_launch; outputs[s] is workset s's output buffer."""
     _hip_call(_native.hip().ps_sddmm_launch(len(worksets), _workset_array(worksets),
                                             _ptr(residue_offset), rows, cols, N, _ptr(lhs),
                                             _ptr(rhs), _out_array(outputs, len(worksets)),
-                                            _ptr(stream)))
+                                            int(task_chunk), _ptr(stream)))

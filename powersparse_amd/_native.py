@@ -100,22 +100,23 @@ HIP_API = [
     ("ps_stream_wait_event", ctypes.c_int, [c_void_p, c_void_p]),
     ("ps_spmm_launch", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
-      ctypes.c_int, c_void_p, c_void_p, c_void_p]),
+      ctypes.c_int, c_void_p, c_void_p, ctypes.c_int, c_void_p]),
     ("ps_spmm_workset_launch", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
       ctypes.c_int, c_void_p, c_void_p, c_void_p]),
     ("ps_sddmm_launch", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-      c_void_p, c_void_p, ctypes.POINTER(c_void_p), c_void_p]),
+      c_void_p, c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int, c_void_p]),
     ("ps_sddmm_workset_launch", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
       c_void_p, c_void_p, c_void_p, c_void_p]),
     ("ps_sddmm_csr_launch", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int,
-      ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+      ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, c_void_p, ctypes.c_int, c_void_p]),
     ("ps_sddmm_scatter_launch", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int,
-      ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, ctypes.POINTER(c_void_p), c_void_p]),
+      ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int,
+      c_void_p]),
     ("ps_pre_exec_positions", ctypes.c_int,
      [ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p]),
     ("ps_pre_locality_score", ctypes.c_int,

@@ -85,18 +85,28 @@ __device__ __forceinline__ float xor_shfl(float v) {
 }
 
 // Workgroup -> logical index. The hardware deals workgroups round-robin over
-// the 8 XCDs, each with its own L2. Windows of 8 * kXcdChunk consecutive
-// workgroups are re-dealt so that each XCD takes kXcdChunk consecutive logical
-// indices: neighbouring tasks (which share B / Y rows after the signature
-// ordering) run under one L2, while every XCD still gets a slice of every
-// window, which keeps the XCDs balanced when task costs vary along the list.
-// The last, partial window keeps the hardware order.
-constexpr uint32_t kXcd = 8, kXcdChunk = 16;
-__device__ __forceinline__ uint32_t balanced_block(uint32_t b, uint32_t n) {
-  constexpr uint32_t kWin = kXcd * kXcdChunk;
-  const uint32_t w = b / kWin;
-  if ((w + 1) * kWin > n) return b;
-  return w * kWin + (b % kXcd) * kXcdChunk + (b / kXcd) % kXcdChunk;
+// the 8 XCDs, each with its own L2. With chunk = 2^chunk_log2 > 1, windows of
+// 8 * chunk consecutive workgroups are re-dealt so that each XCD takes chunk
+// consecutive logical indices: neighbouring tasks run under one L2, while every
+// XCD still gets a slice of every window, which keeps the XCDs balanced when
+// task costs vary along the list. The last, partial window keeps the hardware
+// order; chunk_log2 == 0 keeps it everywhere.
+constexpr uint32_t kXcd = 8;
+__device__ __forceinline__ uint32_t balanced_block(uint32_t b, uint32_t n, uint32_t chunk_log2) {
+  if (chunk_log2 == 0) return b;
+  const uint32_t chunk = 1u << chunk_log2;
+  const uint32_t win = kXcd * chunk;
+  const uint32_t w = b / win;
+  if ((w + 1) * win > n) return b;
+  return w * win + (b % kXcd) * chunk + (b / kXcd) % chunk;
+}
+
+// log2 of a launch's task chunk (a power of two in [1, 256]; 0 means 1), or -1.
+inline int task_chunk_log2(int task_chunk) {
+  if (task_chunk == 0) return 0;
+  for (int l = 0; l <= 8; ++l)
+    if (task_chunk == (1 << l)) return l;
+  return -1;
 }
 
 // 128-bit loads at byte offsets from a base: through a buffer resource with

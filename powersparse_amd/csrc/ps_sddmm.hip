@@ -48,6 +48,7 @@ struct SddmmArgs {
   uint64_t rhs_bytes;
   const int* out_pos[PS_MAX_WORKSETS];  // mode 1: per-nonzero map; mode 2: per-group base
   int32_t residue_add;                  // modes 1-2: residue results added, not stored
+  uint32_t chunk_log2;                  // workgroup -> XCD mapping (balanced_block)
 };
 
 // Transposing reduction over the 8 lanes of a slot: in p[j] each lane holds
@@ -109,7 +110,7 @@ template <int KQ, bool kBuf, int kMode>
 __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs args) {
   constexpr int K = 32 * KQ;
   __shared__ __attribute__((aligned(16))) int stage[kWavesPerBlock][8 * kStage];
-  const uint32_t blk = balanced_block(blockIdx.x, gridDim.x);
+  const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, args.chunk_log2);
   const uint32_t task =
       __builtin_amdgcn_readfirstlane(blk * kWavesPerBlock + threadIdx.x / kWave);
   if (task >= args.total_tasks) return;
@@ -250,14 +251,18 @@ void launch_kq(const SddmmArgs& a, bool buf, int mode, unsigned grid, hipStream_
 int launch(int count, const int* order, const ps_workset* worksets, float* const* outs,
            int mode, const int* const* out_pos, int residue_add, const int* residue_offset,
            int rows,
-           int cols, int N, const float* lhs, const float* rhs, hipStream_t stream) {
+           int cols, int N, const float* lhs, const float* rhs, int task_chunk,
+           hipStream_t stream) {
   PS_CHECK_ARG(N > 0 && N % 32 == 0 && N <= 512,
                "SDDMM requires N to be a multiple of 32 between 32 and 512");
   PS_CHECK_ARG(int64_t(rows) * N <= INT32_MAX && int64_t(cols) * N <= INT32_MAX,
                "Dense dimensions exceed the 32-bit kernel indexing range");
   PS_CHECK_ARG(lhs && rhs && outs, "Invalid SDDMM buffers");
   PS_CHECK_ARG(aligned16(lhs) && aligned16(rhs), "SDDMM dense buffers must be 16-byte aligned");
+  const int chunk_log2 = task_chunk_log2(task_chunk);
+  PS_CHECK_ARG(chunk_log2 >= 0, "SDDMM task_chunk must be 0 or a power of two up to 256");
   SddmmArgs a{};
+  a.chunk_log2 = uint32_t(chunk_log2);
   a.residue_add = residue_add;
   a.N = N;
   a.lhs = lhs;
@@ -333,7 +338,7 @@ extern "C" {
 
 int ps_sddmm_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
                     int rows, int cols, int N, const float* lhs, const float* rhs,
-                    float* const* out, ps_stream_t stream) {
+                    float* const* out, int task_chunk, ps_stream_t stream) {
   PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets && out,
                "Invalid SDDMM workset count");
   int order[PS_MAX_WORKSETS];
@@ -345,13 +350,13 @@ int ps_sddmm_launch(int workset_count, const ps_workset* worksets, const int* re
     outs[q] = out[workset_count - 1 - q];
   }
   return ps::launch(workset_count, order, ordered, outs, 0, nullptr, 0, residue_offset, rows,
-                    cols, N, lhs, rhs, ps::to_hip(stream));
+                    cols, N, lhs, rhs, task_chunk, ps::to_hip(stream));
 }
 
 int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
                             const int* residue_offset, const int* const* out_base, int rows,
                             int cols, int N, const float* lhs, const float* rhs,
-                            float* const* out, ps_stream_t stream) {
+                            float* const* out, int task_chunk, ps_stream_t stream) {
   PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets && out_base &&
                    out,
                "Invalid SDDMM workset count");
@@ -366,12 +371,12 @@ int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
     outs[q] = out[workset_count - 1 - q];
   }
   return ps::launch(workset_count, order, ordered, outs, 2, pos, 1, residue_offset, rows, cols,
-                    N, lhs, rhs, ps::to_hip(stream));
+                    N, lhs, rhs, task_chunk, ps::to_hip(stream));
 }
 
 int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
                         const int* const* csr_pos, int rows, int cols, int N, const float* lhs,
-                        const float* rhs, float* out_csr, ps_stream_t stream) {
+                        const float* rhs, float* out_csr, int task_chunk, ps_stream_t stream) {
   PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets && csr_pos &&
                    out_csr,
                "Invalid SDDMM workset count");
@@ -386,7 +391,7 @@ int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int
     outs[q] = out_csr;
   }
   return ps::launch(workset_count, order, ordered, outs, 1, pos, 0, residue_offset, rows, cols,
-                    N, lhs, rhs, ps::to_hip(stream));
+                    N, lhs, rhs, task_chunk, ps::to_hip(stream));
 }
 
 int ps_workset_to_csr(int workset_count, const long long* lengths, const int* const* csr_pos,
@@ -413,7 +418,7 @@ int ps_sddmm_workset_launch(int s, const ps_workset* workset, const int* residue
                             float* out, ps_stream_t stream) {
   PS_CHECK_ARG(s >= 0 && s < PS_MAX_WORKSETS && workset, "Invalid SDDMM workset");
   return ps::launch(1, &s, workset, &out, 0, nullptr, 0, residue_offset, rows, cols, N, lhs,
-                    rhs, ps::to_hip(stream));
+                    rhs, 1, ps::to_hip(stream));
 }
 
 }  // extern "C"

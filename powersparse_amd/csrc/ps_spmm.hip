@@ -26,11 +26,12 @@
 // cols * N * 4 fits in 32 bits.
 //
 // Workgroup -> task mapping: the hardware deals workgroups round-robin over
-// the 8 XCDs. Windows of 8 * kChunk consecutive workgroups are re-dealt so
-// that each XCD takes kChunk consecutive ones: neighbouring tasks (similar
-// column signatures) share an XCD's L2, while every XCD still gets a slice of
-// every window, which keeps the XCDs balanced when task costs vary along the
-// list (blocks of large groups first, residue groups last).
+// the 8 XCDs. With task_chunk > 1, windows of 8 * task_chunk consecutive
+// workgroups are re-dealt so that each XCD takes task_chunk consecutive ones:
+// neighbouring tasks share an XCD's L2, while every XCD still gets a slice of
+// every window (balance when task costs vary along the list). Worksets in row
+// order (neighbouring rows share columns) gain from long runs; in signature
+// order the hardware's round robin was as fast or faster.
 //
 // Reference behaviour kept (PowerSparse_SpMM/spmm_solution.cu:7-34,
 // spmm_kernel_block.cu:60-162, spmm_kernel_residue.cu:5-82): block groups and
@@ -63,6 +64,7 @@ struct SpmmArgs {
   const uint8_t* residue_atomic;
   const float* B;
   float* C;
+  uint32_t chunk_log2;  // workgroup -> XCD mapping (balanced_block)
 };
 
 __device__ __forceinline__ void fma4(float4& acc, float a, const float4& b) {
@@ -92,7 +94,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs ar
   constexpr int SL = 64 / LPN;
   __shared__ __attribute__((aligned(16))) int lds[kWavesPerBlock][SL * kSlotWords];
   const int wave = threadIdx.x / kWave;
-  const uint32_t blk = balanced_block(blockIdx.x, gridDim.x);
+  const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, args.chunk_log2);
   const uint32_t task = __builtin_amdgcn_readfirstlane(blk * kWavesPerBlock + wave);
   if (task >= args.total_tasks) return;
   // slice-major: every task of column slice 0, then slice 1, ...
@@ -258,8 +260,10 @@ void launch_lpn(const SpmmArgs& a, bool buf, unsigned grid, hipStream_t stream) 
 
 int launch(int count, const int* order, const ps_workset* worksets, const int* residue_offset,
            const uint8_t* residue_atomic, int rows, int cols, int N, const float* B, float* C,
-           hipStream_t stream) {
+           int task_chunk, hipStream_t stream) {
   PS_CHECK_ARG(N > 0 && N % 32 == 0, "SpMM requires N to be a positive multiple of 32");
+  const int chunk_log2 = task_chunk_log2(task_chunk);
+  PS_CHECK_ARG(chunk_log2 >= 0, "SpMM task_chunk must be 0 or a power of two up to 256");
   PS_CHECK_ARG(int64_t(rows) * N <= INT32_MAX && int64_t(cols) * N <= INT32_MAX,
                "Dense dimensions exceed the 32-bit kernel indexing range");
   PS_CHECK_ARG(B && C, "Invalid SpMM buffers");
@@ -267,6 +271,7 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
   const int lpn = pick_lpn(N);
   const int SL = 64 / lpn;
   SpmmArgs a{};
+  a.chunk_log2 = uint32_t(chunk_log2);
   a.N = N;
   a.slices = N / (4 * lpn);
   a.B = B;
@@ -326,7 +331,7 @@ extern "C" {
 
 int ps_spmm_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
                    const uint8_t* residue_atomic, int rows, int cols, int N, const float* B,
-                   float* C, ps_stream_t stream) {
+                   float* C, int task_chunk, ps_stream_t stream) {
   PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets,
                "Invalid SpMM workset count");
   // Largest groups first, as the reference submits s = S-1 .. 0
@@ -338,14 +343,14 @@ int ps_spmm_launch(int workset_count, const ps_workset* worksets, const int* res
     ordered[q] = worksets[workset_count - 1 - q];
   }
   return ps::launch(workset_count, order, ordered, residue_offset, residue_atomic, rows, cols,
-                    N, B, C, ps::to_hip(stream));
+                    N, B, C, task_chunk, ps::to_hip(stream));
 }
 
 int ps_spmm_workset_launch(int s, const ps_workset* workset, const int* residue_offset,
                            const uint8_t* residue_atomic, int rows, int cols, int N,
                            const float* B, float* C, ps_stream_t stream) {
   PS_CHECK_ARG(s >= 0 && s < PS_MAX_WORKSETS && workset, "Invalid SpMM workset");
-  return ps::launch(1, &s, workset, residue_offset, residue_atomic, rows, cols, N, B, C,
+  return ps::launch(1, &s, workset, residue_offset, residue_atomic, rows, cols, N, B, C, 1,
                     ps::to_hip(stream));
 }
 

@@ -563,6 +563,7 @@ ExecutionLayout PowerSparseMatrixGPU::Execution() const {
     e.residue_offset = _exec_residue_offset;
     e.residue_atomic = _exec_residue_atomic;
     e.out_base = _exec_out_base;
+    e.task_chunk = kRowOrderTaskChunk;
     e.csr_pos = _exec_csr_pos;
   } else {
     e.col_ind = _workset_col_ind;

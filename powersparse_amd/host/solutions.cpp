@@ -55,7 +55,7 @@ void SpMMAsync(const PowerSparseMatrixGPU& m, int N, const float* B, float* C,
   const auto ws = Worksets(m, e);
   ThrowOnError(ps_spmm_launch(m.GroupTypeNum(), ws.data(), e.residue_offset,
                               reinterpret_cast<const uint8_t*>(e.residue_atomic), m.MatrixRow(),
-                              m.MatrixCol(), N, B, C, stream));
+                              m.MatrixCol(), N, B, C, e.task_chunk, stream));
 }
 
 void SpMM(const PowerSparseMatrixGPU& m, int N, const float* B, float* C, int stream_count,
@@ -77,10 +77,10 @@ void SDDMMAsync(const PowerSparseMatrixGPU& m, int N, const float* lhs, const fl
   if (e.out_base)  // row-ordered copy: results written to the public layout
     ThrowOnError(ps_sddmm_scatter_launch(m.GroupTypeNum(), ws.data(), e.residue_offset,
                                          e.out_base, m.MatrixRow(), m.MatrixCol(), N, lhs, rhs,
-                                         out, stream));
+                                         out, e.task_chunk, stream));
   else
     ThrowOnError(ps_sddmm_launch(m.GroupTypeNum(), ws.data(), e.residue_offset, m.MatrixRow(),
-                                 m.MatrixCol(), N, lhs, rhs, out, stream));
+                                 m.MatrixCol(), N, lhs, rhs, out, e.task_chunk, stream));
 }
 
 void SDDMMToCSR(const PowerSparseMatrixGPU& m, int N, const float* lhs, const float* rhs,
@@ -92,7 +92,8 @@ void SDDMMToCSR(const PowerSparseMatrixGPU& m, int N, const float* lhs, const fl
   const ExecutionLayout e = m.Execution();
   const auto ws = Worksets(m, e);
   ThrowOnError(ps_sddmm_csr_launch(m.GroupTypeNum(), ws.data(), e.residue_offset, e.csr_pos,
-                                   m.MatrixRow(), m.MatrixCol(), N, lhs, rhs, out_csr, stream));
+                                   m.MatrixRow(), m.MatrixCol(), N, lhs, rhs, out_csr,
+                                   e.task_chunk, stream));
 }
 
 void WorksetToCSR(const PowerSparseMatrixGPU& m, const float* const* values, float* out_csr,

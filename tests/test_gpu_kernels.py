@@ -241,3 +241,44 @@ def test_residue_order_out_of_range_entries_skipped():
     for g in dropped:
         expect[off[g]:off[g + 1]] = 0.0
     np.testing.assert_array_equal(runs.download(np.float32, n0), expect)
+
+
+@pytest.mark.parametrize("name", ["c1_small", "c4_small", "hubs"])
+def test_task_chunk_mapping(name):
+    """The workgroup -> XCD run length (task_chunk) changes only which XCD runs
+    a task: SDDMM bitwise equal for every chunk, SpMM within tolerance (atomic
+    addition order), invalid chunks rejected before any launch."""
+    setup()
+    csr, w = graph(name)
+    up = Uploaded(w)
+    rng = np.random.default_rng(31)
+    N = 32
+    B = rng.uniform(-1, 1, (csr.cols, N)).astype(np.float32)
+    X = rng.normal(size=(csr.rows, N)).astype(np.float32)
+    Y = rng.normal(size=(csr.cols, N)).astype(np.float32)
+    dB, dX, dY = ps.DeviceBuffer(host=B), ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
+    E, M = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, N, B, with_mag=True)
+    ref = None
+    for chunk in (0, 1, 2, 16, 64, 256):
+        dC = ps.DeviceBuffer.zeros(csr.rows * N * 4)
+        ps.spmm_launch(up.worksets, up.offset, up.atomic, csr.rows, csr.cols, N, dB, dC,
+                       task_chunk=chunk)
+        outs = [ps.DeviceBuffer.zeros(max(w.col[s].size, 1) * 4) for s in range(w.S)]
+        ps.sddmm_launch(up.worksets, up.offset, csr.rows, csr.cols, N, dX, dY, outs,
+                        task_chunk=chunk)
+        ps.synchronize()
+        tolerance.check(dC.download(np.float32).reshape(csr.rows, N), E, M,
+                        f"spmm {name} task_chunk={chunk}")
+        got = [outs[s].download(np.float32, w.col[s].size) for s in range(w.S)]
+        if ref is None:
+            ref = got
+        for s in range(w.S):
+            np.testing.assert_array_equal(got[s], ref[s], err_msg=f"chunk {chunk} workset {s}")
+    dC = ps.DeviceBuffer.zeros(csr.rows * N * 4)
+    for bad in (3, 512, -1):
+        with pytest.raises(ValueError, match="task_chunk"):
+            ps.spmm_launch(up.worksets, up.offset, up.atomic, csr.rows, csr.cols, N, dB, dC,
+                           task_chunk=bad)
+        with pytest.raises(ValueError, match="task_chunk"):
+            ps.sddmm_launch(up.worksets, up.offset, csr.rows, csr.cols, N, dX, dY,
+                            [dC] * w.S, task_chunk=bad)
