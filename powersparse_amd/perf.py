@@ -11,6 +11,12 @@
       gathers (128- and 512-byte rows) against table size: the hardware ceiling
       of the operators' per-nonzero B / Y row gathers.
 
+  python -m powersparse_amd.perf csr [--config C1] [--n 128]
+      Times the SDDMM output orders on one matrix built with csr_positions:
+      workset order (SDDMMAsync), input-CSR order in one launch (SDDMMToCSR),
+      and workset order followed by the permutation (SDDMMAsync +
+      WorksetToCSR); mean of 20 calls after one warm-up, HIP events.
+
   python -m powersparse_amd.perf summarize --trace KT.db [--fetch F.db --write W.db]
         [--l2 L.db] [--valu V.db] [--config C1] [--json OUT.json]
       Reads rocprofv3 SQLite result databases: per kernel the dispatch count and
@@ -127,6 +133,48 @@ def ceiling(args):
     print("\n".join(lines))
 
 
+def csr_order(args):
+    """Times the SDDMM output orders (workset / CSR / workset + permutation)."""
+    import powersparse_amd as ps
+
+    ps.set_device(0)
+    csr = ps.synth(args.config, seed=1)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, csr_positions=True)
+    n, rows, cols = args.n, csr.rows, csr.cols
+    st = ps.Stream()
+    X = ps.DeviceBuffer(rows * n * 4)
+    Y = ps.DeviceBuffer(cols * n * 4)
+    ps.fill_random(X, rows * n, 12, 0.0, 1.0, normal=True, stream=st)
+    ps.fill_random(Y, cols * n, 13, 0.0, 1.0, normal=True, stream=st)
+    outs = [ps.DeviceBuffer(max(sz, 1) * 4) for sz in m.sddmm_output_sizes()]
+    for o in outs:
+        o.zero(st)
+    out_csr = ps.DeviceBuffer(csr.nnz * 4)
+    t0, t1 = ps.Event(), ps.Event()
+
+    def timed(fn, reps=20):
+        fn()
+        t0.record(st)
+        for _ in range(reps):
+            fn()
+        t1.record(st)
+        t1.synchronize()
+        return t0.elapsed_ms(t1) / reps
+
+    def workset_then_csr():
+        ps.SDDMMAsync(m, n, X, Y, outs, st)
+        ps.WorksetToCSR(m, outs, out_csr, st)
+
+    rows_out = [("workset order (SDDMMAsync)", timed(lambda: ps.SDDMMAsync(m, n, X, Y, outs, st))),
+                ("CSR order, one launch (SDDMMToCSR)",
+                 timed(lambda: ps.SDDMMToCSR(m, n, X, Y, out_csr, st))),
+                ("workset order + WorksetToCSR", timed(workset_then_csr))]
+    print(f"SDDMM output order, {args.config} (nnz {csr.nnz}, task order {m.task_order}), "
+          f"N = {n}\n\n| output | ms per call |\n|---|---|")
+    for name, ms in rows_out:
+        print(f"| {name} | {ms:.3f} |")
+
+
 def read_counters(db, counter):
     """[(kernel, grid, value)] of every dispatch, in dispatch order."""
     con = sqlite3.connect(db)
@@ -237,6 +285,9 @@ def main(argv=None):
     w.add_argument("--config", default="C1", choices=sorted(CONFIG_OPS))
     w.add_argument("--steps", type=int, default=3)
     sub.add_parser("ceiling")
+    c = sub.add_parser("csr")
+    c.add_argument("--config", default="C1", choices=sorted(CONFIG_OPS))
+    c.add_argument("--n", type=int, default=128)
     s = sub.add_parser("summarize")
     s.add_argument("--trace", required=True)
     s.add_argument("--fetch")
@@ -250,6 +301,8 @@ def main(argv=None):
         workload(args)
     elif args.cmd == "ceiling":
         ceiling(args)
+    elif args.cmd == "csr":
+        csr_order(args)
     else:
         summarize(args)
     return 0
