@@ -290,6 +290,9 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
       PS_CHECK_ARG(aligned16(w.col_ind), "Block workset arrays must be 16-byte aligned");
       PS_CHECK_ARG(w.group_size >= 32 && (w.group_size & (w.group_size - 1)) == 0,
                    "Block workset group size must be a power of two >= 32");
+      // the kernel indexes a block workset's nonzeros (plus a 64-wide tile) in int
+      PS_CHECK_ARG(uint64_t(w.group_num) * uint64_t(w.group_size) <= uint64_t(INT32_MAX) - 64,
+                   "Block workset exceeds the 32-bit kernel indexing range");
       t = (uint64_t(w.group_num) * w.group_size + 63) / 64;
     } else {
       PS_CHECK_ARG(residue_offset, "Missing residue offsets");
