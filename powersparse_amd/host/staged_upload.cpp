@@ -7,12 +7,21 @@
 
 #include "matrix_utils.h"
 
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
 namespace PowerSparse {
 namespace {
 
 constexpr size_t kChunk = size_t(32) << 20;       // bytes per DMA
 constexpr size_t kMinStaged = size_t(64) << 20;   // smaller copies: one plain copy
 constexpr size_t kCopyBlock = size_t(1) << 20;    // host-copy work item
+// Host threads filling a staging buffer: the copy is bound by host memory
+// bandwidth, and 8 threads beat 16 (measured on the MI355X box: 103 vs 84 GB/s
+// into page-locked memory; C3 upload 33 -> 26 ms, the DMA engine's 56 GB/s
+// being the limit).
+constexpr int kCopyThreads = 8;
 
 // Two page-locked buffers shared by every upload of the process (allocated on
 // first use, kept until exit); one upload at a time uses them.
@@ -29,7 +38,10 @@ StagingPool& Pool() {
 
 void ParallelCopy(void* dst, const void* src, size_t bytes) {
   const long long blocks = (long long)((bytes + kCopyBlock - 1) / kCopyBlock);
-#pragma omp parallel for schedule(static)
+#ifdef _OPENMP
+  const int threads = std::max(1, std::min(kCopyThreads, omp_get_max_threads()));
+#endif
+#pragma omp parallel for schedule(static) num_threads(threads)
   for (long long b = 0; b < blocks; ++b) {
     const size_t off = size_t(b) * kCopyBlock;
     std::memcpy(static_cast<char*>(dst) + off, static_cast<const char*>(src) + off,
