@@ -87,7 +87,8 @@ def test_sddmm_csr_order_random(seed):
     X = rng.normal(size=(csr.rows, N)).astype(np.float32)
     Y = rng.normal(size=(csr.cols, N)).astype(np.float32)
     out = ps.DeviceBuffer(host=np.full(csr.nnz, np.nan, np.float32))
-    ps.SDDMMToCSR(m, N, ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y), out)
+    dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)  # alive until the sync
+    ps.SDDMMToCSR(m, N, dX, dY, out)
     ps.synchronize()
     E, M = expected_csr(csr, N, X, Y)
     tolerance.check(out.download(np.float32, csr.nnz), E, M, "SDDMMToCSR random")

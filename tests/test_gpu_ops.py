@@ -198,7 +198,8 @@ def test_operands_over_4gib():
     say("  ", tolerance.check(C.download(np.float32).reshape(rows, N), E, M, "SpMM > 4 GiB"))
     X = rng.normal(size=(rows, N)).astype(np.float32)
     out = ps.DeviceBuffer(csr.nnz * 4)
-    ps.SDDMMToCSR(m, N, ps.DeviceBuffer(host=X), big, out)
+    dX = ps.DeviceBuffer(host=X)  # alive until the sync
+    ps.SDDMMToCSR(m, N, dX, big, out)
     ps.synchronize()
     E, M = oracle.sddmm(np.arange(rows, dtype=np.int32), csr.row_ptr, cc, csr.values, N, X,
                         compact, with_mag=True)

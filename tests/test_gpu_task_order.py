@@ -25,7 +25,8 @@ def sddmm_public(m, N, dX, dY, calls=1):
 
 
 @pytest.mark.parametrize("cfg,scale,cu,N", [("C0", 1, 256, 32), ("C1", 20, 8, 64),
-                                            ("C4", 16, 256, 64), ("C3", 60, 2, 128)])
+                                            ("C4", 16, 256, 64), ("C3", 60, 2, 128),
+                                            ("C4", 64, 256, 96), ("C4", 64, 256, 256)])
 def test_row_order_matches_signature_order(cfg, scale, cu, N):
     setup()
     csr = ps.synth(cfg, seed=31, scale=scale)
@@ -85,7 +86,8 @@ def test_row_order_random(seed):
     B = rng.uniform(-1, 1, (csr.cols, N)).astype(np.float32)
     E, M = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, N, B, with_mag=True)
     C = ps.DeviceBuffer.zeros(csr.rows * N * 4)
-    ps.SpMMAsync(b, N, ps.DeviceBuffer(host=B), C)
+    dB = ps.DeviceBuffer(host=B)  # alive until the sync
+    ps.SpMMAsync(b, N, dB, C)
     ps.synchronize()
     tolerance.check(C.download(np.float32).reshape(csr.rows, N), E, M, "SpMM row order")
 
