@@ -131,7 +131,7 @@ def per_row_checks(csr, m):
     np.testing.assert_allclose(s_val, np.bincount(row_of, weights=csr.values.astype(np.float64), minlength=rows), rtol=1e-12, atol=1e-9)
 
 
-@pytest.mark.parametrize("cfg", ["C1", "C4"])
+@pytest.mark.parametrize("cfg", ["C1", "C4", "C3"])
 def test_full_size_properties(cfg):
     """At the BASELINE size: worksets preserve every row's entries; SpMM against
     an all-ones B gives each row's value sum, and SpMM is linear in B."""
@@ -157,6 +157,41 @@ def test_full_size_properties(cfg):
     _, M1 = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, N, np.abs(B1) + np.abs(B2),
                         with_mag=True)
     tolerance.check(Cab, Ca.astype(np.float64) + Cb, M1, f"{cfg} SpMM linearity")
+
+
+@pytest.mark.parametrize("cfg", ["C1", "C4", "C3"])
+def test_full_size_sddmm_exact(cfg):
+    """At the BASELINE size, SDDMM with X[i, :] = (i % 5) / 8 and Y[j, :] = j % 7
+    (K = 32): every dot is the exact integer 4 * (i % 5) * (j % 7), so every
+    output is the float32 product value * dot exactly, whatever the summation
+    order; this pins the row and column of every stored nonzero."""
+    setup()
+    csr = ps.synth(cfg, seed=1)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr)
+    say(f"full {cfg} SDDMM exact: nnz={csr.nnz} S={m.GroupTypeNum()} task order {m.task_order}")
+    N = 32
+    X = np.repeat(((np.arange(csr.rows) % 5) / 8.0).astype(np.float32)[:, None], N, 1)
+    Y = np.repeat((np.arange(csr.cols) % 7).astype(np.float32)[:, None], N, 1)
+    dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
+    del X, Y
+    sizes = m.sddmm_output_sizes()
+    outs = [ps.DeviceBuffer.zeros(max(n, 1) * 4) for n in sizes]
+    ps.SDDMMAsync(m, N, dX, dY, outs)
+    ps.synchronize()
+    G = m.GroupNum()
+    for s in range(m.GroupTypeNum()):
+        if G[s] == 0:
+            continue
+        col, val, des = m.download_workset(s)
+        if s == 0:
+            rows = np.repeat(des, np.diff(m.residue_offset()))
+        else:
+            rows = np.repeat(des, 32 << (s - 1))
+        dot = (4 * (rows % 5) * (col % 7)).astype(np.float32)
+        got = outs[s].download(np.float32, sizes[s])
+        # exact equality of values (residue results are added to +0.0, so a
+        # product -0.0 arrives as +0.0)
+        np.testing.assert_array_equal(got, val * dot, err_msg=f"{cfg} workset {s}")
 
 
 def test_operands_over_4gib():
