@@ -88,6 +88,16 @@ def test_full_c4_bit_lists():
     assert w.L == 582720 and w.signature[0] is None
 
 
+@pytest.mark.parametrize("cfg", ["C1", "C3"])
+def test_full_size_bit_exact(cfg):
+    # the BASELINE graphs at full size (C3: 171 M nonzeros, the north-star
+    # graph): every workset array equal to the oracle's, values bitwise
+    setup()
+    csr = ps.synth(cfg, seed=1)
+    say(f"full {cfg} rows={csr.rows} nnz={csr.nnz}")
+    compare(csr, 256)
+
+
 def run_order(group_sets, length):
     """ps_pre_signature_order on worksets given as lists of bit sets."""
     from powersparse_amd import _native
