@@ -194,6 +194,38 @@ def test_full_size_sddmm_exact(cfg):
         np.testing.assert_array_equal(got, val * dot, err_msg=f"{cfg} workset {s}")
 
 
+@pytest.mark.parametrize("cfg,ops", [("C1", [("spmm", 32), ("spmm", 128), ("sddmm", 128),
+                                             ("sddmm", 32)]),
+                                     ("C3", [("spmm", 32), ("spmm", 128), ("sddmm", 128)])])
+def test_full_size_numerics(cfg, ops):
+    """The bench's operators on the full-size BASELINE graph against the
+    oracle's double-precision results (tests/tolerance.py), with the bench's
+    input distributions: B ~ U(-1, 1), X and Y ~ N(0, 1)."""
+    setup()
+    csr = ps.synth(cfg, seed=1)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, csr_positions=True)
+    say(f"full {cfg} numerics: nnz={csr.nnz} task order {m.task_order}")
+    rng = np.random.default_rng(8)
+    rows = np.arange(csr.rows, dtype=np.int32)
+    for op, N in ops:
+        if op == "spmm":
+            B = rng.uniform(-1, 1, (csr.cols, N)).astype(np.float32)
+            C = run_spmm(m, N, B)
+            E, M = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, N, B, with_mag=True)
+            say("  ", tolerance.check(C, E, M, f"{cfg} SpMM N={N}"))
+        else:
+            X = rng.standard_normal((csr.rows, N), dtype=np.float32)
+            Y = rng.standard_normal((csr.cols, N), dtype=np.float32)
+            dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
+            out = ps.DeviceBuffer(csr.nnz * 4)
+            ps.SDDMMToCSR(m, N, dX, dY, out)
+            ps.synchronize()
+            E, M = oracle.sddmm(rows, csr.row_ptr, csr.col_ind, csr.values, N, X, Y,
+                                with_mag=True)
+            say("  ", tolerance.check(out.download(np.float32, csr.nnz), E, M,
+                                      f"{cfg} SDDMM N={N}"))
+
+
 def test_operands_over_4gib():
     # B / Y of cols x 512 floats = 4.3 GB: beyond 32-bit buffer offsets, so the
     # kernels take their 64-bit global-load path. Only three clusters of
