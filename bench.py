@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the PowerSparse hot path on one MI355X.
 
-One step = one pass of the hot path over the synthetic BASELINE graph (config
+One step = one pass of the hot path over the synthetic benchmark graph (config
 C1 by default: Chung-Lu n = 1e6, gamma 2.1, mean degree 50, degree clip 5e4,
 values U(0,1); C2's SDDMM uses the same pattern): SpMM at N = 32, SpMM at
 N = 128, SDDMM at N = 128 and SDDMM at N = 32 (C2's two widths), each one

@@ -86,7 +86,7 @@ int ps_memset_async(void* dst, int value, size_t bytes, ps_stream_t stream);
 /* Fills count floats with a counter-based hash of (seed, index): uniform in
  * [lo, hi) when normal == 0, N(lo, hi^2) (mean lo, std hi) when normal != 0.
  * No counterpart in the reference, whose inputs come from the host
- * (benchmark_utils.h:100-104); used for the synthetic BASELINE configs. */
+ * (benchmark_utils.h:100-104); used for the synthetic benchmark graphs (host/synth.h). */
 int ps_fill_random_async(float* dst, size_t count, uint64_t seed, float lo, float hi,
                          int normal, ps_stream_t stream);
 

@@ -1,7 +1,6 @@
 """The drop-in API end to end on the GPU: PowerSparseMatrixGPU (GPU
 preprocessing) + SpMM / SDDMM with the reference's stream contract, against
-the oracle; argument errors; and size-independent properties at the full
-BASELINE sizes."""
+the oracle; argument errors; and checks at the full benchmark sizes."""
 import numpy as np
 import pytest
 
@@ -133,7 +132,7 @@ def per_row_checks(csr, m):
 
 @pytest.mark.parametrize("cfg", ["C1", "C4", "C3"])
 def test_full_size_properties(cfg):
-    """At the BASELINE size: worksets preserve every row's entries; SpMM against
+    """At full benchmark size (the graphs bench.py builds): worksets preserve every row's entries; SpMM against
     an all-ones B gives each row's value sum, and SpMM is linear in B."""
     setup()
     csr = ps.synth(cfg, seed=1)
@@ -161,7 +160,7 @@ def test_full_size_properties(cfg):
 
 @pytest.mark.parametrize("cfg", ["C1", "C4", "C3"])
 def test_full_size_sddmm_exact(cfg):
-    """At the BASELINE size, SDDMM with X[i, :] = (i % 5) / 8 and Y[j, :] = j % 7
+    """At full benchmark size, SDDMM with X[i, :] = (i % 5) / 8 and Y[j, :] = j % 7
     (K = 32): every dot is the exact integer 4 * (i % 5) * (j % 7), so every
     output is the float32 product value * dot exactly, whatever the summation
     order; this pins the row and column of every stored nonzero."""
@@ -198,7 +197,7 @@ def test_full_size_sddmm_exact(cfg):
                                              ("sddmm", 32)]),
                                      ("C3", [("spmm", 32), ("spmm", 128), ("sddmm", 128)])])
 def test_full_size_numerics(cfg, ops):
-    """The bench's operators on the full-size BASELINE graph against the
+    """The bench's operators on the full-size benchmark graph against the
     oracle's double-precision results (tests/tolerance.py), with the bench's
     input distributions: B ~ U(-1, 1), X and Y ~ N(0, 1)."""
     setup()
