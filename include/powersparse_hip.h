@@ -101,6 +101,17 @@ int ps_copy_f32_async(float* dst, const float* src, size_t count, ps_stream_t st
  * lane, and writes a checksum to out[0]. Its throughput for a given table size
  * is the gather ceiling the SpMM / SDDMM kernels work against. No reference
  * counterpart. */
+/* Measurement probe for the operators' C-row writes: `n` updates of 128-byte
+ * rows of C (rows x 32 floats) at rows hash(seed, i) mod rows. mode 0: plain
+ * 128-bit stores; 1: float atomics with each of 8 lanes adding its own four
+ * consecutive floats one by one (the lanes of one instruction 16 bytes apart);
+ * 2: float atomics, 8 lanes adding 8 consecutive floats per instruction; 3:
+ * float atomics, 32 lanes adding a whole row per instruction. Rows per second
+ * by mode is the cost model of the SpMM kernel's atomic row writes. No
+ * reference counterpart. */
+int ps_probe_row_update_async(float* C, int rows, long long n, int mode, uint64_t seed,
+                              ps_stream_t stream);
+
 int ps_probe_gather_async(const float* table, int rows, int row_floats, long long n,
                           uint64_t seed, float* out, ps_stream_t stream);
 

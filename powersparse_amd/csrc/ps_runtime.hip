@@ -95,10 +95,76 @@ __global__ __launch_bounds__(256) void probe_gather_kernel(const float* table, u
   if (s == -1.2345e-37f) out[0] = s;  // keeps the loads alive; never true for the fills used
 }
 
+// 32-bit index mix used by the probes (two xorshift-multiply rounds).
+__device__ __forceinline__ uint32_t mix32(uint32_t h) {
+  h = (h ^ (h >> 16)) * 0x7feb352du;
+  h = (h ^ (h >> 15)) * 0x846ca68bu;
+  return h ^ (h >> 16);
+}
+
+// n updates of 128-byte rows of C (rows x 32 floats) at uniformly random rows;
+// a wave handles 8 rows per step. Modes: 0 plain float4 stores (8 lanes per
+// row); 1 float atomics, each of 8 lanes adding its float4 component by
+// component (per instruction the lanes of a row are 16 bytes apart); 2 float
+// atomics, 8 lanes adding 8 consecutive floats per instruction; 3 float
+// atomics, 32 lanes adding a whole row per instruction.
+template <int MODE>
+__global__ __launch_bounds__(256) void probe_row_update_kernel(float* __restrict__ C,
+                                                               uint32_t rows, uint64_t n,
+                                                               uint32_t seed) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t wave = (uint64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  const uint64_t waves = (uint64_t(gridDim.x) * blockDim.x) >> 6;
+  auto row_of = [&](uint64_t k) {
+    return size_t((uint64_t(mix32(uint32_t(k) ^ seed)) * rows) >> 32) * 32u;
+  };
+  for (uint64_t base = wave * 8; base < n; base += waves * 8) {
+    if constexpr (MODE == 3) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint64_t k = base + 2 * i + lane / 32;
+        if (k < n) unsafeAtomicAdd(C + row_of(k) + lane % 32, 1.0f);
+      }
+    } else {
+      const int slot = lane / 8, sub = lane % 8;
+      const uint64_t k = base + slot;
+      if (k >= n) continue;
+      float* const row = C + row_of(k);
+      if constexpr (MODE == 0) {
+        *reinterpret_cast<float4*>(row + 4 * sub) = make_float4(1.f, 2.f, 3.f, 4.f);
+      } else if constexpr (MODE == 1) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) unsafeAtomicAdd(row + 4 * sub + c, 1.0f);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) unsafeAtomicAdd(row + 8 * c + sub, 1.0f);
+      }
+    }
+  }
+}
+
 }  // namespace
 }  // namespace ps
 
 extern "C" {
+
+int ps_probe_row_update_async(float* C, int rows, long long n, int mode, uint64_t seed,
+                              ps_stream_t stream) {
+  PS_CHECK_ARG(C && rows > 0 && n >= 0 && mode >= 0 && mode <= 3,
+               "ps_probe_row_update_async: bad argument");
+  PS_CHECK_ARG(ps::aligned16(C), "ps_probe_row_update_async: C must be 16-byte aligned");
+  const unsigned grid = 256 * 16;
+  hipStream_t st = ps::to_hip(stream);
+  const uint32_t r = uint32_t(rows), s = uint32_t(seed);
+  switch (mode) {
+    case 0: ps::probe_row_update_kernel<0><<<grid, 256, 0, st>>>(C, r, uint64_t(n), s); break;
+    case 1: ps::probe_row_update_kernel<1><<<grid, 256, 0, st>>>(C, r, uint64_t(n), s); break;
+    case 2: ps::probe_row_update_kernel<2><<<grid, 256, 0, st>>>(C, r, uint64_t(n), s); break;
+    default: ps::probe_row_update_kernel<3><<<grid, 256, 0, st>>>(C, r, uint64_t(n), s); break;
+  }
+  PS_LAUNCHED();
+  return PS_OK;
+}
 
 int ps_probe_gather_async(const float* table, int rows, int row_floats, long long n,
                           uint64_t seed, float* out, ps_stream_t stream) {

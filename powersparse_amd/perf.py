@@ -7,9 +7,11 @@
       `rocprofv3 --pmc FETCH_SIZE` and `rocprofv3 --pmc WRITE_SIZE`.
 
   python -m powersparse_amd.perf ceiling
-      Streaming-copy bandwidth and the throughput of uniformly random row
-      gathers (128- and 512-byte rows) against table size: the hardware ceiling
-      of the operators' per-nonzero B / Y row gathers.
+      Streaming-copy bandwidth, the throughput of uniformly random row
+      gathers (128- and 512-byte rows) against table size (the hardware
+      ceiling of the operators' per-nonzero B / Y row gathers), and the rate of
+      128-byte row updates at random rows by plain stores and by float atomics
+      in three lane layouts (the cost of the SpMM kernel's C-row writes).
 
   python -m powersparse_amd.perf csr [--config C1] [--n 128]
       Times the SDDMM output orders on one matrix built with csr_positions:
@@ -94,7 +96,8 @@ def workload(args):
 
 
 def ceiling(args):
-    """Streaming-copy bandwidth and random row-gather throughput vs table size."""
+    """Streaming-copy bandwidth, random row-gather throughput vs table size, and
+    random row-update rates by store and atomic lane layout."""
     import powersparse_amd as ps
     from powersparse_amd import _native
 
@@ -124,12 +127,21 @@ def ceiling(args):
              f"| streaming copy (read + write) | 1 GiB | {ms:.3f} | {2 * (1 << 30) / ms / 1e6:.0f} |"]
     n = 1 << 24
     for row_floats in (32, 128):
-        for mb in (8, 32, 128, 256, 512, 2048):
+        for mb in (2, 4, 8, 32, 128, 256, 512, 2048):
             rows = (mb << 20) // (4 * row_floats)
             ms = timed(lambda: ps._hip_call(_native.hip().ps_probe_gather_async(
                 table.ptr, rows, row_floats, n, 9, out.ptr, st.ptr)))
             lines.append(f"| random {4 * row_floats}-byte row gathers | {mb} MB table | "
                          f"{ms:.3f} | {n * 4 * row_floats / ms / 1e6:.0f} |")
+    lines += ["", "| 128-byte row updates at random rows of a 128 MB C | time for 4 M (ms) | "
+                  "M rows/s |", "|---|---|---|"]
+    modes = ("plain 128-bit stores", "float atomics, lanes 16 B apart (4 per lane)",
+             "float atomics, 8 lanes x 4 consecutive bytes", "float atomics, 32 lanes per row")
+    nu = 1 << 22
+    for mode, name in enumerate(modes):
+        ms = timed(lambda: ps._hip_call(_native.hip().ps_probe_row_update_async(
+            dst.ptr, 1 << 20, nu, mode, 5, st.ptr)))
+        lines.append(f"| {name} | {ms:.3f} | {nu / ms / 1e3:.0f} |")
     print("\n".join(lines))
 
 
