@@ -221,8 +221,8 @@ def main():
         "config": {"workload": WORKLOADS[args.config], "graph": args.config, "rows": rows,
                    "nnz": nnz, "worksets": S, "group_num": m.GroupNum(),
                    "preprocess_ms": preprocess_ms, "parallelism": "single GPU",
-                   "device": f"{props['name']} ({props['arch'].split(':')[0]}, "
-                             f"{props['cu_count']} CUs)"},
+                   "device": (f"{props['name']} " if props["name"].strip() else "")
+                             + f"({props['arch'].split(':')[0]}, {props['cu_count']} CUs)"},
         "ops": detail,
         "roofline": {"bound": "hbm", "kernel": kernel, "op": f"{dom['op']} N={dom['N']}",
                      "achieved": dom["alg_GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",

@@ -35,6 +35,7 @@ namespace {
 constexpr int kWavesPerBlock = 4;
 constexpr int kStage = 32;  // residue columns staged in LDS per slot
 constexpr int kTaskOut = 256;  // residue results of one task collected in LDS
+static_assert(kTaskOut >= 8 * kStage, "a task's slots each collect up to kStage results");
 
 struct SddmmArgs {
   ps_workset ws[PS_MAX_WORKSETS];
@@ -188,6 +189,9 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     const int beg = has ? args.residue_offset[g] : 0;
     const int len = has ? args.residue_offset[g + 1] - beg : 0;
     const int row = has ? ws.group_des[g] : 0;
+    // row-order copy (mode 2) adding its results: a group of up to kStage
+    // results is collected in LDS and added with 32 lanes on its output range
+    const bool group_collect = kMode == 2 && args.residue_add && len <= kStage;
 #pragma unroll
     for (int qq = 0; qq < KQ; ++qq)
       x[qq] = X.load(Off(uint32_t(row)) * row_bytes + piece + 128u * qq);
@@ -226,14 +230,32 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
       const int k = c0 + sub;
       if (k < len) {
         const float v = dot * ws.sp_data[beg + k];
-        if constexpr (kMode != 0) {
-          const int at = kMode == 1 ? out_pos[beg + k] : out_pos[g] + k;
+        if constexpr (kMode == 2) {
+          if (group_collect) res_lds[slot * kStage + k] = v;
+          else if (args.residue_add) unsafeAtomicAdd(out + out_pos[g] + k, v);
+          else out[out_pos[g] + k] = v;
+        } else if constexpr (kMode == 1) {
+          const int at = out_pos[beg + k];
           if (args.residue_add) unsafeAtomicAdd(out + at, v);
           else out[at] = v;
         } else if (collect) {
           res_lds[beg + k - out0] = v;
         } else {
           unsafeAtomicAdd(out + beg + k, v);
+        }
+      }
+    }
+    if constexpr (kMode == 2) {
+      // groups of up to kStage results, collected per slot: two groups per
+      // instruction, 32 lanes on each group's contiguous output range
+      if (args.residue_add) {
+        const int base = has ? out_pos[g] : 0;
+        wave_lds_sync();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int q = 2 * j + lane / 32, e = lane % 32;
+          const int lq = __shfl(len, q * 8), bq = __shfl(base, q * 8);
+          if (e < lq && lq <= kStage) unsafeAtomicAdd(out + bq + e, res_lds[q * kStage + e]);
         }
       }
     }
