@@ -195,11 +195,14 @@ def test_full_size_sddmm_exact(cfg):
 
 @pytest.mark.parametrize("cfg,ops", [("C1", [("spmm", 32), ("spmm", 128), ("sddmm", 128),
                                              ("sddmm", 32)]),
-                                     ("C3", [("spmm", 32), ("spmm", 128), ("sddmm", 128)])])
+                                     ("C3", [("spmm", 32), ("spmm", 128), ("sddmm", 128)]),
+                                     ("C4", [("spmm", 64), ("sddmm", 64)])])
 def test_full_size_numerics(cfg, ops):
     """The bench's operators on the full-size benchmark graph against the
     oracle's double-precision results (tests/tolerance.py), with the bench's
-    input distributions: B ~ U(-1, 1), X and Y ~ N(0, 1)."""
+    input distributions: B ~ U(-1, 1), X and Y ~ N(0, 1). SDDMM is checked in
+    CSR order and in workset order (each stored nonzero's CSR position maps it
+    back; C4 runs its row-ordered execution copy)."""
     setup()
     csr = ps.synth(cfg, seed=1)
     m = ps.PowerSparseMatrixGPU.from_csr(csr, csr_positions=True)
@@ -222,7 +225,17 @@ def test_full_size_numerics(cfg, ops):
             E, M = oracle.sddmm(rows, csr.row_ptr, csr.col_ind, csr.values, N, X, Y,
                                 with_mag=True)
             say("  ", tolerance.check(out.download(np.float32, csr.nnz), E, M,
-                                      f"{cfg} SDDMM N={N}"))
+                                      f"{cfg} SDDMM N={N} (CSR order)"))
+            # the workset-order operator (the bench's call), mapped to CSR order
+            sizes = m.sddmm_output_sizes()
+            outs = [ps.DeviceBuffer.zeros(max(sz, 1) * 4) for sz in sizes]
+            ps.SDDMMAsync(m, N, dX, dY, outs)
+            ps.synchronize()
+            ws = np.full(csr.nnz, np.nan, np.float32)
+            for s, sz in enumerate(sizes):
+                if sz:
+                    ws[m.download_csr_position(s)] = outs[s].download(np.float32, sz)
+            say("  ", tolerance.check(ws, E, M, f"{cfg} SDDMM N={N} (workset order)"))
 
 
 def test_operands_over_4gib():
