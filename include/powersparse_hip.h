@@ -101,6 +101,12 @@ int ps_copy_f32_async(float* dst, const float* src, size_t count, ps_stream_t st
  * lane, and writes a checksum to out[0]. Its throughput for a given table size
  * is the gather ceiling the SpMM / SDDMM kernels work against. No reference
  * counterpart. */
+/* Records in out[b] the XCD (XCC) that runs workgroup b of a launch of
+ * `workgroups` workgroups, read from the hardware's XCC_ID register. The
+ * operators' workgroup -> task mapping (task_chunk) assumes the hardware's
+ * round robin, workgroup b on XCD b mod 8. No reference counterpart. */
+int ps_probe_xcc_ids_async(int* out, int workgroups, ps_stream_t stream);
+
 /* Measurement probe for the operators' C-row writes: `n` updates of 128-byte
  * rows of C (rows x 32 floats) at rows hash(seed, i) mod rows. mode 0: plain
  * 128-bit stores; 1: float atomics with each of 8 lanes adding its own four

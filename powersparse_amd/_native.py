@@ -86,6 +86,7 @@ HIP_API = [
      [c_void_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_int,
       c_void_p]),
     ("ps_copy_f32_async", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
+    ("ps_probe_xcc_ids_async", ctypes.c_int, [c_void_p, ctypes.c_int, c_void_p]),
     ("ps_probe_row_update_async", ctypes.c_int,
      [c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_int, ctypes.c_uint64, c_void_p]),
     ("ps_probe_gather_async", ctypes.c_int,

@@ -143,10 +143,24 @@ __global__ __launch_bounds__(256) void probe_row_update_kernel(float* __restrict
   }
 }
 
+// Writes the XCC (XCD) id of every workgroup: hardware register XCC_ID
+// (s_getreg_b32, bits 3:0), read by the workgroup's first lane.
+__global__ void probe_xcc_kernel(int* __restrict__ out, int n) {
+  if (threadIdx.x == 0 && int(blockIdx.x) < n)
+    out[blockIdx.x] = int(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 0xF);
+}
+
 }  // namespace
 }  // namespace ps
 
 extern "C" {
+
+int ps_probe_xcc_ids_async(int* out, int workgroups, ps_stream_t stream) {
+  PS_CHECK_ARG(out && workgroups > 0, "ps_probe_xcc_ids_async: bad argument");
+  ps::probe_xcc_kernel<<<unsigned(workgroups), 64, 0, ps::to_hip(stream)>>>(out, workgroups);
+  PS_LAUNCHED();
+  return PS_OK;
+}
 
 int ps_probe_row_update_async(float* C, int rows, long long n, int mode, uint64_t seed,
                               ps_stream_t stream) {

@@ -77,3 +77,17 @@ def test_row_update_probe(mode):
         assert got.sum(dtype=np.float64) == 32.0 * n
         # each touched row holds the same count in all 32 floats
         np.testing.assert_array_equal(got, got[:, :1].repeat(32, 1))
+
+
+def test_workgroups_dealt_round_robin_over_xcds():
+    """The task_chunk mapping assumes the hardware deals workgroups round-robin
+    over the XCDs: workgroup b on XCD b mod (number of XCDs)."""
+    setup()
+    n = 4096
+    say("xcc ids of 4096 workgroups")
+    out = ps.DeviceBuffer(n * 4)
+    ps._hip_call(_native.hip().ps_probe_xcc_ids_async(out.ptr, n, None))
+    ids = out.download(np.int32, n)
+    xcds = int(ids.max()) + 1
+    assert xcds == 8 or ps.device_props(0)["cu_count"] != 256
+    np.testing.assert_array_equal(ids, np.arange(n) % xcds)
