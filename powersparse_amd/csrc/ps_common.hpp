@@ -84,8 +84,10 @@ __device__ __forceinline__ float xor_shfl(float v) {
   return __int_as_float(r);
 }
 
-// Workgroup -> logical index. The hardware deals workgroups round-robin over
-// the 8 XCDs, each with its own L2. With chunk = 2^chunk_log2 > 1, windows of
+// Workgroup -> logical index. The hardware deals a launch's workgroups
+// round-robin over the 8 XCDs, each with its own L2: workgroup b runs on XCD
+// (x0 + b) mod 8, x0 being where the previous dispatch's dealing stopped, so
+// workgroups b and b' share an XCD exactly when b = b' mod 8. With chunk = 2^chunk_log2 > 1, windows of
 // 8 * chunk consecutive workgroups are re-dealt so that each XCD takes chunk
 // consecutive logical indices: neighbouring tasks run under one L2, while every
 // XCD still gets a slice of every window, which keeps the XCDs balanced when

@@ -26,7 +26,7 @@
 // cols * N * 4 fits in 32 bits.
 //
 // Workgroup -> task mapping: the hardware deals workgroups round-robin over
-// the 8 XCDs. With task_chunk > 1, windows of 8 * task_chunk consecutive
+// the 8 XCDs (workgroups b and b + 8 on the same one). With task_chunk > 1, windows of 8 * task_chunk consecutive
 // workgroups are re-dealt so that each XCD takes task_chunk consecutive ones:
 // neighbouring tasks share an XCD's L2, while every XCD still gets a slice of
 // every window (balance when task costs vary along the list). Worksets in row
