@@ -7,10 +7,10 @@
 //
 // Radix pass = histogram kernel + scan of the (digit-major, tile-minor) count
 // table + scatter kernel. The scatter ranks each tile's elements stably: wave w
-// of the tile owns items [1024w, 1024w + 1024) and walks them in 16 rounds of 64
-// in order; inside a round the lanes holding the same 8-bit digit are found with
-// eight ballots, so an element's offset is (earlier rounds' count of its digit in
-// this wave) + (lower lanes with the same digit in this round). Wave prefixes and
+// of the tile owns items [1024w, 1024w + 1024) and walks them in 16 steps of 64
+// in order; inside a step the lanes holding the same 8-bit digit are found with
+// eight ballots, so an element's offset is (earlier steps' count of its digit in
+// this wave) + (lower lanes with the same digit in this step). Wave prefixes and
 // the tile's global digit offsets from the scanned table complete the position.
 #include <vector>
 
