@@ -15,7 +15,10 @@ operator, benchmark.cu:189) / wall time between two events, in GFLOPS; the
 `roofline` object is for the dominant kernel (algorithmic bytes per launch /
 its mean launch time, HIP events on its stream); `cpu_baseline` is the OpenMP
 double-precision restatement of the reference's check path (the oracle) timed
-on this host over the same graph and operators.
+on this host over the same graph and operators. `roofline.traffic` is the
+kernel's measured HBM-side bytes per launch (calibrated FETCH_SIZE + WRITE_SIZE
+from the committed rocprofv3 summary of the same workload), `traffic_GBps` that
+over the launch time.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C1]
 """
@@ -227,6 +230,10 @@ def main():
         "roofline": {"bound": "hbm", "kernel": kernel, "op": f"{dom['op']} N={dom['N']}",
                      "achieved": dom["alg_GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": dom["roofline_frac"], "traffic": traffic,
+                     # measured HBM-side bytes per launch over the same launch time
+                     "traffic_GBps": traffic / (dom["ms"] * 1e-3) / 1e9 if traffic else None,
+                     "traffic_frac": (traffic / (dom["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBPS
+                                      if traffic else None),
                      "l2_hit_pct": counters.get("l2_hit_pct"),
                      "valu_busy_pct": counters.get("valu_busy_pct"),
                      "valu_utilization_pct": counters.get("valu_utilization_pct"),
