@@ -16,9 +16,9 @@ operator, benchmark.cu:189) / wall time between two events, in GFLOPS; the
 its mean launch time, HIP events on its stream); `cpu_baseline` is the OpenMP
 double-precision restatement of the reference's check path (the oracle) timed
 on this host over the same graph and operators. `roofline.traffic` is the
-kernel's measured HBM-side bytes per launch (calibrated FETCH_SIZE + WRITE_SIZE
-from the committed rocprofv3 summary of the same workload), `traffic_GBps` that
-over the launch time.
+bytes per launch the kernel's L2 exchanges with the memory fabric (Infinity
+Cache and HBM; calibrated FETCH_SIZE + WRITE_SIZE from the committed rocprofv3
+summary of the same workload), `traffic_GBps` that over the launch time.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C1]
 """
@@ -230,7 +230,7 @@ def main():
         "roofline": {"bound": "hbm", "kernel": kernel, "op": f"{dom['op']} N={dom['N']}",
                      "achieved": dom["alg_GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": dom["roofline_frac"], "traffic": traffic,
-                     # measured HBM-side bytes per launch over the same launch time
+                     # measured L2 <-> fabric bytes per launch over the launch time
                      "traffic_GBps": traffic / (dom["ms"] * 1e-3) / 1e9 if traffic else None,
                      "traffic_frac": (traffic / (dom["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBPS
                                       if traffic else None),
