@@ -231,3 +231,59 @@ def test_rank_sort_row_classes():
                                                 max_count, cb, keys.ptr, vals.ptr, None))
     np.testing.assert_array_equal(vals.download(np.uint32), order.astype(np.uint32))
     np.testing.assert_array_equal(keys.download(np.uint64), exp_keys)
+
+
+def _snapshot(m):
+    """Every public array of a matrix, on the host."""
+    ws = [m.download_workset(s) if m.GroupNum()[s] else None for s in range(m.GroupTypeNum())]
+    return m.GroupNum(), m.SignatureLen(), m.residue_offset(), m.residue_atomic(), ws
+
+
+def _assert_same(a, b, what):
+    assert a[0] == b[0] and a[1] == b[1], what
+    np.testing.assert_array_equal(a[2], b[2], err_msg=what)
+    np.testing.assert_array_equal(a[3], b[3], err_msg=what)
+    for s, (x, y) in enumerate(zip(a[4], b[4])):
+        if x is None:
+            assert y is None, what
+            continue
+        for k in range(3):
+            np.testing.assert_array_equal(x[k].view(np.uint32), y[k].view(np.uint32),
+                                          err_msg=f"{what} workset {s}")
+
+
+def test_concurrent_constructions():
+    """Matrices built at the same time from several host threads (the shared
+    default stream, the process-wide page-locked staging buffers of the
+    full-size upload, each construction's column-bit helper thread) equal the
+    same matrices built one at a time, and the small ones the oracle's."""
+    from concurrent.futures import ThreadPoolExecutor
+    setup()
+    graphs = [ps.synth("C4", seed=1), ps.synth("C1", seed=2, scale=20),
+              ps.synth("C4", seed=1), ps.synth("C3", seed=3, scale=40)]
+    say("concurrent constructions: " + ", ".join(str(g.nnz) for g in graphs))
+
+    def build(csr):
+        m = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=8)
+        snap = _snapshot(m)
+        m.close()
+        return snap
+
+    with ThreadPoolExecutor(len(graphs)) as ex:
+        together = list(ex.map(build, graphs))
+    alone = [build(g) for g in graphs]
+    for i, (a, b) in enumerate(zip(together, alone)):
+        _assert_same(a, b, f"graph {i}: concurrent vs sequential")
+    for i in (1, 3):
+        csr = graphs[i]
+        w = oracle.preprocess(csr.rows, csr.cols, csr.row_ptr, csr.col_ind, csr.values, 8)
+        gn, L, ro, ra, ws = together[i]
+        assert gn == w.group_num and L == w.L
+        np.testing.assert_array_equal(ro, w.residue_offset)
+        np.testing.assert_array_equal(ra, w.residue_atomic)
+        for s in range(w.S):
+            if w.group_num[s]:
+                col, val, des = ws[s]
+                np.testing.assert_array_equal(col, w.col[s])
+                np.testing.assert_array_equal(val.view(np.uint32), w.val[s].view(np.uint32))
+                np.testing.assert_array_equal(des, w.des[s])
