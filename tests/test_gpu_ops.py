@@ -320,3 +320,43 @@ def test_misaligned_buffers_rejected():
     ps.spmm_launch(ws, m.ResidueOffset(), m.ResidueAtomic(), csr.rows, csr.cols, N, B.ptr,
                    C.ptr)
     ps.synchronize()
+
+
+def test_operators_on_concurrent_streams():
+    """SpMM and SDDMM of two matrices enqueued on two streams at once (the
+    kernels keep no state between calls) give the results of the same calls
+    made one at a time: SDDMM bitwise, SpMM within FP32 atomic reordering."""
+    setup()
+    a = ps.synth("C1", seed=5, scale=20)
+    b = ps.synth("C4", seed=6, scale=16)
+    ma = ps.PowerSparseMatrixGPU.from_csr(a)
+    mb = ps.PowerSparseMatrixGPU.from_csr(b)
+    say(f"concurrent streams: nnz {a.nnz} / {b.nnz}, task orders {ma.task_order} / {mb.task_order}")
+    rng = np.random.default_rng(12)
+    N = 64
+    B = ps.DeviceBuffer(host=rng.uniform(-1, 1, (a.cols, N)).astype(np.float32))
+    X = ps.DeviceBuffer(host=rng.standard_normal((b.rows, N), dtype=np.float32))
+    Y = ps.DeviceBuffer(host=rng.standard_normal((b.cols, N), dtype=np.float32))
+    sizes = mb.sddmm_output_sizes()
+
+    def run(sa, sb):
+        C = ps.DeviceBuffer.zeros(a.rows * N * 4)
+        outs = [ps.DeviceBuffer.zeros(max(sz, 1) * 4) for sz in sizes]
+        ps.synchronize()  # the zero fills first
+        for _ in range(3):  # accumulate: C and the residue outputs add up over calls
+            ps.SpMMAsync(ma, N, B, C, sa)
+            ps.SDDMMAsync(mb, N, X, Y, outs, sb)
+        ps.synchronize()
+        return (C.download(np.float32),
+                [o.download(np.float32, sz) if sz else None for o, sz in zip(outs, sizes)])
+
+    s1, s2 = ps.Stream(), ps.Stream()
+    c_cc, o_cc = run(s1, s2)
+    c_seq, o_seq = run(s1, s1)
+    # the two runs differ only in the order of FP32 atomic additions into C
+    # (three calls accumulated): a few units of 2^-24 of the summed magnitudes
+    np.testing.assert_allclose(c_cc, c_seq, rtol=1e-4, atol=1e-6 * np.abs(c_seq).max())
+    for s, (x, y) in enumerate(zip(o_cc, o_seq)):
+        if x is not None:
+            np.testing.assert_array_equal(x.view(np.uint32), y.view(np.uint32),
+                                          err_msg=f"SDDMM workset {s}")
