@@ -69,6 +69,10 @@ int ps_device_synchronize(void);
  * benchmark_utils.h:13-37). ps_free(NULL) is a no-op. */
 int ps_malloc(void** ptr, size_t bytes);
 int ps_free(void* ptr);
+/* Free and total device memory of the current device, in bytes (hipMemGetInfo).
+ * No reference counterpart: callers and tests use it to check that a matrix
+ * releases every device allocation it made. */
+int ps_mem_get_info(size_t* free_bytes, size_t* total_bytes);
 /* Replaces: thrust::copy / cudaMemcpy H2D and D2H (matrix_utils.cu:495-497, 637;
  * benchmark_utils.h:30-46). Synchronous with respect to the host. */
 int ps_memcpy_htod(void* dst, const void* src, size_t bytes);

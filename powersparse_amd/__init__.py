@@ -66,6 +66,13 @@ def device_count():
     return n.value
 
 
+def mem_get_info():
+    """(free, total) bytes of device memory on the current device."""
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    _hip_call(_native.hip().ps_mem_get_info(ctypes.byref(free), ctypes.byref(total)))
+    return free.value, total.value
+
+
 def device_props(device=0):
     p = DeviceProps()
     _hip_call(_native.hip().ps_get_device_props(device, ctypes.byref(p)))

@@ -74,6 +74,8 @@ HIP_API = [
     ("ps_driver_version", ctypes.c_int, [c_int_p]),
     ("ps_device_synchronize", ctypes.c_int, []),
     ("ps_malloc", ctypes.c_int, [ctypes.POINTER(c_void_p), ctypes.c_size_t]),
+    ("ps_mem_get_info", ctypes.c_int,
+     [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
     ("ps_free", ctypes.c_int, [c_void_p]),
     ("ps_memcpy_htod", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t]),
     ("ps_memcpy_dtoh", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t]),

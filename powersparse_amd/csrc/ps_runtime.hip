@@ -289,6 +289,12 @@ int ps_free(void* ptr) {
   return PS_OK;
 }
 
+int ps_mem_get_info(size_t* free_bytes, size_t* total_bytes) {
+  PS_CHECK_ARG(free_bytes && total_bytes, "ps_mem_get_info: null output");
+  PS_HIP(hipMemGetInfo(free_bytes, total_bytes));
+  return PS_OK;
+}
+
 int ps_memcpy_htod(void* dst, const void* src, size_t bytes) {
   if (bytes == 0) return PS_OK;
   PS_CHECK_ARG(dst && src, "ps_memcpy_htod: null pointer");

@@ -287,3 +287,27 @@ def test_concurrent_constructions():
                 np.testing.assert_array_equal(col, w.col[s])
                 np.testing.assert_array_equal(val.view(np.uint32), w.val[s].view(np.uint32))
                 np.testing.assert_array_equal(des, w.des[s])
+
+
+def test_constructions_release_device_memory():
+    """Building and closing matrices, with and without the row-ordered
+    execution copy and the CSR positions, leaves the device's free memory
+    where it was."""
+    setup()
+    graphs = [ps.synth("C1", seed=2, scale=10), ps.synth("C4", seed=4, scale=8)]
+    # one warm-up pass: runtime-internal buffers of first use are not leaks
+    for csr in graphs:
+        ps.PowerSparseMatrixGPU.from_csr(csr).close()
+    ps.synchronize()
+    free0, total = ps.mem_get_info()
+    say(f"device memory free {free0 >> 20} MB of {total >> 20} MB")
+    for rep in range(3):
+        for csr in graphs:
+            for kw in ({}, {"csr_positions": True}, {"task_order": "row"},
+                       {"task_order": "signature", "csr_positions": True}):
+                m = ps.PowerSparseMatrixGPU.from_csr(csr, **kw)
+                m.close()
+    ps.synchronize()
+    free1, _ = ps.mem_get_info()
+    say(f"after 24 constructions: free {free1 >> 20} MB")
+    assert free1 >= free0 - (4 << 20), (free0, free1)
