@@ -61,3 +61,18 @@ def random_graph(rng, rows, cols, max_deg, hubs=0, hub_deg=0, dup=False):
     ci = np.concatenate(ci) if ci else np.zeros(0, np.int32)
     va = rng.uniform(-1, 1, ci.size).astype(np.float32)
     return ps.HostCsr(rows, cols, np.array(rp, np.int32), ci, va)
+
+
+def star_graph(rng, rows, cols, max_deg, long_rows=0, long_deg=0):
+    """Every row holds the two hub columns 0 and 1 plus up to max_deg random
+    other columns (long_rows rows: long_deg): two columns as popular as there
+    are rows, ties everywhere else."""
+    rp, ci = [0], []
+    for r in range(rows):
+        d = long_deg if r < long_rows else int(rng.integers(0, max_deg + 1))
+        other = np.unique(rng.integers(2, cols, d))
+        ci.append(np.concatenate([[0, 1], other]).astype(np.int32))
+        rp.append(rp[-1] + len(ci[-1]))
+    ci = np.concatenate(ci)
+    return ps.HostCsr(rows, cols, np.array(rp, np.int32), ci,
+                      rng.uniform(-1, 1, ci.size).astype(np.float32))

@@ -8,7 +8,7 @@ import pytest
 import oracle
 import powersparse_amd as ps
 import tolerance
-from gpu_util import Uploaded, random_graph, say, setup
+from gpu_util import Uploaded, random_graph, say, setup, star_graph
 
 pytestmark = pytest.mark.gpu
 
@@ -21,6 +21,8 @@ GRAPHS = {
     "hubs": (lambda: random_graph(np.random.default_rng(5), 300, 5000, 40, hubs=6,
                                   hub_deg=4500), 1),
     "dups": (lambda: random_graph(np.random.default_rng(6), 200, 50, 90, dup=True), 1),
+    "star": (lambda: star_graph(np.random.default_rng(7), 20000, 9000, 8, long_rows=40,
+                                long_deg=700), 4),
 }
 _cache = {}
 

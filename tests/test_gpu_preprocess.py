@@ -5,7 +5,7 @@ import pytest
 
 import oracle
 import powersparse_amd as ps
-from gpu_util import random_graph, say, setup
+from gpu_util import random_graph, say, setup, star_graph
 from test_oracle_preprocess import csr_from_rows
 
 pytestmark = pytest.mark.gpu
@@ -311,3 +311,16 @@ def test_constructions_release_device_memory():
     free1, _ = ps.mem_get_info()
     say(f"after 24 constructions: free {free1 >> 20} MB")
     assert free1 >= free0 - (4 << 20), (free0, free1)
+
+
+@pytest.mark.parametrize("order", ORDERS)
+def test_star_columns(order):
+    """Two hub columns in every row (col_nnz = rows for both, the two top
+    columns FFC puts in bucket 0), many rows tied on every other column
+    count, plus a few long rows: ranking ties, one huge histogram bin and
+    signatures that all share their first bit."""
+    setup()
+    csr = star_graph(np.random.default_rng(77), 120000, 50000, 8, long_rows=40, long_deg=700)
+    say(f"star columns rows={csr.rows} nnz={csr.nnz} order={order}")
+    w = compare(csr, 4, order)
+    assert w.S >= 2
