@@ -72,7 +72,7 @@ def test_spmm_kernel(name, N):
 
 
 @pytest.mark.parametrize("name", sorted(GRAPHS))
-@pytest.mark.parametrize("N", [32, 64, 128, 96])
+@pytest.mark.parametrize("N", [32, 64, 128, 96, 256, 512])
 def test_sddmm_kernel(name, N):
     setup()
     csr, w = graph(name)
