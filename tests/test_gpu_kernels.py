@@ -47,7 +47,7 @@ def row_factor(csr, w):
 
 
 @pytest.mark.parametrize("name", sorted(GRAPHS))
-@pytest.mark.parametrize("N", [32, 64, 128, 96, 256, 288])
+@pytest.mark.parametrize("N", [32, 64, 128, 96, 256, 288, 1024])
 def test_spmm_kernel(name, N):
     setup()
     csr, w = graph(name)
