@@ -139,7 +139,8 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     const int total = ws.group_num * ws.group_size;
     const int p0 = local * 64 + slot * 8;
     const bool valid = p0 < total;
-    const int g = valid ? p0 / ws.group_size : 0;
+    const int gs_shift = __builtin_ctz(unsigned(ws.group_size));  // a power of two
+    const int g = valid ? p0 >> gs_shift : 0;
     const int row = valid ? ws.group_des[g] : 0;
     int4 c0 = make_int4(0, 0, 0, 0), c1 = make_int4(0, 0, 0, 0);
     if (valid) {
@@ -159,7 +160,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
       if constexpr (kMode == 1) {
         out[out_pos[pos]] = v;
       } else if constexpr (kMode == 2) {
-        const int gl = pos / ws.group_size;
+        const int gl = pos >> gs_shift;
         out[out_pos[gl] + (pos - gl * ws.group_size)] = v;
       } else {
         out[pos] = v;

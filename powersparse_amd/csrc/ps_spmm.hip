@@ -201,7 +201,8 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs ar
     acc.w = group_sum<LPN>(acc.w, spg);
     // every slot of a group holds its sum; the group's first slot adds it
     const bool leader = slot_first < total && slot % spg == 0;
-    const int row = leader ? ws.group_des[int(slot_first / GS)] : -1;
+    // GS is a power of two (checked at launch): a shift, not a 64-bit division
+    const int row = leader ? ws.group_des[int(slot_first >> __builtin_ctz(unsigned(GS)))] : -1;
     add_rows_atomic<LPN>(args.C, N, col0, my_lds, acc, row);
   } else {
     // ------------------------------------------------------- residue groups
