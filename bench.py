@@ -1,26 +1,30 @@
 #!/usr/bin/env python3
 """Benchmark of the PowerSparse hot path on one MI355X.
 
-One step = one pass of the hot path over the synthetic benchmark graph (config
-C1 by default: Chung-Lu n = 1e6, gamma 2.1, mean degree 50, degree clip 5e4,
-values U(0,1); C2's SDDMM uses the same pattern): SpMM at N = 32, SpMM at
-N = 128, SDDMM at N = 128 and SDDMM at N = 32 (C2's two widths), each one
-fused launch covering every workset,
-enqueued back to back on one stream with the operands resident in HBM. The
-outputs are not cleared between calls, as in the reference harness
-(benchmarks/benchmark.cu:179-187).
+One step = one pass of the hot path over the synthetic benchmark graph, each
+operator one fused launch covering every workset, enqueued back to back on one
+stream with the operands resident in HBM. The default is config C3, the
+north-star graph (Chung-Lu n = 1.6e6, gamma 1.8, mean degree 165, degree clip
+1e5, ~264 M nonzeros, values U(0,1)): SpMM at N = 32, SpMM at N = 128 and
+SDDMM at N = 128, dense operands U(-1,1). `--config C1` runs the C1/C2 graph
+(n = 1e6, gamma 2.1, mean 50, clip 5e4): SpMM N = 32 and 128 with B ~ U(-1,1),
+SDDMM N = 128 and 32 with X, Y ~ N(0,1); `--config C4` the community graph
+(SpMM and SDDMM at N = 64, operands N(0,1)). The outputs are not cleared
+between calls, as in the reference harness (benchmarks/benchmark.cu:179-187).
 
 Prints one JSON line: value = total FLOP of the timed steps (2 * nnz * N per
 operator, benchmark.cu:189) / wall time between two events, in GFLOPS; the
 `roofline` object is for the dominant kernel (algorithmic bytes per launch /
 its mean launch time, HIP events on its stream); `cpu_baseline` is the OpenMP
 double-precision restatement of the reference's check path (the oracle) timed
-on this host over the same graph and operators. `roofline.traffic` is the
-bytes per launch the kernel's L2 exchanges with the memory fabric (Infinity
-Cache and HBM; calibrated FETCH_SIZE + WRITE_SIZE from the committed rocprofv3
-summary of the same workload), `traffic_GBps` that over the launch time.
+on this host over a bounded row sample of the same graph and operators.
+`roofline.traffic` is the bytes per launch the kernel's L2 exchanges with the
+memory fabric (Infinity Cache and HBM; calibrated FETCH_SIZE + WRITE_SIZE),
+taken from the committed rocprofv3 summary of the same workload when that
+summary was made from the current kernel sources (else null);
+`traffic_GBps` is that byte count over this run's launch time.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C1]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3]
 """
 import argparse
 import json
@@ -35,17 +39,11 @@ sys.path.insert(0, ROOT)
 
 METRIC = "SpMM/SDDMM GFLOPS + achieved HBM GB/s (% of roofline), N=32/128, 1 GPU"
 HBM_PEAK_GBPS = 8000.0
-WORKLOADS = {
-    "C1": "C1/C2 power-law graph (Chung-Lu n=1e6, gamma 2.1, mean 50, clip 5e4): "
-          "SpMM N=32 + SpMM N=128 + SDDMM N=128 + SDDMM N=32",
-    "C3": "C3 power-law graph (Chung-Lu n=1.6e6, gamma 1.8, mean 165, clip 1e5): "
-          "SpMM N=32 + SpMM N=128 + SDDMM N=128",
-    "C4": "C4 community graph (2048 x 1024 nodes, 2% intra, +8 inter, 5% empty, 5% singleton): "
-          "SpMM N=64 + SDDMM N=64",
+GRAPHS = {
+    "C1": "C1/C2 power-law graph (Chung-Lu n=1e6, gamma 2.1, target mean degree 50, clip 5e4)",
+    "C3": "C3 power-law graph (Chung-Lu n=1.6e6, gamma 1.8, target mean degree 165, clip 1e5)",
+    "C4": "C4 community graph (2048 x 1024 nodes, 2% intra, +8 inter, 5% empty, 5% singleton)",
 }
-OPS = {"C1": [("spmm", 32), ("spmm", 128), ("sddmm", 128), ("sddmm", 32)],
-       "C3": [("spmm", 32), ("spmm", 128), ("sddmm", 128)],
-       "C4": [("spmm", 64), ("sddmm", 64)]}
 
 
 def log(*a):
@@ -63,33 +61,66 @@ def measured_counters(config, op, n):
     """From the committed rocprofv3 summary of the same workload
     (profiles/traffic_<config>.json, made by `python -m powersparse_amd.perf
     summarize`): HBM bytes per launch of the operator kernel (FETCH_SIZE +
-    WRITE_SIZE), its L2 hit rate and VALU figures (None where absent), and the
-    summary's path."""
+    WRITE_SIZE), its L2 hit rate and VALU figures, the summary's path and a
+    note. All figures are None when the summary was made from other kernel
+    sources than the ones built here."""
+    from powersparse_amd.perf import sources_digest
+
     path = os.path.join(ROOT, "profiles", f"traffic_{config}.json")
     try:
         with open(path) as fh:
             summary = json.load(fh)
     except (OSError, ValueError):
-        return None, {}, None
+        return None, {}, None, "no profile summary"
+    rel = os.path.relpath(path, ROOT)
+    if summary.get("sources_digest") != sources_digest():
+        return None, {}, rel, "profile summary made from other kernel sources: not used"
     key = f"{op}_N{n}"
     traffic = summary.get("traffic", {}).get(key, {}).get("traffic_bytes")
     counters = summary.get("counters", {}).get(key, {})
-    return traffic, counters, os.path.relpath(path, ROOT)
+    return traffic, counters, rel, "from the profile summary of the same kernel sources"
 
 
-def cpu_baseline(csr, host_ops, reps=3):
-    """Times the oracle (OpenMP, double accumulation) on the same workload."""
+def host_description():
+    """nproc, the CPU model and the OpenMP thread count of this host."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": len(os.sched_getaffinity(0)), "cpu_model": model}
+
+
+def row_sample(csr, stride):
+    """Every stride-th row of the CSR: (row ids, row_ptr, col_ind, values)."""
+    rows = np.arange(0, csr.rows, stride, dtype=np.int64)
+    starts = csr.row_ptr[rows].astype(np.int64)
+    lens = csr.row_ptr[rows + 1].astype(np.int64) - starts
+    rp = np.zeros(rows.size + 1, np.int64)
+    np.cumsum(lens, out=rp[1:])
+    idx = np.repeat(starts - rp[:-1], lens) + np.arange(rp[-1], dtype=np.int64)
+    return rows.astype(np.int32), rp.astype(np.int32), csr.col_ind[idx], csr.values[idx]
+
+
+def cpu_baseline(csr, host_ops, stride, reps=3):
+    """Times the oracle (OpenMP, double accumulation) over every stride-th row
+    of the graph with the same operators and operands: (median seconds per
+    step, FLOP per sampled step, sampled nonzeros, threads)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     threads = oracle.max_threads()
-    rows_as_groups = np.arange(csr.rows, dtype=np.int32)
+    rows, rp, ci, sv = row_sample(csr, stride)
 
     def run():
         for op, n, a, b in host_ops:
             if op == "spmm":
-                oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, n, a)
-            else:
-                oracle.sddmm(rows_as_groups, csr.row_ptr, csr.col_ind, csr.values, n, a, b)
+                oracle.spmm(rp, ci, sv, n, a)
+            else:  # one group per sampled row, X rows addressed by row id
+                oracle.sddmm(rows, rp, ci, sv, n, a, b)
 
     run()  # warm-up
     times = []
@@ -97,7 +128,8 @@ def cpu_baseline(csr, host_ops, reps=3):
         t = time.perf_counter()
         run()
         times.append(time.perf_counter() - t)
-    return float(np.median(times)), threads
+    flop = sum(2.0 * ci.size * n for _, n, _, _ in host_ops)
+    return float(np.median(times)), flop, int(ci.size), threads
 
 
 def main():
@@ -105,7 +137,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="C1", choices=sorted(WORKLOADS))
+    ap.add_argument("--config", default="C3", choices=sorted(GRAPHS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -116,6 +148,7 @@ def main():
         return 2
 
     import powersparse_amd as ps
+    from powersparse_amd.perf import CONFIG_OPS, fill_operand
 
     ps.set_device(0)
     props = ps.device_props(0)
@@ -138,11 +171,11 @@ def main():
     ops = []
     seed = 100
     sizes = m.sddmm_output_sizes()
-    for op, n in OPS[args.config]:
+    for op, n in CONFIG_OPS[args.config]:
         seed += 1
         if op == "spmm":
             B = ps.DeviceBuffer(cols * n * 4)
-            ps.fill_random(B, cols * n, seed, -1.0, 1.0, stream=stream)
+            fill_operand(B, cols * n, seed, args.config, op, stream=stream)
             C = ps.DeviceBuffer(rows * n * 4)
             C.zero(stream)
             ops.append(dict(op=op, N=n, bufs=(B, C),
@@ -150,8 +183,8 @@ def main():
         else:
             X = ps.DeviceBuffer(rows * n * 4)
             Y = ps.DeviceBuffer(cols * n * 4)
-            ps.fill_random(X, rows * n, seed, 0.0, 1.0, normal=True, stream=stream)
-            ps.fill_random(Y, cols * n, seed + 50, 0.0, 1.0, normal=True, stream=stream)
+            fill_operand(X, rows * n, seed, args.config, op, stream=stream)
+            fill_operand(Y, cols * n, seed + 50, args.config, op, stream=stream)
             outs = [ps.DeviceBuffer(max(sz, 1) * 4) for sz in sizes]
             for o in outs:
                 o.zero(stream)
@@ -194,7 +227,8 @@ def main():
             f"{detail[-1]['alg_GBps']:.0f} GB/s ({100 * detail[-1]['roofline_frac']:.1f}% of 8 TB/s)")
     dom = max(detail, key=lambda d: d["ms"])
     kernel = "ps::spmm_kernel" if dom["op"] == "spmm" else "ps::sddmm_kernel"
-    traffic, counters, traffic_src = measured_counters(args.config, dom["op"], dom["N"])
+    traffic, counters, traffic_src, traffic_note = measured_counters(args.config, dom["op"],
+                                                                      dom["N"])
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -208,20 +242,30 @@ def main():
                 X, Y, _ = o["bufs"]
                 host_ops.append(("sddmm", o["N"], X.download(np.float32).reshape(rows, o["N"]),
                                  Y.download(np.float32).reshape(cols, o["N"])))
-        cpu_s, threads = cpu_baseline(csr, host_ops)
-        cpu = {"value": flop_step / cpu_s / 1e9, "unit": "GFLOPS", "cores": threads,
-               "kind": "port",
-               "sample": f"full {args.config} graph, one step ("
+        # about 64 M sampled nonzeros: every row of C1 and C4, every 4th of C3
+        stride = max(1, int(round(nnz / 64e6)))
+        cpu_s, cpu_flop, cpu_nnz, threads = cpu_baseline(csr, host_ops, stride)
+        host = host_description()
+        cpu = {"value": cpu_flop / cpu_s / 1e9, "unit": "GFLOPS", "cores": threads,
+               "kind": "port", "nproc": host["nproc"], "cpu_model": host["cpu_model"],
+               "omp_threads": threads,
+               "sample": f"every {stride} row(s) of the {args.config} graph ({cpu_nnz} of "
+                         f"{nnz} nonzeros), one step ("
                          + ", ".join(f"{o['op']} N={o['N']}" for o in ops)
                          + "), oracle/oracle.cpp OpenMP double accumulation, median of 3 "
-                           f"after 1 warm-up, {cpu_s:.2f} s per step"}
-        log(f"cpu baseline: {cpu['value']:.2f} GFLOPS on {threads} threads")
+                           f"after 1 warm-up, {cpu_s:.2f} s per sampled step"}
+        log(f"cpu baseline: {cpu['value']:.2f} GFLOPS on {threads} threads "
+            f"({host['nproc']} CPUs, {host['cpu_model']})")
 
     line = {
         "metric": METRIC, "value": value, "unit": "GFLOPS", "n_gpus": 1, "steps": K,
         "warmup": args.warmup, "ms_per_step": total_ms / K, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
-        "config": {"workload": WORKLOADS[args.config], "graph": args.config, "rows": rows,
+        "config": {"workload": f"{GRAPHS[args.config]}: {nnz} nonzeros, realized mean degree "
+                               f"{nnz / rows:.1f}; "
+                               + " + ".join(f"{o['op'].replace('spmm', 'SpMM').replace('sddmm', 'SDDMM')}"
+                                            f" N={o['N']}" for o in ops),
+                   "graph": args.config, "rows": rows,
                    "nnz": nnz, "worksets": S, "group_num": m.GroupNum(),
                    "preprocess_ms": preprocess_ms, "parallelism": "single GPU",
                    "device": (f"{props['name']} " if props["name"].strip() else "")
@@ -237,7 +281,7 @@ def main():
                      "l2_hit_pct": counters.get("l2_hit_pct"),
                      "valu_busy_pct": counters.get("valu_busy_pct"),
                      "valu_utilization_pct": counters.get("valu_utilization_pct"),
-                     "traffic_source": traffic_src},
+                     "traffic_source": traffic_src, "traffic_note": traffic_note},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -5,8 +5,9 @@
 // synchronises the device when there is more than one workset
 // (PowerSparse_SpMM/spmm_solution.cu:7-34, PowerSparse_SDDMM/sddmm_solution.cu:7-50).
 // Here every workset is covered by a single launch (ps_spmm_launch /
-// ps_sddmm_launch), enqueued on the first supplied stream; the synchronisation
-// contract is kept: asynchronous for one workset, device-synchronising for more.
+// ps_sddmm_launch), enqueued on the first supplied stream after the others are
+// joined into it; the synchronisation contract is kept: asynchronous for one
+// workset, device-synchronising for more.
 #include <stdexcept>
 #include <vector>
 
@@ -46,6 +47,33 @@ void CheckSddmmArgs(const PowerSparseMatrixGPU& m, int N, const float* lhs, cons
   if (!lhs || !rhs || !out) throw std::invalid_argument("Invalid SDDMM buffers or stream count");
 }
 
+// The reference runs workset s on streams[s] (spmm_solution.cu:18-26,
+// sddmm_solution.cu:24-26), so work a caller queued on streams[s] before the
+// call runs before that workset. The fused launch goes to streams[0]; every
+// other distinct stream is joined into it first, which keeps that ordering.
+// The events are released after the dispatcher's device synchronisation.
+class StreamJoin {
+ public:
+  StreamJoin(int count, const ps_stream_t* streams) {
+    for (int s = 1; s < count; ++s) {
+      if (streams[s] == streams[0]) continue;
+      ps_event_t e = nullptr;
+      ThrowOnError(ps_event_create(&e));
+      events_.push_back(e);
+      ThrowOnError(ps_event_record(e, streams[s]));
+      ThrowOnError(ps_stream_wait_event(streams[0], e));
+    }
+  }
+  ~StreamJoin() {
+    for (ps_event_t e : events_) ps_event_destroy(e);
+  }
+  StreamJoin(const StreamJoin&) = delete;
+  StreamJoin& operator=(const StreamJoin&) = delete;
+
+ private:
+  std::vector<ps_event_t> events_;
+};
+
 }  // namespace
 
 void SpMMAsync(const PowerSparseMatrixGPU& m, int N, const float* B, float* C,
@@ -63,8 +91,13 @@ void SpMM(const PowerSparseMatrixGPU& m, int N, const float* B, float* C, int st
   CheckSpmmArgs(m, N, B, C);
   if (stream_count != m.GroupTypeNum() || (stream_count > 1 && !streams))
     throw std::invalid_argument("Invalid SpMM buffers or stream count");
-  SpMMAsync(m, N, B, C, stream_count == 1 ? nullptr : streams[0]);
-  if (stream_count > 1) ThrowOnError(ps_device_synchronize());
+  if (stream_count == 1) {
+    SpMMAsync(m, N, B, C, nullptr);
+    return;
+  }
+  StreamJoin join(stream_count, streams);
+  SpMMAsync(m, N, B, C, streams[0]);
+  ThrowOnError(ps_device_synchronize());
 }
 
 void SDDMMAsync(const PowerSparseMatrixGPU& m, int N, const float* lhs, const float* rhs,
@@ -123,8 +156,13 @@ void SDDMM(const PowerSparseMatrixGPU& m, int N, const float* lhs, const float* 
   CheckSddmmArgs(m, N, lhs, rhs, out);
   if (stream_count != m.GroupTypeNum() || (stream_count > 1 && !streams))
     throw std::invalid_argument("Invalid SDDMM buffers or stream count");
-  SDDMMAsync(m, N, lhs, rhs, out, stream_count == 1 ? nullptr : streams[0]);
-  if (stream_count > 1) ThrowOnError(ps_device_synchronize());
+  if (stream_count == 1) {
+    SDDMMAsync(m, N, lhs, rhs, out, nullptr);
+    return;
+  }
+  StreamJoin join(stream_count, streams);
+  SDDMMAsync(m, N, lhs, rhs, out, streams[0]);
+  ThrowOnError(ps_device_synchronize());
 }
 
 }  // namespace PowerSparse

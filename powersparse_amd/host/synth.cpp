@@ -142,6 +142,31 @@ HostCsr BuildRows(int rows, int cols, uint64_t seed, Gen gen) {
   return csr;
 }
 
+// Open-addressing set of non-negative ints sized for `expected` members.
+class DistinctSet {
+ public:
+  explicit DistinctSet(int expected) {
+    size_t cap = 16;
+    while (cap < 2 * size_t(expected)) cap <<= 1;
+    slots_.assign(cap, -1);
+    mask_ = cap - 1;
+  }
+  // Adds v; false when it was already present.
+  bool Insert(int v) {
+    for (size_t h = (uint32_t(v) * 0x9E3779B1u) & mask_;; h = (h + 1) & mask_) {
+      if (slots_[h] == v) return false;
+      if (slots_[h] < 0) {
+        slots_[h] = v;
+        return true;
+      }
+    }
+  }
+
+ private:
+  std::vector<int> slots_;
+  size_t mask_;
+};
+
 void SortUnique(std::vector<int>& v) {
   std::sort(v.begin(), v.end());
   v.erase(std::unique(v.begin(), v.end()), v.end());
@@ -170,7 +195,7 @@ HostCsr SynthUniformDegree(int rows, int cols, int deg_lo, int deg_hi, float val
 
 HostCsr SynthChungLu(int n, double gamma, double mean_deg, double max_deg, float val_lo,
                      float val_hi, uint64_t seed) {
-  if (n <= 0 || gamma <= 1.0 || mean_deg <= 0 || max_deg <= 0)
+  if (n <= 0 || gamma <= 1.0 || mean_deg <= 0 || max_deg <= 0 || max_deg > std::max(1.0, n / 4.0))
     throw std::invalid_argument("SynthChungLu: bad parameters");
   const double alpha = 1.0 / (gamma - 1.0);
   std::vector<double> base(static_cast<size_t>(n));
@@ -191,10 +216,16 @@ HostCsr SynthChungLu(int n, double gamma, double mean_deg, double max_deg, float
   const AliasTable table(w);
   return BuildRows(n, n, seed, [&](int r, RowRng& rng, std::vector<int>& rc,
                                    std::vector<float>& rv) {
-    const int d = std::min(rng.Poisson(w[size_t(r)]), n);
+    // The row keeps its Poisson degree: endpoints that repeat one already
+    // drawn are drawn again, so hub columns do not thin out heavy rows.
+    const int d = std::min(rng.Poisson(w[size_t(r)]), n / 2);
+    DistinctSet seen(d);
     rc.reserve(size_t(d));
-    for (int j = 0; j < d; ++j) rc.push_back(table.Sample(rng));
-    SortUnique(rc);
+    while (int(rc.size()) < d) {
+      const int c = table.Sample(rng);
+      if (seen.Insert(c)) rc.push_back(c);
+    }
+    std::sort(rc.begin(), rc.end());
     for (size_t i = 0; i < rc.size(); ++i) rv.push_back(rng.UniformF(val_lo, val_hi));
   });
 }

@@ -26,8 +26,10 @@ HostCsr SynthUniformDegree(int rows, int cols, int deg_lo, int deg_hi, float val
 
 // Square Chung-Lu graph: weights w_i = c (i+1)^(-1/(gamma-1)), min(w_i, max_deg),
 // with c set so the clipped weights average mean_deg; out-degree of row i is
-// Poisson(w_i); endpoints drawn proportional to the same weights (alias table),
-// de-duplicated and sorted; values U(val_lo, val_hi).
+// Poisson(w_i) (capped at n / 2); endpoints drawn proportional to the same
+// weights (alias table), a repeat of a column already in the row drawn again,
+// so every row holds exactly its degree of distinct columns, sorted; values
+// U(val_lo, val_hi). max_deg must be at most n / 4.
 HostCsr SynthChungLu(int n, double gamma, double mean_deg, double max_deg, float val_lo,
                      float val_hi, uint64_t seed);
 

@@ -37,12 +37,57 @@ import re
 import sqlite3
 import sys
 
+import numpy as np
+
 CALIB_BYTES = 1 << 30
 
 # operators of each bench configuration, in launch order (kernel, N)
 CONFIG_OPS = {"C1": [("spmm", 32), ("spmm", 128), ("sddmm", 128), ("sddmm", 32)],
               "C3": [("spmm", 32), ("spmm", 128), ("sddmm", 128)],
               "C4": [("spmm", 64), ("sddmm", 64)]}
+
+# Dense operand distributions of each configuration: SpMM's B, SDDMM's X and Y,
+# as ("uniform", lo, hi) or ("normal", mean, std). C1: B ~ U(-1, 1); C2 (the
+# SDDMM of C1's pattern): X, Y ~ N(0, 1); C3: every dense operand U(-1, 1);
+# C4: every dense operand N(0, 1).
+OPERANDS = {"C1": {"spmm": ("uniform", -1.0, 1.0), "sddmm": ("normal", 0.0, 1.0)},
+            "C3": {"spmm": ("uniform", -1.0, 1.0), "sddmm": ("uniform", -1.0, 1.0)},
+            "C4": {"spmm": ("normal", 0.0, 1.0), "sddmm": ("normal", 0.0, 1.0)}}
+
+
+def fill_operand(buf, count, seed, config, op, stream=None):
+    """Fills a device operand of `config`'s operator `op` on the device."""
+    import powersparse_amd as ps
+
+    kind, a, b = OPERANDS[config][op]
+    ps.fill_random(buf, count, seed, a, b, normal=kind == "normal", stream=stream)
+
+
+def host_operand(rng, shape, config, op):
+    """A host (numpy float32) operand with `config`'s distribution for `op`."""
+    kind, a, b = OPERANDS[config][op]
+    if kind == "normal":
+        return (a + b * rng.standard_normal(shape)).astype(np.float32)
+    return rng.uniform(a, b, shape).astype(np.float32)
+
+
+def sources_digest(root=None):
+    """SHA-256 over the kernel sources and the C ABI header: ties a committed
+    profile summary to the kernels it measured."""
+    import glob
+    import hashlib
+    import os
+
+    root = root or os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    files = sorted(glob.glob(os.path.join(root, "powersparse_amd", "csrc", "*.hip")) +
+                   glob.glob(os.path.join(root, "powersparse_amd", "csrc", "*.hpp")) +
+                   [os.path.join(root, "include", "powersparse_hip.h")])
+    h = hashlib.sha256()
+    for f in files:
+        h.update(os.path.basename(f).encode())
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
 
 
 def short_name(name):
@@ -76,7 +121,7 @@ def workload(args):
     for op, n in CONFIG_OPS[args.config]:
         if op == "spmm":
             B = ps.DeviceBuffer(cols * n * 4)
-            ps.fill_random(B, cols * n, 11, -1.0, 1.0)
+            fill_operand(B, cols * n, 11, args.config, op)
             C = ps.DeviceBuffer(rows * n * 4)
             C.zero()
             for _ in range(1 + args.steps):
@@ -84,8 +129,8 @@ def workload(args):
         else:
             X = ps.DeviceBuffer(rows * n * 4)
             Y = ps.DeviceBuffer(cols * n * 4)
-            ps.fill_random(X, rows * n, 12, 0.0, 1.0, normal=True)
-            ps.fill_random(Y, cols * n, 13, 0.0, 1.0, normal=True)
+            fill_operand(X, rows * n, 12, args.config, op)
+            fill_operand(Y, cols * n, 13, args.config, op)
             outs = [ps.DeviceBuffer(max(s, 1) * 4) for s in sizes]
             for o in outs:
                 o.zero()
@@ -245,7 +290,9 @@ def summarize(args):
     lines = ["| kernel | grid (work-items) | dispatches | mean duration (us) |",
              "|---|---|---|---|"]
     trace = read_trace(args.trace)
-    result = {"config": args.config, "kernels": []}
+    # the kernel sources these counters belong to; bench.py drops the figures
+    # when its own sources differ
+    result = {"config": args.config, "sources_digest": sources_digest(), "kernels": []}
     for name, grid, calls, avg in trace:
         result["kernels"].append({"kernel": name, "grid": grid, "dispatches": calls,
                                   "mean_us": avg})

@@ -200,9 +200,12 @@ def test_full_size_sddmm_exact(cfg):
 def test_full_size_numerics(cfg, ops):
     """The bench's operators on the full-size benchmark graph against the
     oracle's double-precision results (tests/tolerance.py), with the bench's
-    input distributions: B ~ U(-1, 1), X and Y ~ N(0, 1). SDDMM is checked in
-    CSR order and in workset order (each stored nonzero's CSR position maps it
-    back; C4 runs its row-ordered execution copy)."""
+    input distributions (C1: B ~ U(-1, 1), X and Y ~ N(0, 1); C3: all U(-1, 1);
+    C4: all N(0, 1)). SDDMM is checked in CSR order and in workset order (each
+    stored nonzero's CSR position maps it back; C4 runs its row-ordered
+    execution copy). Prints per operator how many outputs pass only by the
+    condition-aware bound (`only_cond`)."""
+    from powersparse_amd.perf import host_operand
     setup()
     csr = ps.synth(cfg, seed=1)
     m = ps.PowerSparseMatrixGPU.from_csr(csr, csr_positions=True)
@@ -211,13 +214,13 @@ def test_full_size_numerics(cfg, ops):
     rows = np.arange(csr.rows, dtype=np.int32)
     for op, N in ops:
         if op == "spmm":
-            B = rng.uniform(-1, 1, (csr.cols, N)).astype(np.float32)
+            B = host_operand(rng, (csr.cols, N), cfg, op)
             C = run_spmm(m, N, B)
             E, M = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, N, B, with_mag=True)
             say("  ", tolerance.check(C, E, M, f"{cfg} SpMM N={N}"))
         else:
-            X = rng.standard_normal((csr.rows, N), dtype=np.float32)
-            Y = rng.standard_normal((csr.cols, N), dtype=np.float32)
+            X = host_operand(rng, (csr.rows, N), cfg, op)
+            Y = host_operand(rng, (csr.cols, N), cfg, op)
             dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
             out = ps.DeviceBuffer(csr.nnz * 4)
             ps.SDDMMToCSR(m, N, dX, dY, out)

@@ -90,7 +90,7 @@ def test_full_c4_bit_lists():
 
 @pytest.mark.parametrize("cfg", ["C1", "C3"])
 def test_full_size_bit_exact(cfg):
-    # the benchmark graphs at full size (C3: 171 M nonzeros, the north-star
+    # the benchmark graphs at full size (C3: ~264 M nonzeros, the north-star
     # graph): every workset array equal to the oracle's, values bitwise
     setup()
     csr = ps.synth(cfg, seed=1)

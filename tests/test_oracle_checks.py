@@ -83,3 +83,24 @@ def test_dense_input_draw_order():
     lhs, rhs = oracle.dense_input(1, 10, 7)
     both = oracle.dense_input(1, 17)
     np.testing.assert_array_equal(np.concatenate([lhs, rhs]), both)
+
+
+def test_tolerance_counts_outputs_passing_only_by_the_condition_bound():
+    """tolerance.check: an output beyond 1e-4 relative and 1e-5 absolute but
+    within 16 * 2^-24 * sum|a b| passes and is counted in `only_cond`; a planted
+    error beyond all three bounds fails."""
+    import pytest
+
+    import tolerance
+    # a cancelled sum: expected 1e-3, magnitudes summed 1e3, error 5e-5
+    exp = np.array([1.0, 1e-3, 2.0, 0.0])
+    mag = np.array([1.0, 1e3, 2.0, 1.0])
+    act = exp + np.array([5e-5, 5e-5, 1e-4, 5e-6])
+    r = tolerance.check(act, exp, mag, "counts")
+    # output 0 passes by 1e-4 relative (5e-5 <= 1e-4), output 1 only by the
+    # condition bound (5e-5 <= 16 * 2^-24 * 1e3 ~ 9.5e-4), output 2 relative
+    # (1e-4 <= 2e-4), output 3 absolute
+    assert r["n"] == 4 and r["only_cond"] == 1
+    assert r["only_cond_max_abs"] == pytest.approx(5e-5)
+    with pytest.raises(AssertionError, match="1 of 4 outputs out of tolerance"):
+        tolerance.check(exp + np.array([0, 2e-3, 0, 0]), exp, mag, "planted")

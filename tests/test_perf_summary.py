@@ -116,10 +116,18 @@ def test_bench_reads_counters(dbs, tmp_path, monkeypatch):
                "--write", dbs["write"], "--l2", dbs["l2"], "--valu", dbs["valu"],
                "--json", str(profiles / "traffic_C1.json")])
     monkeypatch.setattr(bench, "ROOT", str(tmp_path))
-    traffic, counters, src = bench.measured_counters("C1", "sddmm", 128)
+    traffic, counters, src, note = bench.measured_counters("C1", "sddmm", 128)
     assert traffic == 3000 * KIB * 0.5 + 30 * KIB
     assert counters["valu_busy_pct"] == 13.0 and src == os.path.join("profiles", "traffic_C1.json")
-    assert bench.measured_counters("C4", "spmm", 64) == (None, {}, None)
+    assert "same kernel sources" in note
+    assert bench.measured_counters("C4", "spmm", 64) == (None, {}, None, "no profile summary")
+    # a summary made from other kernel sources is not used
+    path = profiles / "traffic_C1.json"
+    summary = json.loads(path.read_text())
+    summary["sources_digest"] = "0" * 16
+    path.write_text(json.dumps(summary))
+    traffic, counters, src, note = bench.measured_counters("C1", "sddmm", 128)
+    assert traffic is None and counters == {} and "other kernel sources" in note
 
 
 def test_bench_one_gpu_only():
