@@ -1,166 +1,228 @@
-// MatrixMarket coordinate reader with the reference harness's semantics
-// (ParCIS/PowerSparse benchmarks/matrix_market.cpp:12-134):
-//   banner "%%MatrixMarket matrix coordinate {pattern|real|integer}
-//   {general|symmetric}"; '%' lines and blank lines skipped; 1-based indices
-//   checked against the declared size; pattern -> 1.0f, integer -> float,
-//   real -> strtod then float (finite, within FP32 range); symmetric input
-//   mirrors every off-diagonal entry; two passes over the file (count, then
-//   fill) so entries keep file order inside each row; 32-bit CSR limits.
-// Error texts match the reference's, since the CLI prints them.
+// MatrixMarket coordinate reader for the CSV harness.
+//
+// Design: the file is read into memory once (chunked reads, so a pipe works as
+// well as a regular file), scanned line by line in place into a list of
+// (row, col, value) entries in file order (a symmetric file's mirror entry
+// follows its source entry), and the list is turned into CSR by a stable
+// counting sort on the row: per-row counts, a prefix sum, then a scatter in
+// list order, which keeps file order inside every row.
+//
+// Accepted input and error texts are those of the reference harness's reader
+// (ParCIS/PowerSparse benchmarks/matrix_market.cpp:12-134), since the CLI
+// prints them and scripts match on them:
+//   first line "%%MatrixMarket matrix coordinate {pattern|real|integer}
+//   {general|symmetric}" (exactly five words); later lines that are blank or
+//   start with '%' after leading blanks are skipped; the size line holds three
+//   integers; each entry line holds a 1-based row and column (checked against
+//   the size before its value is parsed), then an integer (integer files) or a
+//   finite real within FP32 range, parsed as double and rounded (real files),
+//   or nothing (pattern files, value 1); no field may follow; the file must
+//   hold exactly the declared number of entry lines; sizes and the expanded
+//   entry count stay below INT32_MAX - 32.
 #include "matrix_market.h"
 
+#include <algorithm>
 #include <cerrno>
 #include <cmath>
 #include <cstdlib>
+#include <cstring>
 #include <fstream>
 #include <limits>
-#include <sstream>
 #include <stdexcept>
+#include <vector>
 
 namespace PowerSparse {
 namespace {
 
-constexpr long long kMaxIndex = std::numeric_limits<int>::max() - 32;
+constexpr long long kLimit = std::numeric_limits<int>::max() - 32;
 
-inline bool IsBlank(char c) {
+[[noreturn]] void Fail(const char* what) { throw std::runtime_error(what); }
+
+bool Blank(char c) {
   return c == ' ' || c == '\t' || c == '\r' || c == '\n' || c == '\f' || c == '\v';
 }
 
-// Next line that is neither blank nor a comment.
-bool NextRecord(std::istream& in, std::string& line) {
-  while (std::getline(in, line)) {
-    size_t i = 0;
-    while (i < line.size() && IsBlank(line[i])) ++i;
-    if (i < line.size() && line[i] != '%') return true;
-  }
-  if (in.bad()) throw std::runtime_error("Error reading MatrixMarket input");
-  return false;
+const char* SkipBlanks(const char* p) {
+  while (Blank(*p)) ++p;
+  return p;
 }
 
-class Fields {
+// The whole input, split into NUL-terminated lines in place.
+class LineBuffer {
  public:
-  explicit Fields(const std::string& line) : p_(line.c_str()) {}
-  long long Int() {
-    Skip();
-    errno = 0;
-    char* end = nullptr;
-    const long long v = std::strtoll(p_, &end, 10);
-    if (end == p_ || errno == ERANGE || (*end && !IsBlank(*end)))
-      throw std::runtime_error("Invalid integer in MatrixMarket input");
-    p_ = end;
-    return v;
+  explicit LineBuffer(const std::string& path) {
+    std::ifstream in(path, std::ios::binary);
+    if (!in) throw std::runtime_error("Cannot open matrix: " + path);
+    constexpr size_t kChunk = size_t(1) << 22;
+    for (;;) {
+      const size_t at = text_.size();
+      text_.resize(at + kChunk);
+      in.read(&text_[at], std::streamsize(kChunk));
+      text_.resize(at + size_t(in.gcount()));
+      if (in.bad()) Fail("Error reading MatrixMarket input");
+      if (!in) break;
+    }
+    text_.push_back('\0');  // the last line ends here if the file lacks a final newline
   }
-  float Real() {
-    Skip();
-    char* end = nullptr;
-    const double v = std::strtod(p_, &end);
-    if (end == p_ || (*end && !IsBlank(*end)) || !std::isfinite(v) ||
-        std::fabs(v) > double(std::numeric_limits<float>::max()))
-      throw std::runtime_error("Invalid finite FP32 value in MatrixMarket input");
-    p_ = end;
-    return float(v);
+
+  size_t Bytes() const { return text_.size() - 1; }
+
+  // The next line (without its newline), or nullptr at the end of the input.
+  char* Next() {
+    if (pos_ + 1 >= text_.size()) return nullptr;
+    char* line = &text_[pos_];
+    char* nl = static_cast<char*>(std::memchr(line, '\n', text_.size() - 1 - pos_));
+    if (nl) {
+      *nl = '\0';
+      pos_ = size_t(nl - text_.data()) + 1;
+    } else {
+      pos_ = text_.size() - 1;
+    }
+    return line;
   }
-  void End() {
-    Skip();
-    if (*p_) throw std::runtime_error("Unexpected extra fields in MatrixMarket record");
+
+  // The next line holding data: neither blank nor a '%' comment.
+  char* NextData() {
+    while (char* line = Next()) {
+      const char* p = SkipBlanks(line);
+      if (*p && *p != '%') return line;
+    }
+    return nullptr;
   }
 
  private:
-  void Skip() {
-    while (IsBlank(*p_)) ++p_;
-  }
-  const char* p_;
+  std::string text_;
+  size_t pos_ = 0;
 };
 
-struct Banner {
-  long long rows = 0, cols = 0, entries = 0;
-  std::string field, symmetry;
+// Reads one whitespace-delimited integer field.
+long long IntField(const char*& p) {
+  p = SkipBlanks(p);
+  char* end = nullptr;
+  errno = 0;
+  const long long v = std::strtoll(p, &end, 10);
+  if (end == p || errno == ERANGE || (*end && !Blank(*end)))
+    Fail("Invalid integer in MatrixMarket input");
+  p = end;
+  return v;
+}
+
+// Reads one real field that must be finite and representable as FP32.
+float RealField(const char*& p) {
+  p = SkipBlanks(p);
+  char* end = nullptr;
+  const double v = std::strtod(p, &end);
+  if (end == p || (*end && !Blank(*end)) || !std::isfinite(v) ||
+      std::fabs(v) > double(std::numeric_limits<float>::max()))
+    Fail("Invalid finite FP32 value in MatrixMarket input");
+  p = end;
+  return float(v);
+}
+
+void NoMoreFields(const char* p) {
+  if (*SkipBlanks(p)) Fail("Unexpected extra fields in MatrixMarket record");
+}
+
+enum class Field { kPattern, kReal, kInteger };
+
+struct Shape {
+  int rows = 0, cols = 0;
+  long long entries = 0;
+  Field field = Field::kPattern;
+  bool symmetric = false;
 };
 
-Banner ParseBanner(std::istream& in) {
-  std::string line;
-  if (!std::getline(in, line)) throw std::runtime_error("Empty MatrixMarket file");
-  std::istringstream words(line);
-  std::string magic, object, format, field, symmetry, extra;
-  const bool five = bool(words >> magic >> object >> format >> field >> symmetry);
-  if (!five || (words >> extra) || magic != "%%MatrixMarket" || object != "matrix" ||
-      format != "coordinate" || (field != "pattern" && field != "real" && field != "integer") ||
-      (symmetry != "general" && symmetry != "symmetric"))
-    throw std::runtime_error(
-        "Expected MatrixMarket coordinate pattern/real/integer general/symmetric");
-  if (!NextRecord(in, line)) throw std::runtime_error("Missing MatrixMarket dimensions");
-  Fields f(line);
-  Banner b;
-  b.rows = f.Int();
-  b.cols = f.Int();
-  b.entries = f.Int();
-  f.End();
-  b.field = field;
-  b.symmetry = symmetry;
-  if (b.rows <= 0 || b.cols <= 0 || b.entries <= 0 || b.rows > kMaxIndex || b.cols > kMaxIndex ||
-      b.entries > kMaxIndex || (symmetry == "symmetric" && b.rows != b.cols))
-    throw std::runtime_error("Matrix must be nonempty and fit 32-bit CSR indices");
-  return b;
+// Splits the banner line into whitespace-separated words.
+std::vector<std::string> Words(const char* p) {
+  std::vector<std::string> out;
+  for (p = SkipBlanks(p); *p; p = SkipBlanks(p)) {
+    const char* q = p;
+    while (*q && !Blank(*q)) ++q;
+    out.emplace_back(p, size_t(q - p));
+    p = q;
+  }
+  return out;
 }
 
-template <typename Sink>
-void ForEachEntry(std::istream& in, const Banner& b, Sink sink) {
-  std::string line;
-  const bool symmetric = b.symmetry == "symmetric";
-  for (long long e = 0; e < b.entries; ++e) {
-    if (!NextRecord(in, line)) throw std::runtime_error("Truncated MatrixMarket input");
-    Fields f(line);
-    const long long r = f.Int(), c = f.Int();
-    if (r < 1 || r > b.rows || c < 1 || c > b.cols)
-      throw std::runtime_error("MatrixMarket index outside the declared dimensions");
-    float v = 1.0f;
-    if (b.field == "integer") v = float(f.Int());
-    else if (b.field == "real") v = f.Real();
-    f.End();
-    sink(int(r - 1), int(c - 1), v);
-    if (symmetric && r != c) sink(int(c - 1), int(r - 1), v);
+Shape ReadShape(LineBuffer& lines) {
+  const char* banner = lines.Next();
+  if (!banner) Fail("Empty MatrixMarket file");
+  const std::vector<std::string> w = Words(banner);
+  Shape s;
+  bool ok = w.size() == 5 && w[0] == "%%MatrixMarket" && w[1] == "matrix" &&
+            w[2] == "coordinate";
+  if (ok) {
+    if (w[3] == "real") s.field = Field::kReal;
+    else if (w[3] == "integer") s.field = Field::kInteger;
+    else ok = w[3] == "pattern";
   }
-  if (NextRecord(in, line))
-    throw std::runtime_error("More entries than declared in MatrixMarket input");
+  if (ok) {
+    s.symmetric = w[4] == "symmetric";
+    ok = s.symmetric || w[4] == "general";
+  }
+  if (!ok) Fail("Expected MatrixMarket coordinate pattern/real/integer general/symmetric");
+  const char* p = lines.NextData();
+  if (!p) Fail("Missing MatrixMarket dimensions");
+  const long long rows = IntField(p), cols = IntField(p), entries = IntField(p);
+  NoMoreFields(p);
+  if (rows <= 0 || cols <= 0 || entries <= 0 || rows > kLimit || cols > kLimit ||
+      entries > kLimit || (s.symmetric && rows != cols))
+    Fail("Matrix must be nonempty and fit 32-bit CSR indices");
+  s.rows = int(rows);
+  s.cols = int(cols);
+  s.entries = entries;
+  return s;
 }
+
+struct Entry {
+  int row, col;
+  float value;
+};
 
 }  // namespace
 
 HostCsr ReadMatrixMarket(const std::string& path) {
-  std::ifstream in(path);
-  if (!in) throw std::runtime_error("Cannot open matrix: " + path);
-  const Banner b = ParseBanner(in);
-  HostCsr csr;
-  csr.rows = int(b.rows);
-  csr.cols = int(b.cols);
-  csr.row_ptr.assign(size_t(b.rows) + 1, 0);
-  long long count = 0;
-  ForEachEntry(in, b, [&](int r, int, float) {
-    if (++count > kMaxIndex) throw std::runtime_error("Expanded matrix exceeds 32-bit CSR capacity");
-    ++csr.row_ptr[size_t(r) + 1];
-  });
-  for (int r = 0; r < csr.rows; ++r) csr.row_ptr[size_t(r) + 1] += csr.row_ptr[size_t(r)];
-  csr.col_ind.resize(size_t(count));
-  csr.values.resize(size_t(count));
-  std::vector<int> next(csr.row_ptr.begin(), csr.row_ptr.end() - 1);
+  LineBuffer lines(path);
+  const Shape s = ReadShape(lines);
 
-  in.clear();
-  in.seekg(0);
-  if (!in) throw std::runtime_error("Matrix input must be a seekable regular file");
-  const Banner again = ParseBanner(in);
-  if (again.rows != b.rows || again.cols != b.cols || again.entries != b.entries ||
-      again.field != b.field || again.symmetry != b.symmetry)
-    throw std::runtime_error("Matrix header changed between reader passes");
-  ForEachEntry(in, b, [&](int r, int c, float v) {
-    const int at = next[size_t(r)]++;
-    if (at >= csr.row_ptr[size_t(r) + 1])
-      throw std::runtime_error("Matrix row counts changed between reader passes");
-    csr.col_ind[size_t(at)] = c;
-    csr.values[size_t(at)] = v;
-  });
-  for (int r = 0; r < csr.rows; ++r)
-    if (next[size_t(r)] != csr.row_ptr[size_t(r) + 1])
-      throw std::runtime_error("Matrix row counts changed between reader passes");
+  std::vector<Entry> list;
+  // an entry line takes at least 4 bytes ("1 1\n"): never reserve beyond the input
+  const long long fit = std::min<long long>(s.entries, (long long)(lines.Bytes() / 4 + 1));
+  list.reserve(size_t(s.symmetric ? 2 * fit : fit));
+  auto add = [&](int r, int c, float v) {
+    if ((long long)list.size() + 1 > kLimit) Fail("Expanded matrix exceeds 32-bit CSR capacity");
+    list.push_back({r, c, v});
+  };
+  for (long long e = 0; e < s.entries; ++e) {
+    const char* p = lines.NextData();
+    if (!p) Fail("Truncated MatrixMarket input");
+    const long long r = IntField(p), c = IntField(p);
+    if (r < 1 || r > s.rows || c < 1 || c > s.cols)
+      Fail("MatrixMarket index outside the declared dimensions");
+    float v = 1.0f;
+    if (s.field == Field::kInteger) v = float(IntField(p));
+    else if (s.field == Field::kReal) v = RealField(p);
+    NoMoreFields(p);
+    add(int(r) - 1, int(c) - 1, v);
+    if (s.symmetric && r != c) add(int(c) - 1, int(r) - 1, v);
+  }
+  if (lines.NextData()) Fail("More entries than declared in MatrixMarket input");
+
+  // stable counting sort of the list by row
+  HostCsr csr;
+  csr.rows = s.rows;
+  csr.cols = s.cols;
+  csr.row_ptr.assign(size_t(s.rows) + 1, 0);
+  for (const Entry& e : list) ++csr.row_ptr[size_t(e.row) + 1];
+  for (size_t r = 1; r < csr.row_ptr.size(); ++r) csr.row_ptr[r] += csr.row_ptr[r - 1];
+  csr.col_ind.resize(list.size());
+  csr.values.resize(list.size());
+  std::vector<int> fill(csr.row_ptr.begin(), csr.row_ptr.end() - 1);
+  for (const Entry& e : list) {
+    const size_t at = size_t(fill[size_t(e.row)]++);
+    csr.col_ind[at] = e.col;
+    csr.values[at] = e.value;
+  }
   return csr;
 }
 

@@ -102,8 +102,16 @@ def test_single_workset_async_default_stream():
     tolerance.check(C, E, M, "SpMM C0 default stream")
 
 
+def col_hash(col):
+    """A 20-bit multiplicative hash of each column id, as float64: a row's sum
+    of up to 2^33 of them stays an exact integer in float64 (< 2^53), so the
+    per-row sums compare exactly whatever the summation order."""
+    return ((col.astype(np.int64) * 2654435761) & 0xFFFFF).astype(np.float64)
+
+
 def per_row_checks(csr, m):
-    """Multiset of (row, col, value) preserved, via per-row counts and sums."""
+    """Multiset of (row, col, value) preserved, via per-row counts and sums
+    (column sums and column-hash sums are exact integers in float64)."""
     rows = csr.rows
     cnt = np.zeros(rows, np.int64)
     s_col = np.zeros(rows, np.float64)
@@ -118,7 +126,7 @@ def per_row_checks(csr, m):
         row_of = np.repeat(des, np.diff(offs))
         cnt += np.bincount(row_of, minlength=rows)
         s_col += np.bincount(row_of, weights=col.astype(np.float64), minlength=rows)
-        s_col2 += np.bincount(row_of, weights=col.astype(np.float64) ** 2, minlength=rows)
+        s_col2 += np.bincount(row_of, weights=col_hash(col), minlength=rows)
         s_val += np.bincount(row_of, weights=val.astype(np.float64), minlength=rows)
         if s > 0:
             g = col.reshape(-1, ps.GROUP_SIZE(s))
@@ -126,7 +134,7 @@ def per_row_checks(csr, m):
     row_of = np.repeat(np.arange(rows), np.diff(csr.row_ptr))
     np.testing.assert_array_equal(cnt, np.diff(csr.row_ptr))
     np.testing.assert_array_equal(s_col, np.bincount(row_of, weights=csr.col_ind.astype(np.float64), minlength=rows))
-    np.testing.assert_array_equal(s_col2, np.bincount(row_of, weights=csr.col_ind.astype(np.float64) ** 2, minlength=rows))
+    np.testing.assert_array_equal(s_col2, np.bincount(row_of, weights=col_hash(csr.col_ind), minlength=rows))
     np.testing.assert_allclose(s_val, np.bincount(row_of, weights=csr.values.astype(np.float64), minlength=rows), rtol=1e-12, atol=1e-9)
 
 

@@ -136,6 +136,20 @@ MTX_CASES = {
     "inf.mtx": "%%MatrixMarket matrix coordinate real general\n2 2 1\n1 1 1e40\n",
     "fields.mtx": "%%MatrixMarket matrix coordinate real general\n2 2 1\n1 1 1 9\n",
     "symrect.mtx": "%%MatrixMarket matrix coordinate real symmetric\n2 3 1\n1 1 1\n",
+    "no_final_newline.mtx": "%%MatrixMarket matrix coordinate real general\n2 3 3\n2 3 4\n"
+                            "1 1 -1\n2 1 0.5",
+    "empty.mtx": "",
+    "banner_only.mtx": "%%MatrixMarket matrix coordinate real general\n% no size line\n",
+    "blank_first_line.mtx": "\n%%MatrixMarket matrix coordinate real general\n1 1 1\n1 1 1\n",
+    "comments_between.mtx": "%%MatrixMarket matrix coordinate integer symmetric\n  % c\n3 3 3\n"
+                            "2 1 5\n\n   %x\n3 3 -2\n\t3 1 7 \n% tail\n",
+    "integer_real_value.mtx": "%%MatrixMarket matrix coordinate integer general\n2 2 1\n1 1 1.5\n",
+    "range_before_value.mtx": "%%MatrixMarket matrix coordinate real general\n2 2 1\n1 3 abc\n",
+    "six_words.mtx": "%%MatrixMarket matrix coordinate real general extra\n1 1 1\n1 1 1\n",
+    "zero_entries.mtx": "%%MatrixMarket matrix coordinate real general\n2 2 0\n",
+    "sym_pattern_dup.mtx": "%%MatrixMarket matrix coordinate pattern symmetric\n3 3 4\n3 1\n"
+                           "1 3\n2 2\n3 1\n",
+    "nul_in_line.mtx": "%%MatrixMarket matrix coordinate real general\n2 2 1\n1 1 2\x00 junk\n",
 }
 
 
