@@ -1,7 +1,9 @@
 """ctypes bindings of the two in-tree shared libraries.
 
-lib/libpowersparse_hip.so  HIP kernels + C ABI        (include/powersparse_hip.h)
-lib/libpowersparse.so      C++17 host API, C facade   (include/powersparse.h)
+lib/libpowersparse_hip.so     HIP kernels + C ABI        (include/powersparse_hip.h)
+lib/libpowersparse.so         C++17 host API, C facade   (include/powersparse.h)
+lib/libpowersparse_probes.so  measurement probes         (include/powersparse_probes.h),
+                              loaded only by the measurement tooling (probes())
 
 Loading fails loudly when the libraries are missing: there is no CPU fallback.
 """
@@ -12,6 +14,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(_HERE, "lib")
 HIP_LIB_PATH = os.path.join(LIB_DIR, "libpowersparse_hip.so")
 HOST_LIB_PATH = os.path.join(LIB_DIR, "libpowersparse.so")
+PROBES_LIB_PATH = os.path.join(LIB_DIR, "libpowersparse_probes.so")
 
 PS_OK = 0
 PS_ERR_INVALID = 1
@@ -86,13 +89,6 @@ HIP_API = [
     ("ps_memset_async", ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_size_t, c_void_p]),
     ("ps_fill_random_async", ctypes.c_int,
      [c_void_p, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float, ctypes.c_float, ctypes.c_int,
-      c_void_p]),
-    ("ps_copy_f32_async", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
-    ("ps_probe_xcc_ids_async", ctypes.c_int, [c_void_p, ctypes.c_int, c_void_p]),
-    ("ps_probe_row_update_async", ctypes.c_int,
-     [c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_int, ctypes.c_uint64, c_void_p]),
-    ("ps_probe_gather_async", ctypes.c_int,
-     [c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_longlong, ctypes.c_uint64, c_void_p,
       c_void_p]),
     ("ps_stream_create", ctypes.c_int, [ctypes.POINTER(c_void_p)]),
     ("ps_stream_destroy", ctypes.c_int, [c_void_p]),
@@ -176,6 +172,16 @@ HIP_API = [
       c_void_p, c_void_p, c_void_p, c_void_p]),
 ]
 
+PROBES_API = [
+    ("ps_copy_f32_async", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
+    ("ps_probe_xcc_ids_async", ctypes.c_int, [c_void_p, ctypes.c_int, c_void_p]),
+    ("ps_probe_row_update_async", ctypes.c_int,
+     [c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_int, ctypes.c_uint64, c_void_p]),
+    ("ps_probe_gather_async", ctypes.c_int,
+     [c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_longlong, ctypes.c_uint64, c_void_p,
+      c_void_p]),
+]
+
 HOST_API = [
     ("psx_last_error", ctypes.c_char_p, []),
     ("psx_matrix_create", ctypes.c_int,
@@ -236,6 +242,7 @@ HOST_API = [
 
 _hip = None
 _host = None
+_probes = None
 
 
 def _bind(lib, api):
@@ -269,3 +276,17 @@ def hip():
 
 def host():
     return libs()[1]
+
+
+def probes():
+    """Loads (once) and returns the measurement-probe library."""
+    global _probes
+    if _probes is None:
+        libs()
+        if not os.path.exists(PROBES_LIB_PATH):
+            raise ImportError(f"powersparse_amd: probe library {PROBES_LIB_PATH} is missing; "
+                              "build it with `make -C powersparse_amd`")
+        lib = ctypes.CDLL(PROBES_LIB_PATH)
+        _bind(lib, PROBES_API)
+        _probes = lib
+    return _probes

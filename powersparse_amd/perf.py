@@ -174,7 +174,7 @@ def ceiling(args):
     for row_floats in (32, 128):
         for mb in (2, 4, 8, 32, 128, 256, 512, 2048):
             rows = (mb << 20) // (4 * row_floats)
-            ms = timed(lambda: ps._hip_call(_native.hip().ps_probe_gather_async(
+            ms = timed(lambda: ps._hip_call(_native.probes().ps_probe_gather_async(
                 table.ptr, rows, row_floats, n, 9, out.ptr, st.ptr)))
             lines.append(f"| random {4 * row_floats}-byte row gathers | {mb} MB table | "
                          f"{ms:.3f} | {n * 4 * row_floats / ms / 1e6:.0f} |")
@@ -184,7 +184,7 @@ def ceiling(args):
              "float atomics, 8 lanes x 4 consecutive bytes", "float atomics, 32 lanes per row")
     nu = 1 << 22
     for mode, name in enumerate(modes):
-        ms = timed(lambda: ps._hip_call(_native.hip().ps_probe_row_update_async(
+        ms = timed(lambda: ps._hip_call(_native.probes().ps_probe_row_update_async(
             dst.ptr, 1 << 20, nu, mode, 5, st.ptr)))
         lines.append(f"| {name} | {ms:.3f} | {nu / ms / 1e3:.0f} |")
     print("\n".join(lines))

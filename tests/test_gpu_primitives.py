@@ -66,7 +66,7 @@ def test_row_update_probe(mode):
     say(f"row update probe mode={mode}")
     c = ps.DeviceBuffer(rows * 32 * 4)
     c.zero()
-    ps._hip_call(_native.hip().ps_probe_row_update_async(c.ptr, rows, n, mode, 3, None))
+    ps._hip_call(_native.probes().ps_probe_row_update_async(c.ptr, rows, n, mode, 3, None))
     got = c.download(np.float32, rows * 32).reshape(rows, 32)
     if mode == 0:
         touched = got.any(axis=1)
@@ -88,7 +88,7 @@ def test_workgroups_dealt_round_robin_over_xcds():
     n = 4096
     say("xcc ids of 4096 workgroups")
     out = ps.DeviceBuffer(n * 4)
-    ps._hip_call(_native.hip().ps_probe_xcc_ids_async(out.ptr, n, None))
+    ps._hip_call(_native.probes().ps_probe_xcc_ids_async(out.ptr, n, None))
     ids = out.download(np.int32, n)
     xcds = int(ids.max()) + 1
     assert xcds == 8 or ps.device_props(0)["cu_count"] != 256

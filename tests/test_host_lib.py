@@ -23,17 +23,19 @@ def declared(header):
 
 
 @pytest.mark.parametrize("header,libpath", [
-    ("powersparse_hip.h", _native.HIP_LIB_PATH), ("powersparse.h", _native.HOST_LIB_PATH)])
+    ("powersparse_hip.h", _native.HIP_LIB_PATH), ("powersparse.h", _native.HOST_LIB_PATH),
+    ("powersparse_probes.h", _native.PROBES_LIB_PATH)])
 def test_every_declared_symbol_is_exported(header, libpath):
     _native.libs()
+    _native.probes()
     names = declared(header)
-    assert len(names) > 10
+    assert len(names) >= 4
     out = subprocess.run(["nm", "-D", "--defined-only", libpath], capture_output=True, text=True,
                          check=True).stdout
     exported = set(line.split()[-1] for line in out.splitlines() if line.strip())
     missing = [n for n in names if n not in exported]
     assert not missing, missing
-    bound = {n for n, _, _ in (_native.HIP_API + _native.HOST_API)}
+    bound = {n for n, _, _ in (_native.HIP_API + _native.HOST_API + _native.PROBES_API)}
     assert not [n for n in names if n not in bound]
 
 
