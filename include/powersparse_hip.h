@@ -214,6 +214,17 @@ int ps_workset_to_csr(int workset_count, const long long* lengths, const int* co
 size_t ps_scan_workspace_bytes(size_t n);
 int ps_exclusive_scan_u32(const uint32_t* in, uint32_t* out, size_t n, void* workspace,
                           ps_stream_t stream);
+/* ps_exclusive_scan_u32 without a workspace and without any allocation: the
+ * tile sums live in a 256 KiB array the library keeps in each GPU's memory
+ * for the life of the process, so n is limited to what it holds
+ * (268,173,312 values; larger n returns PS_ERR_INVALID). Every call on one GPU uses
+ * that GPU's array: calls that overlap on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller. Launches kernels only
+ * (no hipMalloc, hipFree or memset), so it may be captured in a HIP graph.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops). */
+int ps_exclusive_scan_u32_noalloc(const uint32_t* in, uint32_t* out, size_t n,
+                                  ps_stream_t stream);
 
 /* Stable LSD radix sort of (key, value) pairs by key bits [begin_bit, end_bit);
  * vals and vals_alt both NULL sorts the keys alone. Bits above end_bit inside

@@ -129,6 +129,8 @@ HIP_API = [
     ("ps_scan_workspace_bytes", ctypes.c_size_t, [ctypes.c_size_t]),
     ("ps_exclusive_scan_u32", ctypes.c_int,
      [c_void_p, c_void_p, ctypes.c_size_t, c_void_p, c_void_p]),
+    ("ps_exclusive_scan_u32_noalloc", ctypes.c_int,
+     [c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
     ("ps_radix_workspace_bytes", ctypes.c_size_t, [ctypes.c_size_t]),
     ("ps_radix_sort_pairs_u64", ctypes.c_int,
      [c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,

@@ -12,6 +12,7 @@
 // eight ballots, so an element's offset is (earlier steps' count of its digit in
 // this wave) + (lower lanes with the same digit in this step). Wave prefixes and
 // the tile's global digit offsets from the scanned table complete the position.
+#include <mutex>
 #include <vector>
 
 #include "ps_common.hpp"
@@ -244,9 +245,58 @@ int radix_sort(K* keys, K* keys_alt, uint32_t* vals, uint32_t* vals_alt, size_t 
 }  // namespace
 }  // namespace ps
 
+// The tile sums of ps_exclusive_scan_u32_noalloc: every level of the scan
+// writes its sums here before reading them, so nothing needs clearing. Each
+// GPU holds its own copy for the life of the process; every call on a GPU
+// uses that GPU's copy, so calls that overlap on one GPU race.
+constexpr size_t kNoAllocScanBytes = size_t(256) << 10;  // 256 KiB: n up to 268,173,312
+static __device__ __align__(256) unsigned char scratch[kNoAllocScanBytes];
+
+namespace ps {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};  // device address of `scratch`, per device
+
+// The current device's copy of `scratch`, resolved once per device (with that
+// device current) by hipGetSymbolAddress: host code must never pass the
+// array's name itself to a kernel or a copy.
+int scratch_address(void** addr) {
+  int dev = 0;
+  PS_HIP(hipGetDevice(&dev));
+  PS_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "device index beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    PS_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    PS_CHECK_ARG(p != nullptr, "hipGetSymbolAddress returned no address for the scratch");
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return PS_OK;
+}
+
+}  // namespace
+}  // namespace ps
+
 extern "C" {
 
 size_t ps_scan_workspace_bytes(size_t n) { return ps::scan_ws(n) + 256; }
+
+int ps_exclusive_scan_u32_noalloc(const uint32_t* in, uint32_t* out, size_t n,
+                                  ps_stream_t stream) {
+  if (n == 0) return PS_OK;
+  PS_CHECK_ARG(ps::scan_ws(n) <= kNoAllocScanBytes,
+               "ps_exclusive_scan_u32_noalloc: n = " + std::to_string(n) +
+                   " needs more than the " + std::to_string(kNoAllocScanBytes) +
+                   "-byte static scratch; use ps_exclusive_scan_u32 with a workspace");
+  PS_CHECK_ARG(in && out, "ps_exclusive_scan_u32_noalloc: null buffer");
+  void* ws = nullptr;
+  const int rc = ps::scratch_address(&ws);
+  if (rc != PS_OK) return rc;
+  return ps::scan(in, out, n, reinterpret_cast<char*>(ws), ps::to_hip(stream));
+}
 
 int ps_exclusive_scan_u32(const uint32_t* in, uint32_t* out, size_t n, void* workspace,
                           ps_stream_t stream) {
