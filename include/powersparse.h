@@ -51,6 +51,7 @@ typedef struct psx_build_options {
   int signature_order;
   int csr_positions; /* nonzero: keep each nonzero's CSR position (psx_sddmm_csr) */
   int task_order;    /* PSX_TASK_AUTO, PSX_TASK_SIGNATURE or PSX_TASK_ROW */
+  int stored_order;  /* nonzero: no locality run order (PartitionPolicy::run_order off) */
 } psx_build_options;
 /* Group order the operators run in (same results; TaskOrder in matrix_utils.h):
  * the public signature order, or a row-ordered execution copy kept when it
@@ -67,6 +68,9 @@ int psx_matrix_signature_order(const psx_matrix* m, int* method);
  * locality scores compared (0 when not computed); outputs may be NULL. */
 int psx_matrix_task_order(const psx_matrix* m, int* order, double* score_signature,
                           double* score_row);
+/* Whether the operators run in the locality run order (RunOrderUsed()). No
+ * reference counterpart. */
+int psx_matrix_run_order(const psx_matrix* m, int* used);
 /* Replaces: ~PowerSparseMatrixGPU (matrix_utils.h:24). */
 int psx_matrix_destroy(psx_matrix* m);
 /* Replaces: MatrixRow/MatrixCol/MatrixNNZ/GroupTypeNum/GroupFineSize (matrix_utils.h:30-34);

@@ -188,6 +188,50 @@ int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int
                         const float* rhs, float* out_csr, int task_chunk,
                         ps_stream_t stream);
 
+/* ----------------------------------------------------------- run orders */
+/* Operators of ps_task_count / ps_task_order_build. */
+#define PS_OP_SPMM 0
+#define PS_OP_SDDMM 1
+
+/* Number of tasks of one fused launch of operator op at width N (for SpMM:
+ * of one 32-column slice; every slice runs the same tasks). Tasks are
+ * numbered in launch order: the worksets from the largest group size down to
+ * the residue (empty ones skipped); a block workset of G groups of GS
+ * nonzeros gives ceil(G * GS / T) tile tasks, the residue ceil(G0 / R) tasks
+ * of consecutive groups, with T = 256, R = 8 for SpMM (T = 128, R = 4 at
+ * N = 64) and T = 64, R = 8 for SDDMM. No reference counterpart. */
+int ps_task_count(int op, int N, int workset_count, const ps_workset* worksets,
+                  uint32_t* count);
+/* The locality run order of such a launch into order[count] (device memory,
+ * count = ps_task_count): the block tiles of all worksets sorted stably by
+ * their first column (the smallest, groups being stored columns ascending),
+ * then the residue tasks as stored, so that waves running at the same time
+ * gather from one narrow range of B / Y rows. Allocates temporary device
+ * memory and synchronises `stream`. No reference counterpart (the reference
+ * runs each workset's groups in stored order, one kernel per workset). */
+int ps_task_order_build(int op, int N, int workset_count, const ps_workset* worksets,
+                        uint32_t* order, uint32_t count, ps_stream_t stream);
+
+/* ps_spmm_launch, ps_sddmm_launch and ps_sddmm_csr_launch with the tasks run
+ * in a given order: task t of the launch runs task task_order[t] (a
+ * permutation of the ps_task_count tasks; task_count must equal that count),
+ * workgroups dealt in the hardware's round robin. Every task does the same
+ * work in any order: SDDMM results are bitwise those of the unordered launch,
+ * SpMM's differ only in the order of FP32 atomic additions. */
+int ps_spmm_launch_ordered(int workset_count, const ps_workset* worksets,
+                           const int* residue_offset, const uint8_t* residue_atomic, int rows,
+                           int cols, int N, const float* B, float* C, const uint32_t* task_order,
+                           uint32_t task_count, ps_stream_t stream);
+int ps_sddmm_launch_ordered(int workset_count, const ps_workset* worksets,
+                            const int* residue_offset, int rows, int cols, int N,
+                            const float* lhs, const float* rhs, float* const* out,
+                            const uint32_t* task_order, uint32_t task_count, ps_stream_t stream);
+int ps_sddmm_csr_launch_ordered(int workset_count, const ps_workset* worksets,
+                                const int* residue_offset, const int* const* csr_pos, int rows,
+                                int cols, int N, const float* lhs, const float* rhs,
+                                float* out_csr, const uint32_t* task_order, uint32_t task_count,
+                                ps_stream_t stream);
+
 /* SDDMM of worksets laid out in another group order than the public ones (a
  * task-order execution copy): the result of member j of group g of workset s
  * goes to out[s][out_base[s][g] + j], out[s] being the public workset-order

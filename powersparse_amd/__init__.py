@@ -360,7 +360,7 @@ class PowerSparseMatrixGPU:
 
     def __init__(self, row_num, col_num, nnz_num, row_ptr, col_ind, sp_data, cu_count=0,
                  timings=False, signature_order="auto", csr_positions=False,
-                 task_order="auto"):
+                 task_order="auto", run_order=True):
         row_ptr = np.ascontiguousarray(row_ptr, dtype=np.int32)
         col_ind = np.ascontiguousarray(col_ind, dtype=np.int32)
         sp_data = np.ascontiguousarray(sp_data, dtype=np.float32)
@@ -372,7 +372,8 @@ class PowerSparseMatrixGPU:
         if task_order not in self.TASK_ORDERS:
             raise ValueError(f"task_order must be one of {self.TASK_ORDERS}")
         opts = _native.BuildOptions(int(cu_count), self.ORDER_METHODS.index(signature_order),
-                                    int(bool(csr_positions)), self.TASK_ORDERS.index(task_order))
+                                    int(bool(csr_positions)), self.TASK_ORDERS.index(task_order),
+                                    int(not run_order))
         _host_call(_native.host().psx_matrix_create_ex(
             int(row_num), int(col_num), int(nnz_num),
             row_ptr.ctypes.data if row_ptr.size else None,
@@ -388,6 +389,9 @@ class PowerSparseMatrixGPU:
                                                         ctypes.byref(sig), ctypes.byref(row)))
         self.task_order = self.TASK_ORDERS[order.value]
         self.locality = {"signature": sig.value, "row": row.value}
+        used = ctypes.c_int()
+        _host_call(_native.host().psx_matrix_run_order(self._h, ctypes.byref(used)))
+        self.run_order = bool(used.value)
         self.timings = dict(zip(self.TIMING_KEYS, list(t))) if timings else None
         rows, cols, nnz, S, fine, L, cu = (ctypes.c_int() for _ in range(7))
         _host_call(_native.host().psx_matrix_info(
@@ -401,10 +405,10 @@ class PowerSparseMatrixGPU:
 
     @classmethod
     def from_csr(cls, csr, cu_count=0, timings=False, signature_order="auto",
-                 csr_positions=False, task_order="auto"):
+                 csr_positions=False, task_order="auto", run_order=True):
         return cls(csr.rows, csr.cols, csr.nnz, csr.row_ptr, csr.col_ind, csr.values,
                    cu_count=cu_count, timings=timings, signature_order=signature_order,
-                   csr_positions=csr_positions, task_order=task_order)
+                   csr_positions=csr_positions, task_order=task_order, run_order=run_order)
 
     def close(self):
         if self._h:

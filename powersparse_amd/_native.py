@@ -20,6 +20,8 @@ PS_OK = 0
 PS_ERR_INVALID = 1
 PS_ERR_RUNTIME = 2
 PS_MAX_WORKSETS = 32
+PS_OP_SPMM = 0
+PS_OP_SDDMM = 1
 
 c_int_p = ctypes.POINTER(ctypes.c_int)
 c_float_p = ctypes.POINTER(ctypes.c_float)
@@ -33,7 +35,8 @@ c_void_p = ctypes.c_void_p
 class BuildOptions(ctypes.Structure):
     """psx_build_options (include/powersparse.h)."""
     _fields_ = [("cu_count", ctypes.c_int), ("signature_order", ctypes.c_int),
-                ("csr_positions", ctypes.c_int), ("task_order", ctypes.c_int)]
+                ("csr_positions", ctypes.c_int), ("task_order", ctypes.c_int),
+                ("stored_order", ctypes.c_int)]
 
 
 class DeviceProps(ctypes.Structure):
@@ -118,6 +121,21 @@ HIP_API = [
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int,
       ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int,
       c_void_p]),
+    ("ps_task_count", ctypes.c_int,
+     [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(Workset), c_u32_p]),
+    ("ps_task_order_build", ctypes.c_int,
+     [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(Workset), c_void_p,
+      ctypes.c_uint32, c_void_p]),
+    ("ps_spmm_launch_ordered", ctypes.c_int,
+     [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
+      ctypes.c_int, c_void_p, c_void_p, c_void_p, ctypes.c_uint32, c_void_p]),
+    ("ps_sddmm_launch_ordered", ctypes.c_int,
+     [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+      c_void_p, c_void_p, ctypes.POINTER(c_void_p), c_void_p, ctypes.c_uint32, c_void_p]),
+    ("ps_sddmm_csr_launch_ordered", ctypes.c_int,
+     [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int,
+      ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_uint32,
+      c_void_p]),
     ("ps_pre_exec_positions", ctypes.c_int,
      [ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p]),
     ("ps_pre_locality_score", ctypes.c_int,
@@ -194,6 +212,7 @@ HOST_API = [
       ctypes.POINTER(BuildOptions), c_double_p, ctypes.POINTER(c_void_p)]),
     ("psx_matrix_signature_order", ctypes.c_int, [c_void_p, c_int_p]),
     ("psx_matrix_task_order", ctypes.c_int, [c_void_p, c_int_p, c_double_p, c_double_p]),
+    ("psx_matrix_run_order", ctypes.c_int, [c_void_p, c_int_p]),
     ("psx_matrix_destroy", ctypes.c_int, [c_void_p]),
     ("psx_matrix_info", ctypes.c_int,
      [c_void_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p]),

@@ -103,6 +103,26 @@ __device__ __forceinline__ uint32_t balanced_block(uint32_t b, uint32_t n, uint3
   return w * win + (b % kXcd) * chunk + (b / kXcd) % chunk;
 }
 
+// Task geometry of the fused operator launches, shared by the kernels, their
+// launchers and the run-order builder. A launch's tasks are numbered in launch
+// order: the worksets from the largest group size down to the residue (empty
+// worksets skipped); a block workset of G groups of GS nonzeros gives
+// ceil(G * GS / tile_nnz) tile tasks, the residue workset ceil(G0 /
+// residue_groups) tasks of consecutive groups.
+struct TaskShape {
+  int tile_nnz;
+  int residue_groups;
+};
+// SpMM: lanes per B-row slice (16 for N = 64, else 8), slots of lanes per wave,
+// 32 nonzeros per slot per tile, one residue group per slot.
+inline int spmm_lanes_per_row(int N) { return N == 64 ? 16 : 8; }
+inline TaskShape spmm_task_shape(int N) {
+  const int slots = kWave / spmm_lanes_per_row(N);
+  return {32 * slots, slots};
+}
+// SDDMM: 8 slots of 8 lanes, 8 nonzeros per slot per tile, one residue group per slot.
+inline TaskShape sddmm_task_shape() { return {64, 8}; }
+
 // log2 of a launch's task chunk (a power of two in [1, 256]; 0 means 1), or -1.
 inline int task_chunk_log2(int task_chunk) {
   if (task_chunk == 0) return 0;

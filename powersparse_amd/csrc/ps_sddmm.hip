@@ -21,6 +21,11 @@
 // outputs are stored, residue outputs are added atomically into out[0], the
 // output is in workset order.
 //
+// Run order: a launch may carry a permutation of its tasks (task_map); the
+// C++ API passes the locality order (block tiles by first column) for
+// signature-ordered worksets. A task's work, and so every output, is the same
+// in any order; residue tasks keep their 8 consecutive groups.
+//
 // Store modes (kMode): 0 = at the nonzero's own position (as above); 1 = per
 // nonzero map, out[s][map[s][p]]: CSR order (every out[s] is the one
 // CSR-order array, map = CSR positions, plain stores: each position is
@@ -52,6 +57,7 @@ struct SddmmArgs {
   const int* out_pos[PS_MAX_WORKSETS];  // mode 1: per-nonzero map; mode 2: per-group base
   int32_t residue_add;                  // modes 1-2: residue results added, not stored
   uint32_t chunk_log2;                  // workgroup -> XCD mapping (balanced_block)
+  const uint32_t* task_map;             // run order of the tasks, or null
 };
 
 // Transposing reduction over the 8 lanes of a slot: in p[j] each lane holds
@@ -115,9 +121,12 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
   __shared__ __attribute__((aligned(16))) int stage[kWavesPerBlock][8 * kStage];
   __shared__ float task_out[kWavesPerBlock][kTaskOut];  // residue results of a task
   const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, args.chunk_log2);
-  const uint32_t task =
-      __builtin_amdgcn_readfirstlane(blk * kWavesPerBlock + threadIdx.x / kWave);
+  uint32_t task = __builtin_amdgcn_readfirstlane(blk * kWavesPerBlock + threadIdx.x / kWave);
   if (task >= args.total_tasks) return;
+  if (args.task_map) {  // a permutation of [0, total_tasks)
+    task = __builtin_amdgcn_readfirstlane(args.task_map[task]);
+    if (task >= args.total_tasks) return;
+  }
   int i = 0;
   while (i + 1 < args.count && task >= args.task_begin[i + 1]) ++i;
   const ps_workset ws = args.ws[i];
@@ -299,9 +308,8 @@ void launch_kq(const SddmmArgs& a, bool buf, int mode, unsigned grid, hipStream_
 // (mode 2); residue results are added when residue_add (modes 1-2).
 int launch(int count, const int* order, const ps_workset* worksets, float* const* outs,
            int mode, const int* const* out_pos, int residue_add, const int* residue_offset,
-           int rows,
-           int cols, int N, const float* lhs, const float* rhs, int task_chunk,
-           hipStream_t stream) {
+           int rows, int cols, int N, const float* lhs, const float* rhs, int task_chunk,
+           const uint32_t* task_map, uint32_t task_map_len, hipStream_t stream) {
   PS_CHECK_ARG(N > 0 && N % 32 == 0 && N <= 512,
                "SDDMM requires N to be a multiple of 32 between 32 and 512");
   PS_CHECK_ARG(int64_t(rows) * N <= INT32_MAX && int64_t(cols) * N <= INT32_MAX,
@@ -342,10 +350,12 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
       // the kernel indexes a block workset's nonzeros (plus a 64-wide tile) in int
       PS_CHECK_ARG(uint64_t(w.group_num) * uint64_t(w.group_size) <= uint64_t(INT32_MAX) - 64,
                    "Block workset exceeds the 32-bit kernel indexing range");
-      t = (uint64_t(w.group_num) * w.group_size + 63) / 64;
+      const uint64_t T = uint64_t(sddmm_task_shape().tile_nnz);
+      t = (uint64_t(w.group_num) * w.group_size + T - 1) / T;
     } else {
       PS_CHECK_ARG(residue_offset, "Missing residue offsets");
-      t = (uint64_t(w.group_num) + 7) / 8;  // one slot per group
+      const uint64_t R = uint64_t(sddmm_task_shape().residue_groups);  // one slot per group
+      t = (uint64_t(w.group_num) + R - 1) / R;
     }
     a.ws[n] = w;
     if (s == 0) a.ws[n].group_size = 0;
@@ -360,6 +370,12 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
   a.count = n;
   a.task_begin[n] = uint32_t(tasks);
   a.total_tasks = uint32_t(tasks);
+  if (task_map) {
+    PS_CHECK_ARG(task_map_len == tasks,
+                 "SDDMM task order holds " + std::to_string(task_map_len) + " tasks, the launch " +
+                     std::to_string(tasks));
+    a.task_map = task_map;
+  }
   const unsigned grid = unsigned((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
   switch (N / 32) {
     case 1: launch_kq<1>(a, buf, mode, grid, stream); break;
@@ -402,7 +418,25 @@ int ps_sddmm_launch(int workset_count, const ps_workset* worksets, const int* re
     outs[q] = out[workset_count - 1 - q];
   }
   return ps::launch(workset_count, order, ordered, outs, 0, nullptr, 0, residue_offset, rows,
-                    cols, N, lhs, rhs, task_chunk, ps::to_hip(stream));
+                    cols, N, lhs, rhs, task_chunk, nullptr, 0, ps::to_hip(stream));
+}
+
+int ps_sddmm_launch_ordered(int workset_count, const ps_workset* worksets,
+                            const int* residue_offset, int rows, int cols, int N,
+                            const float* lhs, const float* rhs, float* const* out,
+                            const uint32_t* task_order, uint32_t task_count, ps_stream_t stream) {
+  PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets && out,
+               "Invalid SDDMM workset count");
+  int order[PS_MAX_WORKSETS];
+  ps_workset ordered[PS_MAX_WORKSETS];
+  float* outs[PS_MAX_WORKSETS];
+  for (int q = 0; q < workset_count; ++q) {
+    order[q] = workset_count - 1 - q;
+    ordered[q] = worksets[workset_count - 1 - q];
+    outs[q] = out[workset_count - 1 - q];
+  }
+  return ps::launch(workset_count, order, ordered, outs, 0, nullptr, 0, residue_offset, rows,
+                    cols, N, lhs, rhs, 1, task_order, task_count, ps::to_hip(stream));
 }
 
 int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
@@ -423,12 +457,13 @@ int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
     outs[q] = out[workset_count - 1 - q];
   }
   return ps::launch(workset_count, order, ordered, outs, 2, pos, 1, residue_offset, rows, cols,
-                    N, lhs, rhs, task_chunk, ps::to_hip(stream));
+                    N, lhs, rhs, task_chunk, nullptr, 0, ps::to_hip(stream));
 }
 
-int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
-                        const int* const* csr_pos, int rows, int cols, int N, const float* lhs,
-                        const float* rhs, float* out_csr, int task_chunk, ps_stream_t stream) {
+static int sddmm_csr(int workset_count, const ps_workset* worksets, const int* residue_offset,
+                     const int* const* csr_pos, int rows, int cols, int N, const float* lhs,
+                     const float* rhs, float* out_csr, int task_chunk, const uint32_t* task_order,
+                     uint32_t task_count, ps_stream_t stream) {
   PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets && csr_pos &&
                    out_csr,
                "Invalid SDDMM workset count");
@@ -443,7 +478,23 @@ int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int
     outs[q] = out_csr;
   }
   return ps::launch(workset_count, order, ordered, outs, 1, pos, 0, residue_offset, rows, cols,
-                    N, lhs, rhs, task_chunk, ps::to_hip(stream));
+                    N, lhs, rhs, task_chunk, task_order, task_count, ps::to_hip(stream));
+}
+
+int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int* residue_offset,
+                        const int* const* csr_pos, int rows, int cols, int N, const float* lhs,
+                        const float* rhs, float* out_csr, int task_chunk, ps_stream_t stream) {
+  return sddmm_csr(workset_count, worksets, residue_offset, csr_pos, rows, cols, N, lhs, rhs,
+                   out_csr, task_chunk, nullptr, 0, stream);
+}
+
+int ps_sddmm_csr_launch_ordered(int workset_count, const ps_workset* worksets,
+                                const int* residue_offset, const int* const* csr_pos, int rows,
+                                int cols, int N, const float* lhs, const float* rhs,
+                                float* out_csr, const uint32_t* task_order, uint32_t task_count,
+                                ps_stream_t stream) {
+  return sddmm_csr(workset_count, worksets, residue_offset, csr_pos, rows, cols, N, lhs, rhs,
+                   out_csr, 1, task_order, task_count, stream);
 }
 
 int ps_workset_to_csr(int workset_count, const long long* lengths, const int* const* csr_pos,
@@ -470,7 +521,7 @@ int ps_sddmm_workset_launch(int s, const ps_workset* workset, const int* residue
                             float* out, ps_stream_t stream) {
   PS_CHECK_ARG(s >= 0 && s < PS_MAX_WORKSETS && workset, "Invalid SDDMM workset");
   return ps::launch(1, &s, workset, &out, 0, nullptr, 0, residue_offset, rows, cols, N, lhs,
-                    rhs, 1, ps::to_hip(stream));
+                    rhs, 1, nullptr, 0, ps::to_hip(stream));
 }
 
 }  // extern "C"

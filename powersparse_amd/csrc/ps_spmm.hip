@@ -25,6 +25,11 @@
 // between. B is addressed through a buffer resource with 32-bit offsets when
 // cols * N * 4 fits in 32 bits.
 //
+// Run order: a launch may carry a permutation of one column slice's tasks
+// (task_map); task t of every slice then runs task_map[t]. The C++ API passes
+// the locality order (block tiles by first column) for signature-ordered
+// worksets. Each task's work is the same in any order.
+//
 // Workgroup -> task mapping: the hardware deals workgroups round-robin over
 // the 8 XCDs (workgroups b and b + 8 on the same one). With task_chunk > 1, windows of 8 * task_chunk consecutive
 // workgroups are re-dealt so that each XCD takes task_chunk consecutive ones:
@@ -65,6 +70,7 @@ struct SpmmArgs {
   const float* B;
   float* C;
   uint32_t chunk_log2;  // workgroup -> XCD mapping (balanced_block)
+  const uint32_t* task_map;  // run order of one column slice's tasks, or null
 };
 
 __device__ __forceinline__ void fma4(float4& acc, float a, const float4& b) {
@@ -118,6 +124,8 @@ __device__ __forceinline__ float group_sum(float v, int spg) {
 
 template <int LPN, bool kBuf>
 __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs args) {
+  // the tile of kPer * SL nonzeros and the SL residue groups of a task are
+  // spmm_task_shape(N)
   constexpr int SL = 64 / LPN;
   // per wave: the slots' staged pairs, and later the 256 floats of add_rows_atomic
   constexpr int kWaveWords = SL * kSlotWords > 256 ? SL * kSlotWords : 256;
@@ -129,7 +137,11 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs ar
   // slice-major: every task of column slice 0, then slice 1, ...
   const uint32_t per_slice = args.total_tasks / uint32_t(args.slices);
   const int slice = int(task / per_slice);
-  const uint32_t t = task - uint32_t(slice) * per_slice;
+  uint32_t t = task - uint32_t(slice) * per_slice;
+  if (args.task_map) {  // a permutation of [0, per_slice)
+    t = __builtin_amdgcn_readfirstlane(args.task_map[t]);
+    if (t >= per_slice) return;
+  }
   int i = 0;
   while (i + 1 < args.count && t >= args.task_begin[i + 1]) ++i;
   const ps_workset ws = args.ws[i];
@@ -270,7 +282,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs ar
 // each pass then gathers 128-byte rows from a cols x 32 working set, whose
 // hot rows an XCD's L2 holds four times more of than of full 512-byte rows
 // at N = 128 (measured on the C1 graph: 2.96 -> 2.53 ms at N = 128).
-int pick_lpn(int N) { return N == 64 ? 16 : 8; }
+int pick_lpn(int N) { return spmm_lanes_per_row(N); }
 
 template <int LPN>
 void launch_lpn(const SpmmArgs& a, bool buf, unsigned grid, hipStream_t stream) {
@@ -281,7 +293,7 @@ void launch_lpn(const SpmmArgs& a, bool buf, unsigned grid, hipStream_t stream) 
 
 int launch(int count, const int* order, const ps_workset* worksets, const int* residue_offset,
            const uint8_t* residue_atomic, int rows, int cols, int N, const float* B, float* C,
-           int task_chunk, hipStream_t stream) {
+           int task_chunk, const uint32_t* task_map, uint32_t task_map_len, hipStream_t stream) {
   PS_CHECK_ARG(N > 0 && N % 32 == 0, "SpMM requires N to be a positive multiple of 32");
   const int chunk_log2 = task_chunk_log2(task_chunk);
   PS_CHECK_ARG(chunk_log2 >= 0, "SpMM task_chunk must be 0 or a power of two up to 256");
@@ -290,7 +302,7 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
   PS_CHECK_ARG(B && C, "Invalid SpMM buffers");
   PS_CHECK_ARG(aligned16(B) && aligned16(C), "SpMM dense buffers must be 16-byte aligned");
   const int lpn = pick_lpn(N);
-  const int SL = 64 / lpn;
+  const TaskShape shape = spmm_task_shape(N);
   SpmmArgs a{};
   a.chunk_log2 = uint32_t(chunk_log2);
   a.N = N;
@@ -316,11 +328,11 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
                    "Block workset arrays must be 16-byte aligned");
       PS_CHECK_ARG(w.group_size >= 32 && (w.group_size & (w.group_size - 1)) == 0,
                    "Block workset group size must be a power of two >= 32");
-      const uint64_t T = uint64_t(kPer) * SL;
+      const uint64_t T = uint64_t(shape.tile_nnz);
       t = (uint64_t(w.group_num) * uint64_t(w.group_size) + T - 1) / T;
     } else {
       PS_CHECK_ARG(residue_offset && residue_atomic, "Missing residue offsets or flags");
-      t = (uint64_t(w.group_num) + SL - 1) / SL;
+      t = (uint64_t(w.group_num) + shape.residue_groups - 1) / shape.residue_groups;
     }
     a.ws[n] = w;
     if (s == 0) a.ws[n].group_size = 0;
@@ -331,6 +343,12 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
   if (n == 0) return PS_OK;
   a.count = n;
   a.task_begin[n] = uint32_t(tasks);
+  if (task_map) {
+    PS_CHECK_ARG(task_map_len == tasks,
+                 "SpMM task order holds " + std::to_string(task_map_len) + " tasks, the launch " +
+                     std::to_string(tasks));
+    a.task_map = task_map;
+  }
   tasks *= uint64_t(a.slices);
   PS_CHECK_ARG(tasks < (1ull << 31), "SpMM task count exceeds the launch range");
   a.total_tasks = uint32_t(tasks);
@@ -364,7 +382,23 @@ int ps_spmm_launch(int workset_count, const ps_workset* worksets, const int* res
     ordered[q] = worksets[workset_count - 1 - q];
   }
   return ps::launch(workset_count, order, ordered, residue_offset, residue_atomic, rows, cols,
-                    N, B, C, task_chunk, ps::to_hip(stream));
+                    N, B, C, task_chunk, nullptr, 0, ps::to_hip(stream));
+}
+
+int ps_spmm_launch_ordered(int workset_count, const ps_workset* worksets,
+                           const int* residue_offset, const uint8_t* residue_atomic, int rows,
+                           int cols, int N, const float* B, float* C, const uint32_t* task_order,
+                           uint32_t task_count, ps_stream_t stream) {
+  PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets,
+               "Invalid SpMM workset count");
+  int order[PS_MAX_WORKSETS];
+  ps_workset ordered[PS_MAX_WORKSETS];
+  for (int q = 0; q < workset_count; ++q) {
+    order[q] = workset_count - 1 - q;
+    ordered[q] = worksets[workset_count - 1 - q];
+  }
+  return ps::launch(workset_count, order, ordered, residue_offset, residue_atomic, rows, cols,
+                    N, B, C, 1, task_order, task_count, ps::to_hip(stream));
 }
 
 int ps_spmm_workset_launch(int s, const ps_workset* workset, const int* residue_offset,
@@ -372,7 +406,7 @@ int ps_spmm_workset_launch(int s, const ps_workset* workset, const int* residue_
                            const float* B, float* C, ps_stream_t stream) {
   PS_CHECK_ARG(s >= 0 && s < PS_MAX_WORKSETS && workset, "Invalid SpMM workset");
   return ps::launch(1, &s, workset, residue_offset, residue_atomic, rows, cols, N, B, C, 1,
-                    ps::to_hip(stream));
+                    nullptr, 0, ps::to_hip(stream));
 }
 
 }  // extern "C"

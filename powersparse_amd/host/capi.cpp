@@ -58,7 +58,7 @@ const char* psx_last_error(void) { return g_error.c_str(); }
 
 int psx_matrix_create(int rows, int cols, int nnz, const int* row_ptr, const int* col_ind,
                       const float* sp_data, int cu_count, double* timings_ms, psx_matrix** out) {
-  psx_build_options options{cu_count, PSX_ORDER_AUTO, 0, PSX_TASK_AUTO};
+  psx_build_options options{cu_count, PSX_ORDER_AUTO, 0, PSX_TASK_AUTO, 0};
   return psx_matrix_create_ex(rows, cols, nnz, row_ptr, col_ind, sp_data, &options, timings_ms,
                               out);
 }
@@ -75,6 +75,7 @@ int psx_matrix_create_ex(int rows, int cols, int nnz, const int* row_ptr, const 
       policy.signature_order = static_cast<PowerSparse::SignatureOrder>(options->signature_order);
       policy.csr_positions = options->csr_positions != 0;
       policy.task_order = static_cast<PowerSparse::TaskOrder>(options->task_order);
+      policy.run_order = options->stored_order == 0;
     }
     PowerSparse::PreprocessTimings t;
     auto* m = new PowerSparse::PowerSparseMatrixGPU(rows, cols, nnz, row_ptr, col_ind, sp_data,
@@ -102,6 +103,13 @@ int psx_matrix_task_order(const psx_matrix* m, int* order, double* score_signatu
     if (order) *order = int(m->m->TaskOrderUsed());
     if (score_signature) *score_signature = m->m->LocalityScore(PowerSparse::TaskOrder::kSignature);
     if (score_row) *score_row = m->m->LocalityScore(PowerSparse::TaskOrder::kRow);
+  });
+}
+
+int psx_matrix_run_order(const psx_matrix* m, int* used) {
+  return Guard([&] {
+    Need(m && m->m && used, "psx_matrix_run_order: null argument");
+    *used = m->m->RunOrderUsed() ? 1 : 0;
   });
 }
 

@@ -258,6 +258,7 @@ PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num
   _signature_order = policy.signature_order;
   _keep_csr_pos = policy.csr_positions;
   _task_order = policy.task_order;
+  _want_run_order = policy.run_order;
   if (_cu_count == 0) {
     int dev = 0;
     ThrowOnError(ps_get_device(&dev));
@@ -549,9 +550,35 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
       ReleaseExecution();
     }
   }
+  if (_task_order == TaskOrder::kSignature && _want_run_order) BuildRunOrders();
   ThrowOnError(ps_device_synchronize());
   clock.Mark(&PreprocessTimings::gather_ms);
   clock.Finish();
+}
+
+// The locality run order of each operator's fused launch over the public
+// (signature-ordered) worksets; see PartitionPolicy::run_order.
+void PowerSparseMatrixGPU::BuildRunOrders() {
+  const int S = _group_type_num;
+  std::vector<ps_workset> ws(static_cast<size_t>(S));
+  for (int s = 0; s < S; ++s) {
+    ws[size_t(s)].col_ind = _workset_col_ind[s];
+    ws[size_t(s)].sp_data = _workset_sp_data[s];
+    ws[size_t(s)].group_des = _group_des[s];
+    ws[size_t(s)].group_num = _group_num[s];
+    ws[size_t(s)].group_size = s == 0 ? 0 : GROUP_SIZE(s);
+    ws[size_t(s)].order = nullptr;
+  }
+  const int shapes[3][2] = {{PS_OP_SPMM, 32}, {PS_OP_SPMM, 64}, {PS_OP_SDDMM, 32}};
+  for (int k = 0; k < 3; ++k) {
+    const int op = shapes[k][0], n = shapes[k][1];
+    uint32_t count = 0;
+    ThrowOnError(ps_task_count(op, n, S, ws.data(), &count));
+    if (count == 0) continue;
+    ThrowOnError(ps_malloc(reinterpret_cast<void**>(&_run_order[k]), sizeof(uint32_t) * count));
+    _run_order_tasks[k] = count;
+    ThrowOnError(ps_task_order_build(op, n, S, ws.data(), _run_order[k], count, nullptr));
+  }
 }
 
 ExecutionLayout PowerSparseMatrixGPU::Execution() const {
@@ -572,6 +599,10 @@ ExecutionLayout PowerSparseMatrixGPU::Execution() const {
     e.residue_offset = _residue_offset;
     e.residue_atomic = _residue_atomic;
     e.csr_pos = _workset_csr_pos;
+    for (int k = 0; k < 3; ++k) {
+      e.run_order[k] = _run_order[k];
+      e.run_order_tasks[k] = _run_order_tasks[k];
+    }
   }
   return e;
 }
@@ -604,6 +635,11 @@ void PowerSparseMatrixGPU::ReleaseExecution() noexcept {
 
 void PowerSparseMatrixGPU::Release() noexcept {
   ReleaseExecution();
+  for (int k = 0; k < 3; ++k) {
+    ps_free(_run_order[k]);
+    _run_order[k] = nullptr;
+    _run_order_tasks[k] = 0;
+  }
   for (int s = 0; s < _group_type_num; ++s) {
     if (_workset_col_ind) ps_free(_workset_col_ind[s]);
     if (_workset_sp_data) ps_free(_workset_sp_data[s]);

@@ -69,7 +69,18 @@ struct ExecutionLayout {
   const int* const* out_base = nullptr;
   const int* const* csr_pos = nullptr;
   int task_chunk = kSignatureOrderTaskChunk;
+  // Run orders of the fused launches (null: tasks run as stored), indexed by
+  // RunOrderSlot(): SpMM at N != 64, SpMM at N = 64, SDDMM.
+  const uint32_t* run_order[3] = {nullptr, nullptr, nullptr};
+  uint32_t run_order_tasks[3] = {0, 0, 0};
 };
+
+// Which run order a launch of operator op (PS_OP_SPMM / PS_OP_SDDMM) at width
+// N uses: the three operator task shapes (SpMM tiles of 256 or, at N = 64, 128
+// nonzeros; SDDMM tiles of 64).
+inline int RunOrderSlot(int op, int N) {
+  return op == PS_OP_SDDMM ? 2 : (N == 64 ? 1 : 0);
+}
 
 // Partition settings. The reference hard-codes all of them except the CU
 // count, which it reads from the current device (utils/matrix_utils.cu:31-63);
@@ -81,6 +92,11 @@ struct PartitionPolicy {
   // (4 bytes per nonzero on the device): needed by SDDMMToCSR / WorksetToCSR.
   bool csr_positions = false;
   TaskOrder task_order = TaskOrder::kAuto;
+  // With the signature task order, run each operator's tasks in the locality
+  // order: block tiles of every workset sorted by their first column, the
+  // residue after them as stored (ps_task_order_build). Results are those of
+  // the stored order (SpMM: up to the order of FP32 atomic additions).
+  bool run_order = true;
 };
 
 // Wall-clock milliseconds of the preprocessing stages (host timer, the stream
@@ -132,6 +148,8 @@ class PowerSparseMatrixGPU {
   double LocalityScore(TaskOrder order) const {
     return order == TaskOrder::kRow ? _locality[1] : _locality[0];
   }
+  // Whether the operators run in the locality run order (see PartitionPolicy).
+  bool RunOrderUsed() const { return _run_order[0] != nullptr || _run_order[2] != nullptr; }
   // What the operators launch on.
   ExecutionLayout Execution() const;
 
@@ -140,6 +158,7 @@ class PowerSparseMatrixGPU {
              PreprocessTimings* timings);
   void Release() noexcept;
   void ReleaseExecution() noexcept;
+  void BuildRunOrders();
 
   int _matrix_row, _matrix_col, _matrix_nnz;
   int _group_type_num = 0, _group_fine_size = 16;
@@ -164,6 +183,10 @@ class PowerSparseMatrixGPU {
   int* _exec_residue_offset = nullptr;
   bool* _exec_residue_atomic = nullptr;
   bool* _residue_atomic = nullptr;
+  // locality run orders, by RunOrderSlot()
+  bool _want_run_order = true;
+  uint32_t* _run_order[3] = {nullptr, nullptr, nullptr};
+  uint32_t _run_order_tasks[3] = {0, 0, 0};
 };
 
 // The kernels use signed 32-bit dense element offsets (matrix_utils.h:71-76).

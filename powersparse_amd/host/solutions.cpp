@@ -81,9 +81,16 @@ void SpMMAsync(const PowerSparseMatrixGPU& m, int N, const float* B, float* C,
   CheckSpmmArgs(m, N, B, C);
   const ExecutionLayout e = m.Execution();
   const auto ws = Worksets(m, e);
-  ThrowOnError(ps_spmm_launch(m.GroupTypeNum(), ws.data(), e.residue_offset,
-                              reinterpret_cast<const uint8_t*>(e.residue_atomic), m.MatrixRow(),
-                              m.MatrixCol(), N, B, C, e.task_chunk, stream));
+  const int k = RunOrderSlot(PS_OP_SPMM, N);
+  if (e.run_order[k])
+    ThrowOnError(ps_spmm_launch_ordered(m.GroupTypeNum(), ws.data(), e.residue_offset,
+                                        reinterpret_cast<const uint8_t*>(e.residue_atomic),
+                                        m.MatrixRow(), m.MatrixCol(), N, B, C, e.run_order[k],
+                                        e.run_order_tasks[k], stream));
+  else
+    ThrowOnError(ps_spmm_launch(m.GroupTypeNum(), ws.data(), e.residue_offset,
+                                reinterpret_cast<const uint8_t*>(e.residue_atomic),
+                                m.MatrixRow(), m.MatrixCol(), N, B, C, e.task_chunk, stream));
 }
 
 void SpMM(const PowerSparseMatrixGPU& m, int N, const float* B, float* C, int stream_count,
@@ -111,6 +118,12 @@ void SDDMMAsync(const PowerSparseMatrixGPU& m, int N, const float* lhs, const fl
     ThrowOnError(ps_sddmm_scatter_launch(m.GroupTypeNum(), ws.data(), e.residue_offset,
                                          e.out_base, m.MatrixRow(), m.MatrixCol(), N, lhs, rhs,
                                          out, e.task_chunk, stream));
+  else if (e.run_order[RunOrderSlot(PS_OP_SDDMM, N)])
+    ThrowOnError(ps_sddmm_launch_ordered(m.GroupTypeNum(), ws.data(), e.residue_offset,
+                                         m.MatrixRow(), m.MatrixCol(), N, lhs, rhs, out,
+                                         e.run_order[RunOrderSlot(PS_OP_SDDMM, N)],
+                                         e.run_order_tasks[RunOrderSlot(PS_OP_SDDMM, N)],
+                                         stream));
   else
     ThrowOnError(ps_sddmm_launch(m.GroupTypeNum(), ws.data(), e.residue_offset, m.MatrixRow(),
                                  m.MatrixCol(), N, lhs, rhs, out, e.task_chunk, stream));
@@ -124,9 +137,16 @@ void SDDMMToCSR(const PowerSparseMatrixGPU& m, int N, const float* lhs, const fl
         "SDDMMToCSR needs a matrix built with PartitionPolicy::csr_positions");
   const ExecutionLayout e = m.Execution();
   const auto ws = Worksets(m, e);
-  ThrowOnError(ps_sddmm_csr_launch(m.GroupTypeNum(), ws.data(), e.residue_offset, e.csr_pos,
-                                   m.MatrixRow(), m.MatrixCol(), N, lhs, rhs, out_csr,
-                                   e.task_chunk, stream));
+  const int k = RunOrderSlot(PS_OP_SDDMM, N);
+  if (e.run_order[k])
+    ThrowOnError(ps_sddmm_csr_launch_ordered(m.GroupTypeNum(), ws.data(), e.residue_offset,
+                                             e.csr_pos, m.MatrixRow(), m.MatrixCol(), N, lhs,
+                                             rhs, out_csr, e.run_order[k], e.run_order_tasks[k],
+                                             stream));
+  else
+    ThrowOnError(ps_sddmm_csr_launch(m.GroupTypeNum(), ws.data(), e.residue_offset, e.csr_pos,
+                                     m.MatrixRow(), m.MatrixCol(), N, lhs, rhs, out_csr,
+                                     e.task_chunk, stream));
 }
 
 void WorksetToCSR(const PowerSparseMatrixGPU& m, const float* const* values, float* out_csr,
