@@ -52,6 +52,8 @@ typedef struct psx_build_options {
   int csr_positions; /* nonzero: keep each nonzero's CSR position (psx_sddmm_csr) */
   int task_order;    /* PSX_TASK_AUTO, PSX_TASK_SIGNATURE or PSX_TASK_ROW */
   int stored_order;  /* nonzero: no locality run order (PartitionPolicy::run_order off) */
+  int max_group_types; /* cap on the workset count S (0: none) */
+  int parity_spmm;   /* nonzero: SpMM on the public worksets (SpmmPartition::kParity) */
 } psx_build_options;
 /* Group order the operators run in (same results; TaskOrder in matrix_utils.h):
  * the public signature order, or a row-ordered execution copy kept when it
@@ -71,6 +73,10 @@ int psx_matrix_task_order(const psx_matrix* m, int* order, double* score_signatu
 /* Whether the operators run in the locality run order (RunOrderUsed()). No
  * reference counterpart. */
 int psx_matrix_run_order(const psx_matrix* m, int* used);
+/* The workset count of the partition SpMM runs on (the tuned one, or
+ * GroupTypeNum() when SpMM runs on the public worksets). No reference
+ * counterpart. */
+int psx_matrix_spmm_worksets(const psx_matrix* m, int* group_type_num);
 /* Replaces: ~PowerSparseMatrixGPU (matrix_utils.h:24). */
 int psx_matrix_destroy(psx_matrix* m);
 /* Replaces: MatrixRow/MatrixCol/MatrixNNZ/GroupTypeNum/GroupFineSize (matrix_utils.h:30-34);

@@ -108,6 +108,7 @@ std::vector<int> OrderByBitLists(std::vector<std::vector<int>>& bits) {
 // 0: bitmaps while groups x words stays below kBitmapLimit words, else lists;
 // 1: always the per-word sorts of the bitmaps; 2: always the bit lists.
 int g_order_mode = 0;
+int g_max_group_types = 0;  // cap on S, 0: none
 constexpr size_t kBitmapLimit = size_t(1) << 28;
 
 }  // namespace
@@ -134,6 +135,7 @@ int or_generate_sigbit(int cols, const int* col_nnz, int ffc, int* sigbit) {
 }
 
 void or_set_signature_order(int mode) { g_order_mode = mode; }
+void or_set_max_group_types(int cap) { g_max_group_types = cap; }
 
 void or_order_bit_lists(int groups, const int* begin, const int* bits, int* perm) {
   std::vector<std::vector<int>> b(static_cast<size_t>(groups));
@@ -164,7 +166,10 @@ or_worksets* or_preprocess(int rows, int cols, int nnz, const int* rp, const int
   w->rows = rows;
   w->cols = cols;
   w->nnz = nnz;
-  const int S = AnalyzeS(rows, rp, cu_count);  // matrix_utils.cu:499-506
+  int S = AnalyzeS(rows, rp, cu_count);  // matrix_utils.cu:499-506
+  // optional cap on S (an extension; with the cap at or above S this is the
+  // reference's partition)
+  if (g_max_group_types > 0 && S > g_max_group_types) S = g_max_group_types;
   w->S = S;
   const int fine = w->fine;
 

@@ -72,6 +72,10 @@ int or_generate_sigbit(int cols, const int* col_nnz, int ffc, int* sigbit);
  * groups x L/32 exceeds 2^28 words, then bit lists; 1 = always the per-word
  * sorts of the bitmaps; 2 = always the bit lists. Process-wide. */
 void or_set_signature_order(int mode);
+/* Caps the workset count S of later or_preprocess calls (0: no cap). An
+ * extension for the product's capped partitions; with the cap at or above S
+ * the partition is the reference's. */
+void or_set_max_group_types(int cap);
 
 /* The stable descending-signature order of `groups` groups given as sets of
  * signature bits: group g's bits are bits[begin[g] .. begin[g+1]) (any order,

@@ -44,6 +44,7 @@ def lib():
         L.or_has_signature.restype = ip
         L.or_has_signature.argtypes = [vp, ip]
         L.or_set_signature_order.argtypes = [ip]
+        L.or_set_max_group_types.argtypes = [ip]
         L.or_order_bit_lists.argtypes = [ip, vp, vp, vp]
         L.or_analyze_group_type_num.restype = ip
         L.or_analyze_group_type_num.argtypes = [ip, vp, ip]
@@ -126,22 +127,26 @@ class Worksets:
 ORDER_MODES = {"auto": 0, "bitmap_words": 1, "bit_lists": 2}
 
 
-def preprocess(rows, cols, row_ptr, col_ind, values, cu_count, signature_order="auto"):
+def preprocess(rows, cols, row_ptr, col_ind, values, cu_count, signature_order="auto",
+               max_group_types=0):
     """Runs the CPU restatement; raises ValueError with the reference message.
 
     signature_order: how groups are put in signature order (the same order
     either way): "auto", "bitmap_words" (per-word stable sorts of the bitmaps,
-    as the reference) or "bit_lists" (comparison of sorted bit lists)."""
+    as the reference) or "bit_lists" (comparison of sorted bit lists).
+    max_group_types: cap on the workset count S (0: none, the reference's rule)."""
     row_ptr, col_ind, values = _i32(row_ptr), _i32(col_ind), _f32(values)
     err = ctypes.create_string_buffer(256)
     nnz = int(col_ind.size)
     lib().or_set_signature_order(ORDER_MODES[signature_order])
+    lib().or_set_max_group_types(int(max_group_types))
     try:
         h = lib().or_preprocess(rows, cols, nnz, row_ptr.ctypes.data if row_ptr.size else None,
                                 col_ind.ctypes.data if col_ind.size else None,
                                 values.ctypes.data if values.size else None, cu_count, err, 256)
     finally:
         lib().or_set_signature_order(0)
+        lib().or_set_max_group_types(0)
     if not h:
         raise ValueError(err.value.decode())
     try:

@@ -360,7 +360,8 @@ class PowerSparseMatrixGPU:
 
     def __init__(self, row_num, col_num, nnz_num, row_ptr, col_ind, sp_data, cu_count=0,
                  timings=False, signature_order="auto", csr_positions=False,
-                 task_order="auto", run_order=True):
+                 task_order="auto", run_order=True, max_group_types=0,
+                 spmm_partition="tuned"):
         row_ptr = np.ascontiguousarray(row_ptr, dtype=np.int32)
         col_ind = np.ascontiguousarray(col_ind, dtype=np.int32)
         sp_data = np.ascontiguousarray(sp_data, dtype=np.float32)
@@ -371,9 +372,12 @@ class PowerSparseMatrixGPU:
             raise ValueError(f"signature_order must be one of {self.ORDER_METHODS}")
         if task_order not in self.TASK_ORDERS:
             raise ValueError(f"task_order must be one of {self.TASK_ORDERS}")
+        if spmm_partition not in ("tuned", "parity"):
+            raise ValueError("spmm_partition must be 'tuned' or 'parity'")
         opts = _native.BuildOptions(int(cu_count), self.ORDER_METHODS.index(signature_order),
                                     int(bool(csr_positions)), self.TASK_ORDERS.index(task_order),
-                                    int(not run_order))
+                                    int(not run_order), int(max_group_types),
+                                    int(spmm_partition == "parity"))
         _host_call(_native.host().psx_matrix_create_ex(
             int(row_num), int(col_num), int(nnz_num),
             row_ptr.ctypes.data if row_ptr.size else None,
@@ -392,6 +396,8 @@ class PowerSparseMatrixGPU:
         used = ctypes.c_int()
         _host_call(_native.host().psx_matrix_run_order(self._h, ctypes.byref(used)))
         self.run_order = bool(used.value)
+        _host_call(_native.host().psx_matrix_spmm_worksets(self._h, ctypes.byref(used)))
+        self.spmm_worksets = used.value  # workset count of the partition SpMM runs on
         self.timings = dict(zip(self.TIMING_KEYS, list(t))) if timings else None
         rows, cols, nnz, S, fine, L, cu = (ctypes.c_int() for _ in range(7))
         _host_call(_native.host().psx_matrix_info(
@@ -405,10 +411,12 @@ class PowerSparseMatrixGPU:
 
     @classmethod
     def from_csr(cls, csr, cu_count=0, timings=False, signature_order="auto",
-                 csr_positions=False, task_order="auto", run_order=True):
+                 csr_positions=False, task_order="auto", run_order=True, max_group_types=0,
+                 spmm_partition="tuned"):
         return cls(csr.rows, csr.cols, csr.nnz, csr.row_ptr, csr.col_ind, csr.values,
                    cu_count=cu_count, timings=timings, signature_order=signature_order,
-                   csr_positions=csr_positions, task_order=task_order, run_order=run_order)
+                   csr_positions=csr_positions, task_order=task_order, run_order=run_order,
+                   max_group_types=max_group_types, spmm_partition=spmm_partition)
 
     def close(self):
         if self._h:

@@ -36,7 +36,8 @@ class BuildOptions(ctypes.Structure):
     """psx_build_options (include/powersparse.h)."""
     _fields_ = [("cu_count", ctypes.c_int), ("signature_order", ctypes.c_int),
                 ("csr_positions", ctypes.c_int), ("task_order", ctypes.c_int),
-                ("stored_order", ctypes.c_int)]
+                ("stored_order", ctypes.c_int), ("max_group_types", ctypes.c_int),
+                ("parity_spmm", ctypes.c_int)]
 
 
 class DeviceProps(ctypes.Structure):
@@ -213,6 +214,7 @@ HOST_API = [
     ("psx_matrix_signature_order", ctypes.c_int, [c_void_p, c_int_p]),
     ("psx_matrix_task_order", ctypes.c_int, [c_void_p, c_int_p, c_double_p, c_double_p]),
     ("psx_matrix_run_order", ctypes.c_int, [c_void_p, c_int_p]),
+    ("psx_matrix_spmm_worksets", ctypes.c_int, [c_void_p, c_int_p]),
     ("psx_matrix_destroy", ctypes.c_int, [c_void_p]),
     ("psx_matrix_info", ctypes.c_int,
      [c_void_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p]),

@@ -58,7 +58,7 @@ const char* psx_last_error(void) { return g_error.c_str(); }
 
 int psx_matrix_create(int rows, int cols, int nnz, const int* row_ptr, const int* col_ind,
                       const float* sp_data, int cu_count, double* timings_ms, psx_matrix** out) {
-  psx_build_options options{cu_count, PSX_ORDER_AUTO, 0, PSX_TASK_AUTO, 0};
+  psx_build_options options{cu_count, PSX_ORDER_AUTO, 0, PSX_TASK_AUTO, 0, 0, 0};
   return psx_matrix_create_ex(rows, cols, nnz, row_ptr, col_ind, sp_data, &options, timings_ms,
                               out);
 }
@@ -76,6 +76,9 @@ int psx_matrix_create_ex(int rows, int cols, int nnz, const int* row_ptr, const 
       policy.csr_positions = options->csr_positions != 0;
       policy.task_order = static_cast<PowerSparse::TaskOrder>(options->task_order);
       policy.run_order = options->stored_order == 0;
+      policy.max_group_types = options->max_group_types;
+      policy.spmm_partition = options->parity_spmm ? PowerSparse::SpmmPartition::kParity
+                                                   : PowerSparse::SpmmPartition::kTuned;
     }
     PowerSparse::PreprocessTimings t;
     auto* m = new PowerSparse::PowerSparseMatrixGPU(rows, cols, nnz, row_ptr, col_ind, sp_data,
@@ -110,6 +113,13 @@ int psx_matrix_run_order(const psx_matrix* m, int* used) {
   return Guard([&] {
     Need(m && m->m && used, "psx_matrix_run_order: null argument");
     *used = m->m->RunOrderUsed() ? 1 : 0;
+  });
+}
+
+int psx_matrix_spmm_worksets(const psx_matrix* m, int* group_type_num) {
+  return Guard([&] {
+    Need(m && m->m && group_type_num, "psx_matrix_spmm_worksets: null argument");
+    *group_type_num = m->m->SpmmMatrix().GroupTypeNum();
   });
 }
 

@@ -254,11 +254,16 @@ PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num
     throw std::invalid_argument("PartitionPolicy::signature_order is not a SignatureOrder");
   if (int(policy.task_order) < 0 || int(policy.task_order) > 2)
     throw std::invalid_argument("PartitionPolicy::task_order is not a TaskOrder");
+  if (policy.max_group_types < 0)
+    throw std::invalid_argument("PartitionPolicy::max_group_types must be >= 0");
+  if (int(policy.spmm_partition) < 0 || int(policy.spmm_partition) > 1)
+    throw std::invalid_argument("PartitionPolicy::spmm_partition is not an SpmmPartition");
   _cu_count = policy.cu_count;
   _signature_order = policy.signature_order;
   _keep_csr_pos = policy.csr_positions;
   _task_order = policy.task_order;
   _want_run_order = policy.run_order;
+  _max_group_types = policy.max_group_types;
   if (_cu_count == 0) {
     int dev = 0;
     ThrowOnError(ps_get_device(&dev));
@@ -268,6 +273,17 @@ PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num
   }
   try {
     Build(row_ptr, col_ind, sp_data, timings);
+    if (policy.spmm_partition == SpmmPartition::kTuned && _task_order == TaskOrder::kSignature &&
+        _group_type_num > kTunedSpmmGroupTypes) {
+      PartitionPolicy tuned;
+      tuned.cu_count = _cu_count;
+      tuned.task_order = TaskOrder::kSignature;
+      tuned.run_order = false;
+      tuned.max_group_types = kTunedSpmmGroupTypes;
+      tuned.spmm_partition = SpmmPartition::kParity;
+      _spmm_tuned = new PowerSparseMatrixGPU(row_num, col_num, nnz_num, row_ptr, col_ind,
+                                             sp_data, tuned);
+    }
   } catch (...) {
     Release();
     throw;
@@ -291,7 +307,8 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
   // Worksets S (AnalyzeMatrix) and the column histogram.
   unsigned long long sums[32];
   ThrowOnError(ps_pre_degree_sums(d_rp.data(), rows, sums, st));
-  const int S = WorksetCount(sums, _cu_count);
+  int S = WorksetCount(sums, _cu_count);
+  if (_max_group_types > 0 && S > _max_group_types) S = _max_group_types;
   if (S > PS_MAX_WORKSETS) throw std::runtime_error("Too many worksets");
   _group_type_num = S;
   DeviceArray<int> d_cn(static_cast<size_t>(cols));
@@ -635,6 +652,8 @@ void PowerSparseMatrixGPU::ReleaseExecution() noexcept {
 
 void PowerSparseMatrixGPU::Release() noexcept {
   ReleaseExecution();
+  delete _spmm_tuned;
+  _spmm_tuned = nullptr;
   for (int k = 0; k < 3; ++k) {
     ps_free(_run_order[k]);
     _run_order[k] = nullptr;

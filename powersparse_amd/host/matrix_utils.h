@@ -47,6 +47,24 @@ constexpr int kBitmapMaxWords = 4;
 // (ps_pre_locality_score) and keeps the copy only if its score is below
 // kRowOrderGain times the signature order's.
 enum class TaskOrder { kAuto = 0, kSignature = 1, kRow = 2 };
+
+// Which partition SpMM runs on. kParity: the public worksets (the reference's
+// partition at the policy's CU count). kTuned: a second partition of the same
+// matrix kept for SpMM alone, the reference's algorithm with the number of
+// worksets capped at kTunedSpmmGroupTypes (largest groups of 64 nonzeros),
+// groups in signature order. Its groups are popularity bands of each row
+// (the row's nonzeros ranked by column count, cut into 64s), and the signature
+// sort lays bands with the same hot columns side by side, so the waves
+// running together gather from fewer B rows than with the hub rows' 8192-
+// nonzero groups (measured on MI355X, C3: SpMM N=32 2.03 -> 1.91 ms, N=128
+// 8.14 -> 7.66 ms; see the task-order notes). It is built when the parity
+// partition has more worksets than the cap and the operators run in signature
+// order; it costs a second preprocessing and about 8 bytes per nonzero. SpMM
+// results differ from the parity partition's only in the FP32 summation order:
+// rows with a single group of at most 32 nonzeros are stored, every other row
+// accumulates, exactly as with the public worksets.
+enum class SpmmPartition { kParity = 0, kTuned = 1 };
+constexpr int kTunedSpmmGroupTypes = 3;
 constexpr double kRowOrderGain = 0.85;
 // Workgroup -> XCD runs (ps_spmm_launch's task_chunk) per task order: in a
 // row-ordered copy neighbouring groups share columns, so runs of 64 tasks stay
@@ -97,6 +115,10 @@ struct PartitionPolicy {
   // residue after them as stored (ps_task_order_build). Results are those of
   // the stored order (SpMM: up to the order of FP32 atomic additions).
   bool run_order = true;
+  // Cap on the number of worksets S (0: none, the reference's rule alone);
+  // a capped partition is not the reference's when its rule gives more.
+  int max_group_types = 0;
+  SpmmPartition spmm_partition = SpmmPartition::kTuned;
 };
 
 // Wall-clock milliseconds of the preprocessing stages (host timer, the stream
@@ -150,6 +172,9 @@ class PowerSparseMatrixGPU {
   }
   // Whether the operators run in the locality run order (see PartitionPolicy).
   bool RunOrderUsed() const { return _run_order[0] != nullptr || _run_order[2] != nullptr; }
+  // The partition SpMM runs on: the tuned one (SpmmPartition::kTuned), or
+  // this matrix itself when none was built.
+  const PowerSparseMatrixGPU& SpmmMatrix() const { return _spmm_tuned ? *_spmm_tuned : *this; }
   // What the operators launch on.
   ExecutionLayout Execution() const;
 
@@ -187,6 +212,8 @@ class PowerSparseMatrixGPU {
   bool _want_run_order = true;
   uint32_t* _run_order[3] = {nullptr, nullptr, nullptr};
   uint32_t _run_order_tasks[3] = {0, 0, 0};
+  int _max_group_types = 0;
+  PowerSparseMatrixGPU* _spmm_tuned = nullptr;  // SpmmPartition::kTuned
 };
 
 // The kernels use signed 32-bit dense element offsets (matrix_utils.h:71-76).

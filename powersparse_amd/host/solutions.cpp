@@ -76,9 +76,11 @@ class StreamJoin {
 
 }  // namespace
 
-void SpMMAsync(const PowerSparseMatrixGPU& m, int N, const float* B, float* C,
+void SpMMAsync(const PowerSparseMatrixGPU& matrix, int N, const float* B, float* C,
                ps_stream_t stream) {
-  CheckSpmmArgs(m, N, B, C);
+  CheckSpmmArgs(matrix, N, B, C);
+  // the tuned partition when the matrix keeps one (SpmmPartition::kTuned)
+  const PowerSparseMatrixGPU& m = matrix.SpmmMatrix();
   const ExecutionLayout e = m.Execution();
   const auto ws = Worksets(m, e);
   const int k = RunOrderSlot(PS_OP_SPMM, N);

@@ -23,9 +23,14 @@ def worksets_count(degrees, cu_count):
     return s
 
 
-def preprocess(rows, cols, row_ptr, col_ind, values, cu_count, sigbit, sig_len, fine=16):
+def preprocess(rows, cols, row_ptr, col_ind, values, cu_count, sigbit, sig_len, fine=16,
+               max_group_types=0):
+    """max_group_types caps S (0: no cap); the split of each row below is the
+    same greedy cut from the largest allowed group size down."""
     degrees = [row_ptr[r + 1] - row_ptr[r] for r in range(rows)]
     S = worksets_count(degrees, cu_count)
+    if max_group_types:
+        S = min(S, max_group_types)
     col_nnz = [0] * cols
     for c in col_ind:
         col_nnz[c] += 1

@@ -206,6 +206,37 @@ def test_brute_force_agreement(seed, order):
         assert [bool(x) for x in w.residue_atomic] == b[0]["atomic"]
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_capped_partition_brute_force_agreement(seed):
+    """The oracle's optional cap on the workset count (the product's tuned SpMM
+    partition) against the brute force with the same cap; a cap at or above the
+    reference's S changes nothing."""
+    rng = np.random.default_rng(300 + seed)
+    rows = int(rng.integers(20, 60))
+    cols = int(rng.integers(30, 120))
+    rp, ci, va = random_graph(rng, rows, cols, int(rng.choice([140, 300])))
+    if ci.size == 0:
+        return
+    for cu in (1, 2):
+        full = oracle.preprocess(rows, cols, rp, ci, va, cu)
+        for cap in (1, 2, 3, full.S, full.S + 2):
+            w = oracle.preprocess(rows, cols, rp, ci, va, cu, max_group_types=cap)
+            S, b = brute.preprocess(rows, cols, rp.tolist(), ci.tolist(), va.tolist(), cu,
+                                    w.sigbit.tolist(), w.L, max_group_types=cap)
+            assert w.S == S == min(cap, full.S)
+            for s in range(S):
+                assert list(w.perm[s]) == b[s]["perm"], (cu, cap, s)
+                assert list(w.des[s]) == b[s]["des"]
+                assert list(w.col[s]) == b[s]["col"]
+                np.testing.assert_array_equal(w.val[s], np.array(b[s]["val"], np.float32))
+            assert list(w.residue_offset) == b[0]["offsets"]
+            assert [bool(x) for x in w.residue_atomic] == b[0]["atomic"]
+            if cap >= full.S:  # the reference's partition itself
+                for s in range(S):
+                    np.testing.assert_array_equal(w.col[s], full.col[s])
+                    np.testing.assert_array_equal(w.des[s], full.des[s])
+
+
 def bigint_order(bit_sets, length):
     """Descending order of the L-bit signature integers (bit b weighs
     2^(L-1-b)), ties in group order (sorted() is stable)."""
