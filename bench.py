@@ -274,10 +274,12 @@ def main():
         "roofline": {"bound": "hbm", "kernel": kernel, "op": f"{dom['op']} N={dom['N']}",
                      "achieved": dom["alg_GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": dom["roofline_frac"], "traffic": traffic,
-                     # measured L2 <-> fabric bytes per launch over the launch time
+                     # bytes the L2 exchanged with the memory fabric per launch
+                     # (Infinity Cache hits and HBM together), over this run's
+                     # launch time
+                     "traffic_scope": "L2 to memory fabric (Infinity Cache and HBM), "
+                                      "calibrated FETCH_SIZE + WRITE_SIZE",
                      "traffic_GBps": traffic / (dom["ms"] * 1e-3) / 1e9 if traffic else None,
-                     "traffic_frac": (traffic / (dom["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBPS
-                                      if traffic else None),
                      "l2_hit_pct": counters.get("l2_hit_pct"),
                      "valu_busy_pct": counters.get("valu_busy_pct"),
                      "valu_utilization_pct": counters.get("valu_utilization_pct"),
