@@ -222,11 +222,102 @@ class StageClock {
 
 }  // namespace
 
+// The partition-independent stages of the preprocessing. Members are declared
+// so that the signature-bit thread (sig_len) is joined before the vectors it
+// writes are destroyed.
+struct PowerSparseMatrixGPU::Prepared {
+  StageClock clock;
+  DeviceArray<int> row_ptr, col_ind;
+  DeviceArray<float> sp_data;
+  unsigned long long degree_sums[32] = {};
+  DeviceArray<int> col_nnz;  // device column counts
+  std::vector<int> col_nnz_host, sigbit;
+  int max_count = 0, count_bits = 0;
+  // Each row's nonzeros ranked by column count (descending, ties in CSR order).
+  DeviceArray<uint64_t> keys;
+  DeviceArray<uint32_t> vals;
+  DeviceArray<int> sigbit_device;
+  int signature_len = 0;
+  std::future<int> sig_len;
+
+  Prepared(int rows, int cols, int nnz, const int* host_row_ptr, const int* host_col_ind,
+           const float* host_sp_data, PreprocessTimings* timings)
+      : clock(timings), row_ptr(size_t(rows) + 1), col_ind(size_t(nnz)), sp_data(size_t(nnz)) {
+    ps_stream_t st = nullptr;
+    StagedUpload(row_ptr.data(), host_row_ptr, sizeof(int) * (size_t(rows) + 1));
+    StagedUpload(col_ind.data(), host_col_ind, sizeof(int) * size_t(nnz));
+    StagedUpload(sp_data.data(), host_sp_data, sizeof(float) * size_t(nnz));
+    clock.Mark(&PreprocessTimings::upload_ms);
+
+    // Degree sums (AnalyzeMatrix) and the column histogram.
+    ThrowOnError(ps_pre_degree_sums(row_ptr.data(), rows, degree_sums, st));
+    col_nnz.Allocate(size_t(cols));
+    col_nnz.Zero(st);
+    ThrowOnError(ps_pre_col_histogram(col_ind.data(), nnz, col_nnz.data(), st));
+    col_nnz_host.resize(size_t(cols));
+    col_nnz.Download(col_nnz_host.data(), size_t(cols));
+    max_count = *std::max_element(col_nnz_host.begin(), col_nnz_host.end());
+    clock.Mark(&PreprocessTimings::analyze_ms);
+
+    // Host: the column signature bits, on a thread of their own while this
+    // thread drives the device work that does not need them (joined by
+    // SignatureLen()).
+    sigbit.resize(size_t(cols));
+    sig_len = std::async(std::launch::async, [this, cols] {
+      return GenerateSigBitFFC(cols, col_nnz_host.data(), 2, sigbit.data());
+    });
+
+    count_bits = BitsFor(uint64_t(max_count));
+    keys.Allocate(size_t(nnz));
+    vals.Allocate(size_t(nnz));
+    ThrowOnError(ps_pre_rank_sort(row_ptr.data(), rows, col_ind.data(), nnz, col_nnz.data(),
+                                  max_count, count_bits, keys.data(), vals.data(), st));
+    clock.Mark(&PreprocessTimings::rank_ms);
+  }
+
+  // Joins the signature-bit thread on the first call (sigbit_ms: the time
+  // spent waiting for it) and uploads the bits.
+  int SignatureLen() {
+    if (sig_len.valid()) {
+      signature_len = sig_len.get();
+      clock.Mark(&PreprocessTimings::sigbit_ms);
+      sigbit_device.Allocate(sigbit.size());
+      sigbit_device.Upload(sigbit.data(), sigbit.size());
+    }
+    return signature_len;
+  }
+};
+
 PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num,
                                            const int* row_ptr, const int* col_ind,
                                            const float* sp_data)
     : PowerSparseMatrixGPU(row_num, col_num, nnz_num, row_ptr, col_ind, sp_data,
                            PartitionPolicy{}) {}
+
+PowerSparseMatrixGPU::PowerSparseMatrixGPU(Unbuilt, int row_num, int col_num, int nnz_num,
+                                           int cu_count, const PartitionPolicy& policy)
+    : _matrix_row(row_num), _matrix_col(col_num), _matrix_nnz(nnz_num) {
+  Configure(policy);
+  _cu_count = cu_count;
+}
+
+void PowerSparseMatrixGPU::Configure(const PartitionPolicy& policy) {
+  if (policy.cu_count < 0) throw std::invalid_argument("PartitionPolicy::cu_count must be >= 0");
+  if (int(policy.signature_order) < 0 || int(policy.signature_order) > 2)
+    throw std::invalid_argument("PartitionPolicy::signature_order is not a SignatureOrder");
+  if (int(policy.task_order) < 0 || int(policy.task_order) > 2)
+    throw std::invalid_argument("PartitionPolicy::task_order is not a TaskOrder");
+  if (policy.max_group_types < 0)
+    throw std::invalid_argument("PartitionPolicy::max_group_types must be >= 0");
+  if (int(policy.spmm_partition) < 0 || int(policy.spmm_partition) > 1)
+    throw std::invalid_argument("PartitionPolicy::spmm_partition is not an SpmmPartition");
+  _cu_count = policy.cu_count;
+  _signature_order = policy.signature_order;
+  _keep_csr_pos = policy.csr_positions;
+  _task_order = policy.task_order;
+  _want_run_order = policy.run_order;
+  _max_group_types = policy.max_group_types;
+}
 
 PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num,
                                            const int* row_ptr, const int* col_ind,
@@ -249,21 +340,7 @@ PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num
   for (int p = 0; p < nnz_num; ++p)
     bad |= (col_ind[p] < 0 || col_ind[p] >= col_num || !std::isfinite(sp_data[p]));
   if (bad) throw std::invalid_argument("Invalid CSR column index or sparse value");
-  if (policy.cu_count < 0) throw std::invalid_argument("PartitionPolicy::cu_count must be >= 0");
-  if (int(policy.signature_order) < 0 || int(policy.signature_order) > 2)
-    throw std::invalid_argument("PartitionPolicy::signature_order is not a SignatureOrder");
-  if (int(policy.task_order) < 0 || int(policy.task_order) > 2)
-    throw std::invalid_argument("PartitionPolicy::task_order is not a TaskOrder");
-  if (policy.max_group_types < 0)
-    throw std::invalid_argument("PartitionPolicy::max_group_types must be >= 0");
-  if (int(policy.spmm_partition) < 0 || int(policy.spmm_partition) > 1)
-    throw std::invalid_argument("PartitionPolicy::spmm_partition is not an SpmmPartition");
-  _cu_count = policy.cu_count;
-  _signature_order = policy.signature_order;
-  _keep_csr_pos = policy.csr_positions;
-  _task_order = policy.task_order;
-  _want_run_order = policy.run_order;
-  _max_group_types = policy.max_group_types;
+  Configure(policy);
   if (_cu_count == 0) {
     int dev = 0;
     ThrowOnError(ps_get_device(&dev));
@@ -272,8 +349,13 @@ PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num
     _cu_count = props.cu_count;
   }
   try {
-    Build(row_ptr, col_ind, sp_data, timings);
-    if (policy.spmm_partition == SpmmPartition::kTuned && _task_order == TaskOrder::kSignature &&
+    Prepared in(row_num, col_num, nnz_num, row_ptr, col_ind, sp_data, timings);
+    // A tuned SpMM partition may follow only in signature order (kAuto
+    // decides the order at the end of the build).
+    const bool may_tune =
+        policy.spmm_partition == SpmmPartition::kTuned && _task_order != TaskOrder::kRow;
+    Build(row_ptr, in, !may_tune);
+    if (may_tune && _task_order == TaskOrder::kSignature &&
         _group_type_num > kTunedSpmmGroupTypes) {
       PartitionPolicy tuned;
       tuned.cu_count = _cu_count;
@@ -281,58 +363,35 @@ PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num
       tuned.run_order = false;
       tuned.max_group_types = kTunedSpmmGroupTypes;
       tuned.spmm_partition = SpmmPartition::kParity;
-      _spmm_tuned = new PowerSparseMatrixGPU(row_num, col_num, nnz_num, row_ptr, col_ind,
-                                             sp_data, tuned);
+      _spmm_tuned =
+          new PowerSparseMatrixGPU(Unbuilt{}, row_num, col_num, nnz_num, _cu_count, tuned);
+      _spmm_tuned->Build(row_ptr, in, true);
     }
+    in.clock.Finish();
   } catch (...) {
     Release();
     throw;
   }
 }
 
-void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const float* sp_data,
-                                 PreprocessTimings* timings) {
-  const int rows = _matrix_row, cols = _matrix_col, nnz = _matrix_nnz;
+void PowerSparseMatrixGPU::Build(const int* row_ptr, Prepared& in, bool last_partition) {
+  const int rows = _matrix_row, nnz = _matrix_nnz;
   const int fine = _group_fine_size;
   ps_stream_t st = nullptr;
-  StageClock clock(timings);
+  StageClock& clock = in.clock;
+  DeviceArray<int>& d_rp = in.row_ptr;
+  DeviceArray<int>& d_ci = in.col_ind;
+  DeviceArray<float>& d_sv = in.sp_data;
+  DeviceArray<uint32_t>& vals = in.vals;
+  const int count_bits = in.count_bits;
 
-  DeviceArray<int> d_rp(static_cast<size_t>(rows) + 1), d_ci(static_cast<size_t>(nnz));
-  DeviceArray<float> d_sv(static_cast<size_t>(nnz));
-  StagedUpload(d_rp.data(), row_ptr, sizeof(int) * (size_t(rows) + 1));
-  StagedUpload(d_ci.data(), col_ind, sizeof(int) * size_t(nnz));
-  StagedUpload(d_sv.data(), sp_data, sizeof(float) * size_t(nnz));
-  clock.Mark(&PreprocessTimings::upload_ms);
-
-  // Worksets S (AnalyzeMatrix) and the column histogram.
-  unsigned long long sums[32];
-  ThrowOnError(ps_pre_degree_sums(d_rp.data(), rows, sums, st));
-  int S = WorksetCount(sums, _cu_count);
+  // Worksets S (AnalyzeMatrix), with the policy's cap.
+  int S = WorksetCount(in.degree_sums, _cu_count);
   if (_max_group_types > 0 && S > _max_group_types) S = _max_group_types;
   if (S > PS_MAX_WORKSETS) throw std::runtime_error("Too many worksets");
   _group_type_num = S;
-  DeviceArray<int> d_cn(static_cast<size_t>(cols));
-  d_cn.Zero(st);
-  ThrowOnError(ps_pre_col_histogram(d_ci.data(), nnz, d_cn.data(), st));
-  std::vector<int> col_nnz(static_cast<size_t>(cols));
-  d_cn.Download(col_nnz.data(), size_t(cols));
-  const int max_count = *std::max_element(col_nnz.begin(), col_nnz.end());
-  clock.Mark(&PreprocessTimings::analyze_ms);
-
-  // Host: the column signature bits, on a thread of their own while this
-  // thread drives the device work that does not need them (joined below).
-  std::vector<int> sigbit(static_cast<size_t>(cols));
-  std::future<int> sig_len = std::async(std::launch::async, [&sigbit, &col_nnz, cols] {
-    return GenerateSigBitFFC(cols, col_nnz.data(), 2, sigbit.data());
-  });
-
-  // Rank every row's nonzeros by column count (descending, ties in CSR order).
-  const int count_bits = BitsFor(uint64_t(max_count));
-  DeviceArray<uint64_t> keys(static_cast<size_t>(nnz));
-  DeviceArray<uint32_t> vals(static_cast<size_t>(nnz));
-  ThrowOnError(ps_pre_rank_sort(d_rp.data(), rows, d_ci.data(), nnz, d_cn.data(), max_count,
-                                count_bits, keys.data(), vals.data(), st));
-  clock.Mark(&PreprocessTimings::rank_ms);
+  // No tuned partition follows a partition of at most its cap of worksets.
+  if (S <= kTunedSpmmGroupTypes) last_partition = true;
 
   // Group counts per workset, on the host from row_ptr (the split the device
   // kernels make), so the device arrays are sized without waiting.
@@ -414,17 +473,15 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
     }
   }
 
-  // Join the host thread (sigbit_ms: the time spent waiting for it here).
-  _signature_len = sig_len.get();
-  clock.Mark(&PreprocessTimings::sigbit_ms);
+  _signature_len = in.SignatureLen();
 
   // Groups in signature order: perm[s][k] = initial group at position k.
   const int words = _signature_len / 32;
   if (_signature_order == SignatureOrder::kAuto)
     _signature_order = words <= kBitmapMaxWords ? SignatureOrder::kBitmapWords
                                                 : SignatureOrder::kBitLists;
-  DeviceArray<int> d_sigbit(static_cast<size_t>(cols));
-  d_sigbit.Upload(sigbit.data(), size_t(cols));
+  const int* d_sigbit = in.sigbit_device.data();
+  const uint64_t* keys = in.keys.data();
   std::vector<DeviceArray<uint32_t>> perm(static_cast<size_t>(S));
   std::vector<uint32_t*> perm_ptr(static_cast<size_t>(S), nullptr);
   for (int s = 0; s < S; ++s) {
@@ -437,11 +494,11 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
     size_t total = 0;
     for (int s = 0; s < S; ++s) total += size_t(_group_num[s]);
     DeviceArray<uint32_t> lists(static_cast<size_t>(nnz)), list_begin(total + 1);
-    ThrowOnError(ps_pre_signature_lists(d_rp.data(), rows, S, fine, keys.data(), count_bits,
-                                        vals.data(), nnz, d_ci.data(), d_sigbit.data(),
+    ThrowOnError(ps_pre_signature_lists(d_rp.data(), rows, S, fine, keys, count_bits,
+                                        vals.data(), nnz, d_ci.data(), d_sigbit,
                                         _signature_len, prefix.data(), _group_num, lists.data(),
                                         list_begin.data(), st));
-    keys.Reset();
+    if (last_partition) in.keys.Reset();
     clock.Mark(&PreprocessTimings::signature_ms);
     ThrowOnError(ps_pre_signature_order(lists.data(), list_begin.data(), S, _group_num,
                                         _signature_len, perm_ptr.data(), st));
@@ -454,10 +511,10 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
       sig[size_t(s)].Zero(st);
       sig_ptr[size_t(s)] = sig[size_t(s)].data();
     }
-    ThrowOnError(ps_pre_signatures(d_rp.data(), rows, S, fine, keys.data(), count_bits,
-                                   vals.data(), nnz, d_ci.data(), d_sigbit.data(), prefix.data(),
+    ThrowOnError(ps_pre_signatures(d_rp.data(), rows, S, fine, keys, count_bits,
+                                   vals.data(), nnz, d_ci.data(), d_sigbit, prefix.data(),
                                    _group_num, sig_ptr.data(), st));
-    keys.Reset();
+    if (last_partition) in.keys.Reset();
     clock.Mark(&PreprocessTimings::signature_ms);
     // Stable sort of each workset's groups by signature, descending, word 0
     // most significant: one stable pass per word from the last word to the
@@ -570,7 +627,6 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, const int* col_ind, const f
   if (_task_order == TaskOrder::kSignature && _want_run_order) BuildRunOrders();
   ThrowOnError(ps_device_synchronize());
   clock.Mark(&PreprocessTimings::gather_ms);
-  clock.Finish();
 }
 
 // The locality run order of each operator's fused launch over the public

@@ -59,10 +59,13 @@ enum class TaskOrder { kAuto = 0, kSignature = 1, kRow = 2 };
 // nonzero groups (measured on MI355X, C3: SpMM N=32 2.03 -> 1.91 ms, N=128
 // 8.14 -> 7.66 ms; see the task-order notes). It is built when the parity
 // partition has more worksets than the cap and the operators run in signature
-// order; it costs a second preprocessing and about 8 bytes per nonzero. SpMM
-// results differ from the parity partition's only in the FP32 summation order:
-// rows with a single group of at most 32 nonzeros are stored, every other row
-// accumulates, exactly as with the public worksets.
+// order; it shares the upload, column counts, signature bits and per-row
+// ranking with the public partition and adds its own grouping, signature sort
+// and gather (C3: 220 ms for both partitions, 332 when built separately) and
+// about 8 bytes per nonzero. SpMM results differ from the parity partition's
+// only in the FP32 summation order: rows with a single group of at most 32
+// nonzeros are stored, every other row accumulates, exactly as with the public
+// worksets.
 enum class SpmmPartition { kParity = 0, kTuned = 1 };
 constexpr int kTunedSpmmGroupTypes = 3;
 constexpr double kRowOrderGain = 0.85;
@@ -179,8 +182,18 @@ class PowerSparseMatrixGPU {
   ExecutionLayout Execution() const;
 
  private:
-  void Build(const int* row_ptr, const int* col_ind, const float* sp_data,
-             PreprocessTimings* timings);
+  // The stages that do not depend on the partition (upload, column counts,
+  // signature bits, per-row ranking), shared by the partitions of one matrix.
+  struct Prepared;
+  struct Unbuilt {};
+  // A partition of the same matrix whose Build() the caller runs.
+  PowerSparseMatrixGPU(Unbuilt, int row_num, int col_num, int nnz_num, int cu_count,
+                       const PartitionPolicy& policy);
+  void Configure(const PartitionPolicy& policy);
+  // The partition at this object's settings from the prepared stages; drops
+  // the per-row ranking from `in` once it is no longer needed when
+  // `last_partition` is set.
+  void Build(const int* row_ptr, Prepared& in, bool last_partition);
   void Release() noexcept;
   void ReleaseExecution() noexcept;
   void BuildRunOrders();
