@@ -111,6 +111,9 @@ int ps_stream_wait_event(ps_stream_t stream, ps_event_t event);
 /* ------------------------------------------------------------- operators */
 /* Maximum number of worksets (GroupTypeNum) one call accepts. */
 #define PS_MAX_WORKSETS 32
+/* task_chunk of the launchers: the run length of workgroups per XCD chosen
+ * from the launch size (see ps_spmm_launch). */
+#define PS_TASK_CHUNK_AUTO (-1)
 
 /* One workset as the kernels read it. For s == 0 (residue) group_size is 0 and
  * the group extents come from residue_offset; for s > 0 every group holds
@@ -136,12 +139,15 @@ typedef struct ps_workset {
  * (overwrite) their row. N must be a positive multiple of 32; cols * N and
  * rows * N must fit in int32. B, C and the block worksets' col_ind / sp_data
  * must be 16-byte aligned (as ps_malloc returns them).
- * task_chunk (0 or a power of two up to 256; 0 and 1 mean the hardware's
- * round robin of workgroups over the 8 XCDs): consecutive tasks dealt to one
- * XCD (one L2) in runs of task_chunk. Results do not depend on it. Worksets
- * whose neighbouring groups share columns (a row-ordered copy of a graph with
- * locality) run faster with long runs (64); in signature order 1 was as fast
- * or faster. No reference counterpart.
+ * task_chunk (PS_TASK_CHUNK_AUTO, 0, or a power of two up to 4096; 0 and 1
+ * mean the hardware's round robin of workgroups over the 8 XCDs): consecutive
+ * tasks dealt to one XCD (one L2) in runs of task_chunk workgroups. Results do
+ * not depend on it. Worksets whose neighbouring groups share columns (a
+ * row-ordered copy of a graph with locality) run faster with runs of 64.
+ * PS_TASK_CHUNK_AUTO picks the run from the launch size: the largest power of
+ * two that leaves 128 workgroups per run, at most 1024 (SpMM) or 256 (SDDMM);
+ * measured on signature-ordered worksets and locality run orders (C1, C3:
+ * 1-5% faster than the round robin). No reference counterpart.
  * Replaces: the launch loop of PowerSparse::SpMM (PowerSparse_SpMM/spmm_solution.cu:16-31)
  * and the kernels spmm_kernel_block (spmm_kernel_block.cu:60-162) and
  * spmm_kernel_residue (spmm_kernel_residue.cu:5-82). */
@@ -213,24 +219,24 @@ int ps_task_order_build(int op, int N, int workset_count, const ps_workset* work
                         uint32_t* order, uint32_t count, ps_stream_t stream);
 
 /* ps_spmm_launch, ps_sddmm_launch and ps_sddmm_csr_launch with the tasks run
- * in a given order: task t of the launch runs task task_order[t] (a
- * permutation of the ps_task_count tasks; task_count must equal that count),
- * workgroups dealt in the hardware's round robin. Every task does the same
- * work in any order: SDDMM results are bitwise those of the unordered launch,
- * SpMM's differ only in the order of FP32 atomic additions. */
+ * in a given order: the workgroups are dealt to the XCDs as task_chunk says,
+ * and task t of that sequence runs task task_order[t] (a permutation of the
+ * ps_task_count tasks; task_count must equal that count). Every task does the
+ * same work in any order: SDDMM results are bitwise those of the unordered
+ * launch, SpMM's differ only in the order of FP32 atomic additions. */
 int ps_spmm_launch_ordered(int workset_count, const ps_workset* worksets,
                            const int* residue_offset, const uint8_t* residue_atomic, int rows,
-                           int cols, int N, const float* B, float* C, const uint32_t* task_order,
-                           uint32_t task_count, ps_stream_t stream);
+                           int cols, int N, const float* B, float* C, int task_chunk,
+                           const uint32_t* task_order, uint32_t task_count, ps_stream_t stream);
 int ps_sddmm_launch_ordered(int workset_count, const ps_workset* worksets,
                             const int* residue_offset, int rows, int cols, int N,
-                            const float* lhs, const float* rhs, float* const* out,
+                            const float* lhs, const float* rhs, float* const* out, int task_chunk,
                             const uint32_t* task_order, uint32_t task_count, ps_stream_t stream);
 int ps_sddmm_csr_launch_ordered(int workset_count, const ps_workset* worksets,
                                 const int* residue_offset, const int* const* csr_pos, int rows,
                                 int cols, int N, const float* lhs, const float* rhs,
-                                float* out_csr, const uint32_t* task_order, uint32_t task_count,
-                                ps_stream_t stream);
+                                float* out_csr, int task_chunk, const uint32_t* task_order,
+                                uint32_t task_count, ps_stream_t stream);
 
 /* SDDMM of worksets laid out in another group order than the public ones (a
  * task-order execution copy): the result of member j of group g of workset s

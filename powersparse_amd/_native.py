@@ -20,6 +20,7 @@ PS_OK = 0
 PS_ERR_INVALID = 1
 PS_ERR_RUNTIME = 2
 PS_MAX_WORKSETS = 32
+PS_TASK_CHUNK_AUTO = -1
 PS_OP_SPMM = 0
 PS_OP_SDDMM = 1
 
@@ -129,14 +130,15 @@ HIP_API = [
       ctypes.c_uint32, c_void_p]),
     ("ps_spmm_launch_ordered", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
-      ctypes.c_int, c_void_p, c_void_p, c_void_p, ctypes.c_uint32, c_void_p]),
+      ctypes.c_int, c_void_p, c_void_p, ctypes.c_int, c_void_p, ctypes.c_uint32, c_void_p]),
     ("ps_sddmm_launch_ordered", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-      c_void_p, c_void_p, ctypes.POINTER(c_void_p), c_void_p, ctypes.c_uint32, c_void_p]),
+      c_void_p, c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int, c_void_p, ctypes.c_uint32,
+      c_void_p]),
     ("ps_sddmm_csr_launch_ordered", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, ctypes.POINTER(c_void_p), ctypes.c_int,
-      ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_uint32,
-      c_void_p]),
+      ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, c_void_p, ctypes.c_int, c_void_p,
+      ctypes.c_uint32, c_void_p]),
     ("ps_pre_exec_positions", ctypes.c_int,
      [ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p]),
     ("ps_pre_locality_score", ctypes.c_int,

@@ -123,12 +123,25 @@ inline TaskShape spmm_task_shape(int N) {
 // SDDMM: 8 slots of 8 lanes, 8 nonzeros per slot per tile, one residue group per slot.
 inline TaskShape sddmm_task_shape() { return {64, 8}; }
 
-// log2 of a launch's task chunk (a power of two in [1, 256]; 0 means 1), or -1.
-inline int task_chunk_log2(int task_chunk) {
-  if (task_chunk == 0) return 0;
-  for (int l = 0; l <= 8; ++l)
-    if (task_chunk == (1 << l)) return l;
-  return -1;
+// Whether task_chunk is one a launcher accepts: PS_TASK_CHUNK_AUTO, 0, or a
+// power of two up to 4096.
+inline bool task_chunk_valid(int task_chunk) {
+  return task_chunk == PS_TASK_CHUNK_AUTO || task_chunk == 0 ||
+         (task_chunk > 0 && task_chunk <= 4096 && (task_chunk & (task_chunk - 1)) == 0);
+}
+// log2 of the run length for a launch of `grid` workgroups. AUTO: the largest
+// power of two up to `auto_max` that leaves at least 128 workgroups per run,
+// i.e. 16 windows of 8 runs (the last, partial window keeps the hardware's
+// order, and within a window the XCDs take runs of unequal cost).
+inline int task_chunk_log2(int task_chunk, uint64_t grid, int auto_max) {
+  if (task_chunk == PS_TASK_CHUNK_AUTO) {
+    int l = 0;
+    while ((2 << l) <= auto_max && (uint64_t(2) << l) * 128 <= grid) ++l;
+    return l;
+  }
+  int l = 0;
+  while (task_chunk > (1 << l)) ++l;
+  return l;
 }
 
 // 128-bit loads at byte offsets from a base: through a buffer resource with

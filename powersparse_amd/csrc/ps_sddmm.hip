@@ -40,6 +40,10 @@ namespace {
 constexpr int kWavesPerBlock = 4;
 constexpr int kStage = 32;  // residue columns staged in LDS per slot
 constexpr int kTaskOut = 256;  // residue results of one task collected in LDS
+// Longest XCD run of PS_TASK_CHUNK_AUTO (measured in the locality run order,
+// C3 N = 128: runs of 256 workgroups 1.4% faster than the round robin, 1024
+// slower on C1).
+constexpr int kAutoChunkMax = 256;
 static_assert(kTaskOut >= 8 * kStage, "a task's slots each collect up to kStage results");
 
 struct SddmmArgs {
@@ -316,10 +320,9 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
                "Dense dimensions exceed the 32-bit kernel indexing range");
   PS_CHECK_ARG(lhs && rhs && outs, "Invalid SDDMM buffers");
   PS_CHECK_ARG(aligned16(lhs) && aligned16(rhs), "SDDMM dense buffers must be 16-byte aligned");
-  const int chunk_log2 = task_chunk_log2(task_chunk);
-  PS_CHECK_ARG(chunk_log2 >= 0, "SDDMM task_chunk must be 0 or a power of two up to 256");
+  PS_CHECK_ARG(task_chunk_valid(task_chunk),
+               "SDDMM task_chunk must be PS_TASK_CHUNK_AUTO, 0 or a power of two up to 4096");
   SddmmArgs a{};
-  a.chunk_log2 = uint32_t(chunk_log2);
   a.residue_add = residue_add;
   a.N = N;
   a.lhs = lhs;
@@ -377,6 +380,7 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
     a.task_map = task_map;
   }
   const unsigned grid = unsigned((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
+  a.chunk_log2 = uint32_t(task_chunk_log2(task_chunk, grid, kAutoChunkMax));
   switch (N / 32) {
     case 1: launch_kq<1>(a, buf, mode, grid, stream); break;
     case 2: launch_kq<2>(a, buf, mode, grid, stream); break;
@@ -423,7 +427,7 @@ int ps_sddmm_launch(int workset_count, const ps_workset* worksets, const int* re
 
 int ps_sddmm_launch_ordered(int workset_count, const ps_workset* worksets,
                             const int* residue_offset, int rows, int cols, int N,
-                            const float* lhs, const float* rhs, float* const* out,
+                            const float* lhs, const float* rhs, float* const* out, int task_chunk,
                             const uint32_t* task_order, uint32_t task_count, ps_stream_t stream) {
   PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets && out,
                "Invalid SDDMM workset count");
@@ -436,7 +440,8 @@ int ps_sddmm_launch_ordered(int workset_count, const ps_workset* worksets,
     outs[q] = out[workset_count - 1 - q];
   }
   return ps::launch(workset_count, order, ordered, outs, 0, nullptr, 0, residue_offset, rows,
-                    cols, N, lhs, rhs, 1, task_order, task_count, ps::to_hip(stream));
+                    cols, N, lhs, rhs, task_chunk, task_order, task_count,
+                    ps::to_hip(stream));
 }
 
 int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
@@ -491,10 +496,10 @@ int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int
 int ps_sddmm_csr_launch_ordered(int workset_count, const ps_workset* worksets,
                                 const int* residue_offset, const int* const* csr_pos, int rows,
                                 int cols, int N, const float* lhs, const float* rhs,
-                                float* out_csr, const uint32_t* task_order, uint32_t task_count,
-                                ps_stream_t stream) {
+                                float* out_csr, int task_chunk, const uint32_t* task_order,
+                                uint32_t task_count, ps_stream_t stream) {
   return sddmm_csr(workset_count, worksets, residue_offset, csr_pos, rows, cols, N, lhs, rhs,
-                   out_csr, 1, task_order, task_count, stream);
+                   out_csr, task_chunk, task_order, task_count, stream);
 }
 
 int ps_workset_to_csr(int workset_count, const long long* lengths, const int* const* csr_pos,

@@ -50,6 +50,10 @@ namespace {
 constexpr int kWavesPerBlock = 4;
 constexpr int kPer = 32;          // nonzeros per slot per block tile
 constexpr int kSlotWords = 2 * kPer + 4;  // LDS words per slot (pairs + pad)
+// Longest XCD run of PS_TASK_CHUNK_AUTO (measured on the tuned SpMM partition,
+// C3: runs of 1024 workgroups 3-4% faster than the round robin, 4096 no better;
+// C1: 256 best, 4-5% faster).
+constexpr int kAutoChunkMax = 1024;
 // B loads in flight per lane. 8 keeps the kernel at 62 VGPRs, i.e. 8 waves per
 // SIMD; 16 needs 110 VGPRs (4 waves) and ran 4-9% slower on C1, C3 and C4.
 constexpr int kBatch = 8;
@@ -295,8 +299,8 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
            const uint8_t* residue_atomic, int rows, int cols, int N, const float* B, float* C,
            int task_chunk, const uint32_t* task_map, uint32_t task_map_len, hipStream_t stream) {
   PS_CHECK_ARG(N > 0 && N % 32 == 0, "SpMM requires N to be a positive multiple of 32");
-  const int chunk_log2 = task_chunk_log2(task_chunk);
-  PS_CHECK_ARG(chunk_log2 >= 0, "SpMM task_chunk must be 0 or a power of two up to 256");
+  PS_CHECK_ARG(task_chunk_valid(task_chunk),
+               "SpMM task_chunk must be PS_TASK_CHUNK_AUTO, 0 or a power of two up to 4096");
   PS_CHECK_ARG(int64_t(rows) * N <= INT32_MAX && int64_t(cols) * N <= INT32_MAX,
                "Dense dimensions exceed the 32-bit kernel indexing range");
   PS_CHECK_ARG(B && C, "Invalid SpMM buffers");
@@ -304,7 +308,6 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
   const int lpn = pick_lpn(N);
   const TaskShape shape = spmm_task_shape(N);
   SpmmArgs a{};
-  a.chunk_log2 = uint32_t(chunk_log2);
   a.N = N;
   a.slices = N / (4 * lpn);
   a.B = B;
@@ -353,6 +356,7 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
   PS_CHECK_ARG(tasks < (1ull << 31), "SpMM task count exceeds the launch range");
   a.total_tasks = uint32_t(tasks);
   const unsigned grid = unsigned((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
+  a.chunk_log2 = uint32_t(task_chunk_log2(task_chunk, grid, kAutoChunkMax));
   switch (lpn) {
     case 8: launch_lpn<8>(a, buf, grid, stream); break;
     case 16: launch_lpn<16>(a, buf, grid, stream); break;
@@ -387,8 +391,8 @@ int ps_spmm_launch(int workset_count, const ps_workset* worksets, const int* res
 
 int ps_spmm_launch_ordered(int workset_count, const ps_workset* worksets,
                            const int* residue_offset, const uint8_t* residue_atomic, int rows,
-                           int cols, int N, const float* B, float* C, const uint32_t* task_order,
-                           uint32_t task_count, ps_stream_t stream) {
+                           int cols, int N, const float* B, float* C, int task_chunk,
+                           const uint32_t* task_order, uint32_t task_count, ps_stream_t stream) {
   PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets,
                "Invalid SpMM workset count");
   int order[PS_MAX_WORKSETS];
@@ -398,7 +402,7 @@ int ps_spmm_launch_ordered(int workset_count, const ps_workset* worksets,
     ordered[q] = worksets[workset_count - 1 - q];
   }
   return ps::launch(workset_count, order, ordered, residue_offset, residue_atomic, rows, cols,
-                    N, B, C, 1, task_order, task_count, ps::to_hip(stream));
+                    N, B, C, task_chunk, task_order, task_count, ps::to_hip(stream));
 }
 
 int ps_spmm_workset_launch(int s, const ps_workset* workset, const int* residue_offset,

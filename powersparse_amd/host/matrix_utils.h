@@ -72,9 +72,10 @@ constexpr double kRowOrderGain = 0.85;
 // Workgroup -> XCD runs (ps_spmm_launch's task_chunk) per task order: in a
 // row-ordered copy neighbouring groups share columns, so runs of 64 tasks stay
 // under one L2 (C4: 4% faster than 16, 10-15% faster than the hardware's round
-// robin); in signature order the round robin was as fast or faster (C3: 5-8%
-// faster than runs of 16).
-constexpr int kRowOrderTaskChunk = 64, kSignatureOrderTaskChunk = 1;
+// robin); in signature order and the locality run orders the launchers size
+// the runs from the launch (PS_TASK_CHUNK_AUTO: C3 SpMM on the tuned partition
+// 3-4% and SDDMM N = 128 1.4% faster than the round robin; C1 SpMM 4-5%).
+constexpr int kRowOrderTaskChunk = 64, kSignatureOrderTaskChunk = PS_TASK_CHUNK_AUTO;
 constexpr int kLocalityWindow = 65536, kLocalityWindows = 128;
 
 // The worksets as the operators run them: the public ones (out_base ==

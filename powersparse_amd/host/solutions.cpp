@@ -87,8 +87,8 @@ void SpMMAsync(const PowerSparseMatrixGPU& matrix, int N, const float* B, float*
   if (e.run_order[k])
     ThrowOnError(ps_spmm_launch_ordered(m.GroupTypeNum(), ws.data(), e.residue_offset,
                                         reinterpret_cast<const uint8_t*>(e.residue_atomic),
-                                        m.MatrixRow(), m.MatrixCol(), N, B, C, e.run_order[k],
-                                        e.run_order_tasks[k], stream));
+                                        m.MatrixRow(), m.MatrixCol(), N, B, C, e.task_chunk,
+                                        e.run_order[k], e.run_order_tasks[k], stream));
   else
     ThrowOnError(ps_spmm_launch(m.GroupTypeNum(), ws.data(), e.residue_offset,
                                 reinterpret_cast<const uint8_t*>(e.residue_atomic),
@@ -123,7 +123,7 @@ void SDDMMAsync(const PowerSparseMatrixGPU& m, int N, const float* lhs, const fl
   else if (e.run_order[RunOrderSlot(PS_OP_SDDMM, N)])
     ThrowOnError(ps_sddmm_launch_ordered(m.GroupTypeNum(), ws.data(), e.residue_offset,
                                          m.MatrixRow(), m.MatrixCol(), N, lhs, rhs, out,
-                                         e.run_order[RunOrderSlot(PS_OP_SDDMM, N)],
+                                         e.task_chunk, e.run_order[RunOrderSlot(PS_OP_SDDMM, N)],
                                          e.run_order_tasks[RunOrderSlot(PS_OP_SDDMM, N)],
                                          stream));
   else
@@ -143,8 +143,8 @@ void SDDMMToCSR(const PowerSparseMatrixGPU& m, int N, const float* lhs, const fl
   if (e.run_order[k])
     ThrowOnError(ps_sddmm_csr_launch_ordered(m.GroupTypeNum(), ws.data(), e.residue_offset,
                                              e.csr_pos, m.MatrixRow(), m.MatrixCol(), N, lhs,
-                                             rhs, out_csr, e.run_order[k], e.run_order_tasks[k],
-                                             stream));
+                                             rhs, out_csr, e.task_chunk, e.run_order[k],
+                                             e.run_order_tasks[k], stream));
   else
     ThrowOnError(ps_sddmm_csr_launch(m.GroupTypeNum(), ws.data(), e.residue_offset, e.csr_pos,
                                      m.MatrixRow(), m.MatrixCol(), N, lhs, rhs, out_csr,

@@ -9,6 +9,7 @@ import oracle
 import powersparse_amd as ps
 import tolerance
 from gpu_util import Uploaded, random_graph, say, setup, star_graph
+from powersparse_amd import _native
 
 pytestmark = pytest.mark.gpu
 
@@ -261,7 +262,7 @@ def test_task_chunk_mapping(name):
     dB, dX, dY = ps.DeviceBuffer(host=B), ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
     E, M = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, N, B, with_mag=True)
     ref = None
-    for chunk in (0, 1, 2, 16, 64, 256):
+    for chunk in (0, 1, 2, 16, 64, 256, 4096, _native.PS_TASK_CHUNK_AUTO):
         dC = ps.DeviceBuffer.zeros(csr.rows * N * 4)
         ps.spmm_launch(up.worksets, up.offset, up.atomic, csr.rows, csr.cols, N, dB, dC,
                        task_chunk=chunk)
@@ -277,7 +278,7 @@ def test_task_chunk_mapping(name):
         for s in range(w.S):
             np.testing.assert_array_equal(got[s], ref[s], err_msg=f"chunk {chunk} workset {s}")
     dC = ps.DeviceBuffer.zeros(csr.rows * N * 4)
-    for bad in (3, 512, -1):
+    for bad in (3, 8192, -2):
         with pytest.raises(ValueError, match="task_chunk"):
             ps.spmm_launch(up.worksets, up.offset, up.atomic, csr.rows, csr.cols, N, dB, dC,
                            task_chunk=bad)

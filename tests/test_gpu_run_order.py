@@ -154,7 +154,7 @@ def test_any_permutation_gives_the_same_results():
     dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
     sizes = m.sddmm_output_sizes()
 
-    def sddmm(order):
+    def sddmm(order, chunk=1):
         outs = [ps.DeviceBuffer.zeros(max(k, 1) * 4) for k in sizes]
         oa = (ctypes.c_void_p * S)(*[o.ptr for o in outs])
         if order is None:
@@ -163,8 +163,8 @@ def test_any_permutation_gives_the_same_results():
         else:
             d = ps.DeviceBuffer(host=order)
             ps._hip_call(_native.hip().ps_sddmm_launch_ordered(
-                S, arr, m.ResidueOffset(), csr.rows, csr.cols, N, dX.ptr, dY.ptr, oa, d.ptr,
-                order.size, None))
+                S, arr, m.ResidueOffset(), csr.rows, csr.cols, N, dX.ptr, dY.ptr, oa, chunk,
+                d.ptr, order.size, None))
         ps.synchronize()
         return [o.download(np.float32, k) for o, k in zip(outs, sizes)]
 
@@ -172,10 +172,10 @@ def test_any_permutation_gives_the_same_results():
     ps._hip_call(_native.hip().ps_task_count(_native.PS_OP_SDDMM, N, S, arr,
                                              ctypes.byref(count)))
     base = sddmm(None)
-    for trial in range(3):
+    for trial, chunk in enumerate((1, _native.PS_TASK_CHUNK_AUTO, 4)):
         perm = rng.permutation(count.value).astype(np.uint32)
-        say(f"random task permutation {trial}: {perm.size} tasks")
-        for x, y in zip(base, sddmm(perm)):
+        say(f"random task permutation {trial}: {perm.size} tasks, task_chunk {chunk}")
+        for x, y in zip(base, sddmm(perm, chunk)):
             np.testing.assert_array_equal(x.view(np.uint32), y.view(np.uint32))
     # SpMM with a random permutation against the oracle
     B = rng.uniform(-1, 1, (csr.cols, 32)).astype(np.float32)
@@ -186,12 +186,17 @@ def test_any_permutation_gives_the_same_results():
     C = ps.DeviceBuffer.zeros(csr.rows * 32 * 4)
     ps._hip_call(_native.hip().ps_spmm_launch_ordered(
         S, arr, m.ResidueOffset(), m.ResidueAtomic(), csr.rows, csr.cols, 32, dB.ptr, C.ptr,
-        perm.ptr, count.value, None))
+        _native.PS_TASK_CHUNK_AUTO, perm.ptr, count.value, None))
     ps.synchronize()
     E, M = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, 32, B, with_mag=True)
     tolerance.check(C.download(np.float32).reshape(csr.rows, 32), E, M, "SpMM permuted")
     # a task count that does not match the launch is rejected before any work
     rc = _native.hip().ps_spmm_launch_ordered(
         S, arr, m.ResidueOffset(), m.ResidueAtomic(), csr.rows, csr.cols, 32, dB.ptr, C.ptr,
-        perm.ptr, count.value - 1, None)
+        1, perm.ptr, count.value - 1, None)
     assert rc == _native.PS_ERR_INVALID and b"task order" in _native.hip().ps_last_error()
+    # and so is a task_chunk the launchers do not take
+    rc = _native.hip().ps_spmm_launch_ordered(
+        S, arr, m.ResidueOffset(), m.ResidueAtomic(), csr.rows, csr.cols, 32, dB.ptr, C.ptr,
+        -2, perm.ptr, count.value, None)
+    assert rc == _native.PS_ERR_INVALID and b"task_chunk" in _native.hip().ps_last_error()
