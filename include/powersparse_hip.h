@@ -200,12 +200,12 @@ int ps_sddmm_csr_launch(int workset_count, const ps_workset* worksets, const int
 #define PS_OP_SDDMM 1
 
 /* Number of tasks of one fused launch of operator op at width N (for SpMM:
- * of one 32-column slice; every slice runs the same tasks). Tasks are
- * numbered in launch order: the worksets from the largest group size down to
- * the residue (empty ones skipped); a block workset of G groups of GS
- * nonzeros gives ceil(G * GS / T) tile tasks, the residue ceil(G0 / R) tasks
- * of consecutive groups, with T = 256, R = 8 for SpMM (T = 128, R = 4 at
- * N = 64) and T = 64, R = 8 for SDDMM. No reference counterpart. */
+ * of one column slice; every slice runs the same tasks). Tasks are numbered
+ * in launch order: the worksets from the largest group size down to the
+ * residue (empty ones skipped); a block workset of G groups of GS nonzeros
+ * gives ceil(G * GS / T) tile tasks, the residue ceil(G0 / R) tasks of
+ * consecutive groups, with T = 256, R = 8 for SpMM (T = 128, R = 4 when N is
+ * a multiple of 64) and T = 64, R = 8 for SDDMM. No reference counterpart. */
 int ps_task_count(int op, int N, int workset_count, const ps_workset* worksets,
                   uint32_t* count);
 /* The locality run order of such a launch into order[count] (device memory,

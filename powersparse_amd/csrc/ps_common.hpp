@@ -113,9 +113,10 @@ struct TaskShape {
   int tile_nnz;
   int residue_groups;
 };
-// SpMM: lanes per B-row slice (16 for N = 64, else 8), slots of lanes per wave,
-// 32 nonzeros per slot per tile, one residue group per slot.
-inline int spmm_lanes_per_row(int N) { return N == 64 ? 16 : 8; }
+// SpMM: lanes per B-row slice (16 when N is a multiple of 64: slices of 64
+// floats; else 8: slices of 32), slots of lanes per wave, 32 nonzeros per slot
+// per tile, one residue group per slot.
+inline int spmm_lanes_per_row(int N) { return N % 64 == 0 ? 16 : 8; }
 inline TaskShape spmm_task_shape(int N) {
   const int slots = kWave / spmm_lanes_per_row(N);
   return {32 * slots, slots};

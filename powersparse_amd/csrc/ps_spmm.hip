@@ -5,7 +5,8 @@
 // arguments. Lanes form SL = 64 / LPN slots of LPN lanes; a slot reads one B-row
 // slice of 4 * LPN floats with 128-bit loads, so one wave instruction gathers SL
 // B rows. Every lane accumulates a float4 of its slot's output row. Wide N runs
-// as column slices of 32 floats, all tasks of one slice before the next.
+// as column slices of 64 (N a multiple of 64) or 32 floats, all tasks of one
+// slice before the next.
 //
 //   block workset (groups of GS = 32 * 2^(s-1) nonzeros): a task is a tile of
 //     T = 32 * SL consecutive stored nonzeros; slot q owns nonzeros
@@ -281,11 +282,15 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs ar
   }
 }
 
-// Lanes per B-row slice. N = 64 runs as one 64-float slice (16 lanes); every
-// other N runs as N / 32 slices of 32 floats (8 lanes), slice after slice:
-// each pass then gathers 128-byte rows from a cols x 32 working set, whose
-// hot rows an XCD's L2 holds four times more of than of full 512-byte rows
-// at N = 128 (measured on the C1 graph: 2.96 -> 2.53 ms at N = 128).
+// Lanes per B-row slice. N a multiple of 64 runs as N / 64 slices of 64
+// floats (16 lanes), any other N as N / 32 slices of 32 floats (8 lanes),
+// slice after slice. Narrow slices gather from a smaller working set (cols x
+// 32 floats), wide ones read the matrix fewer times and issue half the
+// gathers; at N = 128 the 64-float slices won in the run order and on the
+// tuned partition (C3: 7.39 -> 6.98 ms tuned, 7.83 -> 7.22 ms run order; C1:
+// 2.05 -> 2.03 and 2.23 -> 2.17 ms; one 128-float slice: 7.25 / 7.19 and
+// 2.13 / 2.19 ms), where in the first build's stored order the 32-float
+// slices had been faster (C1: 2.96 -> 2.53 ms against 128-float slices).
 int pick_lpn(int N) { return spmm_lanes_per_row(N); }
 
 template <int LPN>

@@ -92,16 +92,17 @@ struct ExecutionLayout {
   const int* const* csr_pos = nullptr;
   int task_chunk = kSignatureOrderTaskChunk;
   // Run orders of the fused launches (null: tasks run as stored), indexed by
-  // RunOrderSlot(): SpMM at N != 64, SpMM at N = 64, SDDMM.
+  // RunOrderSlot(): SpMM in 32-float slices, SpMM in 64-float slices, SDDMM.
   const uint32_t* run_order[3] = {nullptr, nullptr, nullptr};
   uint32_t run_order_tasks[3] = {0, 0, 0};
 };
 
 // Which run order a launch of operator op (PS_OP_SPMM / PS_OP_SDDMM) at width
-// N uses: the three operator task shapes (SpMM tiles of 256 or, at N = 64, 128
-// nonzeros; SDDMM tiles of 64).
+// N uses: the three operator task shapes (SpMM tiles of 256 nonzeros, or of
+// 128 when N is a multiple of 64 and runs in 64-float slices; SDDMM tiles of
+// 64).
 inline int RunOrderSlot(int op, int N) {
-  return op == PS_OP_SDDMM ? 2 : (N == 64 ? 1 : 0);
+  return op == PS_OP_SDDMM ? 2 : (N % 64 == 0 ? 1 : 0);
 }
 
 // Partition settings. The reference hard-codes all of them except the CU
