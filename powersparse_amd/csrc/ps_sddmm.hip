@@ -88,13 +88,15 @@ __device__ __forceinline__ float slot_transpose_sum(const float (&p)[8], int sub
 }
 
 // Partial dots of the 8 nonzeros of this lane's slot (Y row byte offsets in
-// yoff[]), `kSteps` nonzeros per batch so that about 16 loads are in flight.
+// yoff[]), `kSteps` nonzeros per batch: 8-16 loads in flight per lane.
 template <int KQ, bool kBuf>
 __device__ __forceinline__ void slot_dots(const Rows<kBuf>& Y,
                                           const typename Rows<kBuf>::Off (&yoff)[8],
                                           const float4 (&x)[KQ], float (&p)[8]) {
-  // a power of two dividing the 8 steps, about 16 / KQ
-  constexpr int kSteps = KQ <= 2 ? 8 : (KQ <= 4 ? 4 : (KQ <= 8 ? 2 : 1));
+  // a power of two dividing the 8 steps: 16 loads for K <= 64, 8 for K = 96,
+  // 128 (in the run order, C3 N = 128: 7.69 ms with 16, 7.50 with 8, 7.74
+  // with 4; C1 2.272 / 2.278 / 2.342 ms), 16 for K <= 256, 16-32 beyond
+  constexpr int kSteps = KQ <= 2 ? 8 : (KQ <= 4 ? 2 : (KQ <= 8 ? 2 : 1));
   static_assert(8 % kSteps == 0, "batches must tile the slot's 8 nonzeros");
 #pragma unroll
   for (int b = 0; b < 8; b += kSteps) {
