@@ -32,12 +32,12 @@
 // worksets. Each task's work is the same in any order.
 //
 // Workgroup -> task mapping: the hardware deals workgroups round-robin over
-// the 8 XCDs (workgroups b and b + 8 on the same one). With task_chunk > 1, windows of 8 * task_chunk consecutive
-// workgroups are re-dealt so that each XCD takes task_chunk consecutive ones:
-// neighbouring tasks share an XCD's L2, while every XCD still gets a slice of
-// every window (balance when task costs vary along the list). Worksets in row
-// order (neighbouring rows share columns) gain from long runs; in signature
-// order the hardware's round robin was as fast or faster.
+// the 8 XCDs (workgroups b and b + 8 on the same one). With task_chunk > 1,
+// windows of 8 * task_chunk consecutive workgroups are re-dealt so that each
+// XCD takes task_chunk consecutive ones: neighbouring tasks share an XCD's
+// L2, while every XCD still gets a slice of every window (balance when task
+// costs vary along the list). The deal applies before the run order's map.
+// PS_TASK_CHUNK_AUTO sizes the runs from the launch (up to kAutoChunkMax).
 //
 // Reference behaviour kept (PowerSparse_SpMM/spmm_solution.cu:7-34,
 // spmm_kernel_block.cu:60-162, spmm_kernel_residue.cu:5-82): block groups and
