@@ -104,14 +104,17 @@ def test_operators_in_run_order_match_stored_order(name):
     setup()
     make, cu = GRAPHS[name]
     csr = make()
+    # SpMM on the public worksets, so that it runs their run order too
     a = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=cu, task_order="signature",
-                                         csr_positions=True)
+                                         csr_positions=True, spmm_partition="parity")
     b = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=cu, task_order="signature",
-                                         csr_positions=True, run_order=False)
+                                         csr_positions=True, run_order=False,
+                                         spmm_partition="parity")
     assert a.run_order and not b.run_order
     rng = np.random.default_rng(7)
     rows = np.arange(csr.rows, dtype=np.int32)
-    for N in (32, 64, 128):
+    # 32- and 64-float SpMM slices (N = 96: three 32-float slices; 256: four 64-float)
+    for N in (32, 64, 96, 128, 256):
         say(f"run order vs stored {name} N={N}")
         B = rng.uniform(-1, 1, (csr.cols, N)).astype(np.float32)
         dB = ps.DeviceBuffer(host=B)
