@@ -145,7 +145,8 @@ typedef struct ps_workset {
  * not depend on it. Worksets whose neighbouring groups share columns (a
  * row-ordered copy of a graph with locality) run faster with runs of 64.
  * PS_TASK_CHUNK_AUTO picks the run from the launch size: the largest power of
- * two that leaves 128 workgroups per run, at most 1024 (SpMM) or 256 (SDDMM);
+ * two that leaves at least 128 runs in the launch (16 windows of 8 runs), at
+ * most 1024 (SpMM) or 256 (SDDMM);
  * measured on signature-ordered worksets and locality run orders (C1, C3:
  * 1-5% faster than the round robin). No reference counterpart.
  * Replaces: the launch loop of PowerSparse::SpMM (PowerSparse_SpMM/spmm_solution.cu:16-31)

@@ -131,7 +131,7 @@ inline bool task_chunk_valid(int task_chunk) {
          (task_chunk > 0 && task_chunk <= 4096 && (task_chunk & (task_chunk - 1)) == 0);
 }
 // log2 of the run length for a launch of `grid` workgroups. AUTO: the largest
-// power of two up to `auto_max` that leaves at least 128 workgroups per run,
+// power of two up to `auto_max` that leaves at least 128 runs in the launch,
 // i.e. 16 windows of 8 runs (the last, partial window keeps the hardware's
 // order, and within a window the XCDs take runs of unequal cost).
 inline int task_chunk_log2(int task_chunk, uint64_t grid, int auto_max) {
