@@ -54,6 +54,9 @@ typedef struct psx_build_options {
   int stored_order;  /* nonzero: no locality run order (PartitionPolicy::run_order off) */
   int max_group_types; /* cap on the workset count S (0: none) */
   int parity_spmm;   /* nonzero: SpMM on the public worksets (SpmmPartition::kParity) */
+  int no_hub_block;  /* nonzero: no dense hub block (HubBlock::kOff) */
+  int hub_min_degree; /* with hub_min_count > 0: explicit block thresholds */
+  int hub_min_count;
 } psx_build_options;
 /* Group order the operators run in (same results; TaskOrder in matrix_utils.h):
  * the public signature order, or a row-ordered execution copy kept when it
@@ -77,6 +80,9 @@ int psx_matrix_run_order(const psx_matrix* m, int* used);
  * GroupTypeNum() when SpMM runs on the public worksets). No reference
  * counterpart. */
 int psx_matrix_spmm_worksets(const psx_matrix* m, int* group_type_num);
+/* The dense hub block the build chose (HubRows() x HubCols(); 0 x 0 when
+ * none); outputs may be NULL. No reference counterpart. */
+int psx_matrix_hub_block(const psx_matrix* m, int* rows, int* cols);
 /* Replaces: ~PowerSparseMatrixGPU (matrix_utils.h:24). */
 int psx_matrix_destroy(psx_matrix* m);
 /* Replaces: MatrixRow/MatrixCol/MatrixNNZ/GroupTypeNum/GroupFineSize (matrix_utils.h:30-34);

@@ -218,13 +218,26 @@ int ps_task_count(int op, int N, int workset_count, const ps_workset* worksets,
  * runs each workset's groups in stored order, one kernel per workset). */
 int ps_task_order_build(int op, int N, int workset_count, const ps_workset* worksets,
                         uint32_t* order, uint32_t count, ps_stream_t stream);
+/* The same order with the tiles of marked groups left out: skip_groups[s]
+ * (device, group_num bytes, or NULL; ignored for the residue) marks groups of
+ * block workset s, and a tile whose groups are all marked goes to the end of
+ * order; *kept receives the number of tasks before them, the task count to
+ * pass to ps_sddmm_launch_ordered so that only those run. No reference
+ * counterpart. */
+int ps_task_order_build_subset(int op, int N, int workset_count, const ps_workset* worksets,
+                               const uint8_t* const* skip_groups, uint32_t* order, uint32_t count,
+                               uint32_t* kept, ps_stream_t stream);
 
 /* ps_spmm_launch, ps_sddmm_launch and ps_sddmm_csr_launch with the tasks run
  * in a given order: the workgroups are dealt to the XCDs as task_chunk says,
  * and task t of that sequence runs task task_order[t] (a permutation of the
- * ps_task_count tasks; task_count must equal that count). Every task does the
- * same work in any order: SDDMM results are bitwise those of the unordered
- * launch, SpMM's differ only in the order of FP32 atomic additions. */
+ * ps_task_count tasks; task_count must equal that count for SpMM). Every task
+ * does the same work in any order: SDDMM results are bitwise those of the
+ * unordered launch, SpMM's differ only in the order of FP32 atomic additions.
+ * The SDDMM variants also take task_count below the launch's count: then only
+ * the first task_count entries of task_order run (see
+ * ps_task_order_build_subset; the outputs of the other tasks are not
+ * written). */
 int ps_spmm_launch_ordered(int workset_count, const ps_workset* worksets,
                            const int* residue_offset, const uint8_t* residue_atomic, int rows,
                            int cols, int N, const float* B, float* C, int task_chunk,
@@ -256,6 +269,73 @@ int ps_sddmm_scatter_launch(int workset_count, const ps_workset* worksets,
  * Replaces: the same caller-side permutation (PowerSparse_SDDMM.h:11-12). */
 int ps_workset_to_csr(int workset_count, const long long* lengths, const int* const* csr_pos,
                       const float* const* in, float* out_csr, ps_stream_t stream);
+
+/* ------------------------------------------------------- dense hub block */
+/* The hub rows (highest degree) restricted to the hot columns (most nonzeros)
+ * of a matrix, run as dense FP32 products (hipBLASLt, compute type 32F).
+ * All pointers are device memory. hot_rank / hub_index map a matrix column /
+ * row to its position in hot_cols / hub_rows, or -1. dense (rows x cols,
+ * row-major) holds the block's stored values (repeated entries summed), 0
+ * where nothing is stored; stored has one bit per dense element (rows x
+ * ceil(cols / 32) words, bit h % 32 of word h / 32) set where an entry is
+ * stored. No reference counterpart. */
+typedef struct ps_hub_block {
+  int matrix_rows, matrix_cols;
+  int rows;              /* R: hub rows */
+  int cols;              /* H: hot columns */
+  const int* hub_rows;   /* [R] */
+  const int* hub_index;  /* [matrix_rows] */
+  const int* hot_cols;   /* [H] */
+  const int* hot_rank;   /* [matrix_cols] */
+  const float* dense;    /* [R * H] */
+  const uint32_t* stored;
+} ps_hub_block;
+
+/* hist[32 * 32] (device, written): hist[a * 32 + b] = stored entries of rows of
+ * degree in [2^a, 2^(a+1)) (degree >= 256 only) whose column count col_nnz is
+ * in [2^b, 2^(b+1)); the statistics a block is chosen from. */
+int ps_hub_histogram(const int* row_ptr, int rows, const int* col_ind, const int* col_nnz,
+                     unsigned long long* hist, ps_stream_t stream);
+/* Words of the stored bit mask. */
+size_t ps_hub_stored_words(const ps_hub_block* hb);
+/* Fills dense (rows x cols floats) and stored from the matrix CSR. */
+int ps_hub_dense_build(const ps_hub_block* hb, const int* row_ptr, const int* col_ind,
+                       const float* sp_data, float* dense, uint32_t* stored, ps_stream_t stream);
+/* counts[r] = stored entries of row r outside the block (matrix_rows values). */
+int ps_hub_kept_counts(const ps_hub_block* hb, const int* row_ptr, const int* col_ind,
+                       uint32_t* counts, ps_stream_t stream);
+/* The CSR without the block's entries (order within rows kept); new_row_ptr is
+ * the exclusive scan of ps_hub_kept_counts. */
+int ps_hub_compact(const ps_hub_block* hb, const int* row_ptr, const int* col_ind,
+                   const float* sp_data, const uint32_t* new_row_ptr, int* new_col,
+                   float* new_val, ps_stream_t stream);
+/* residue_atomic[g] = 1 for every residue group g whose row (group_des[g]) is a
+ * hub row (the rows of a partition without the block keep accumulating). */
+int ps_hub_mark_atomic(const ps_hub_block* hb, const int* group_des, int group_num,
+                       uint8_t* residue_atomic, ps_stream_t stream);
+/* flags[g] = 1 when group g of a block workset of groups >= 64 nonzeros
+ * belongs to a hub row and all its columns are hot, else 0. */
+int ps_hub_group_flags(const ps_hub_block* hb, const ps_workset* workset, uint8_t* flags,
+                       ps_stream_t stream);
+/* Device workspace bytes of ps_hub_spmm_launch (op PS_OP_SPMM) or
+ * ps_hub_sddmm_launch (PS_OP_SDDMM) at width N. */
+size_t ps_hub_workspace_bytes(const ps_hub_block* hb, int op, int N);
+/* C[hub_rows[i], :] += sum over stored block entries (i, h) of value * B[hot_cols[h], :],
+ * B (matrix_cols x N) and C (matrix_rows x N) row-major; Inf / NaN in B reach
+ * exactly the rows that store their column. Calls overlapping on one
+ * workspace race. */
+int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, void* workspace,
+                       size_t workspace_bytes, ps_stream_t stream);
+/* For every listed tile (hot_tiles[s][0 .. hot_tile_count[s]), 64-nonzero tiles
+ * of block workset s, groups >= 64 nonzeros, inside the block):
+ * out[s][p] = sp_data[p] * dot(lhs[group_des[g], :], rhs[col_ind[p], :]) for
+ * its 64 nonzeros p, computed as one dense product of the hub rows of lhs
+ * with the hot rows of rhs; with out_csr, out_csr[out_pos[s][p]] instead. */
+int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
+                        const uint32_t* const* hot_tiles, const uint32_t* hot_tile_count, int N,
+                        const float* lhs, const float* rhs, float* const* out,
+                        const int* const* out_pos, float* out_csr, void* workspace,
+                        size_t workspace_bytes, ps_stream_t stream);
 
 /* ---------------------------------------------------------- primitives */
 /* Device-wide exclusive prefix sum of n uint32 values (out may alias in).

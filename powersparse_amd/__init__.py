@@ -349,8 +349,13 @@ class PowerSparseMatrixGPU:
     each stored nonzero's CSR position (SDDMMToCSR, WorksetToCSR). task_order
     ("auto", "signature" or "row") picks the group order the operators run in
     (same results); `.task_order` and `.locality` report the choice and the
-    scores compared. With timings=True the stage times (ms) are kept in
-    `.timings` (the task-order step counts into "gather").
+    scores compared. hub_block ("auto" or "off") keeps the dense hub block
+    (rows of highest degree x most popular columns) as a dense matrix run on
+    the matrix cores when the cost rule finds one, and hub_min_degree /
+    hub_min_count (both > 0) set its thresholds explicitly; `.hub_block`
+    reports its (rows, columns), (0, 0) when none. With timings=True the stage
+    times (ms) are kept in `.timings` (the task-order step counts into
+    "gather").
     """
 
     TIMING_KEYS = ("upload", "analyze", "rank", "groups", "sigbit", "signature", "order",
@@ -361,7 +366,7 @@ class PowerSparseMatrixGPU:
     def __init__(self, row_num, col_num, nnz_num, row_ptr, col_ind, sp_data, cu_count=0,
                  timings=False, signature_order="auto", csr_positions=False,
                  task_order="auto", run_order=True, max_group_types=0,
-                 spmm_partition="tuned"):
+                 spmm_partition="tuned", hub_block="auto", hub_min_degree=0, hub_min_count=0):
         row_ptr = np.ascontiguousarray(row_ptr, dtype=np.int32)
         col_ind = np.ascontiguousarray(col_ind, dtype=np.int32)
         sp_data = np.ascontiguousarray(sp_data, dtype=np.float32)
@@ -374,10 +379,13 @@ class PowerSparseMatrixGPU:
             raise ValueError(f"task_order must be one of {self.TASK_ORDERS}")
         if spmm_partition not in ("tuned", "parity"):
             raise ValueError("spmm_partition must be 'tuned' or 'parity'")
+        if hub_block not in ("auto", "off"):
+            raise ValueError("hub_block must be 'auto' or 'off'")
         opts = _native.BuildOptions(int(cu_count), self.ORDER_METHODS.index(signature_order),
                                     int(bool(csr_positions)), self.TASK_ORDERS.index(task_order),
                                     int(not run_order), int(max_group_types),
-                                    int(spmm_partition == "parity"))
+                                    int(spmm_partition == "parity"), int(hub_block == "off"),
+                                    int(hub_min_degree), int(hub_min_count))
         _host_call(_native.host().psx_matrix_create_ex(
             int(row_num), int(col_num), int(nnz_num),
             row_ptr.ctypes.data if row_ptr.size else None,
@@ -398,6 +406,9 @@ class PowerSparseMatrixGPU:
         self.run_order = bool(used.value)
         _host_call(_native.host().psx_matrix_spmm_worksets(self._h, ctypes.byref(used)))
         self.spmm_worksets = used.value  # workset count of the partition SpMM runs on
+        hr, hc = ctypes.c_int(), ctypes.c_int()
+        _host_call(_native.host().psx_matrix_hub_block(self._h, ctypes.byref(hr), ctypes.byref(hc)))
+        self.hub_block = (hr.value, hc.value)
         self.timings = dict(zip(self.TIMING_KEYS, list(t))) if timings else None
         rows, cols, nnz, S, fine, L, cu = (ctypes.c_int() for _ in range(7))
         _host_call(_native.host().psx_matrix_info(
@@ -412,11 +423,13 @@ class PowerSparseMatrixGPU:
     @classmethod
     def from_csr(cls, csr, cu_count=0, timings=False, signature_order="auto",
                  csr_positions=False, task_order="auto", run_order=True, max_group_types=0,
-                 spmm_partition="tuned"):
+                 spmm_partition="tuned", hub_block="auto", hub_min_degree=0, hub_min_count=0):
         return cls(csr.rows, csr.cols, csr.nnz, csr.row_ptr, csr.col_ind, csr.values,
                    cu_count=cu_count, timings=timings, signature_order=signature_order,
                    csr_positions=csr_positions, task_order=task_order, run_order=run_order,
-                   max_group_types=max_group_types, spmm_partition=spmm_partition)
+                   max_group_types=max_group_types, spmm_partition=spmm_partition,
+                   hub_block=hub_block, hub_min_degree=hub_min_degree,
+                   hub_min_count=hub_min_count)
 
     def close(self):
         if self._h:

@@ -38,7 +38,8 @@ class BuildOptions(ctypes.Structure):
     _fields_ = [("cu_count", ctypes.c_int), ("signature_order", ctypes.c_int),
                 ("csr_positions", ctypes.c_int), ("task_order", ctypes.c_int),
                 ("stored_order", ctypes.c_int), ("max_group_types", ctypes.c_int),
-                ("parity_spmm", ctypes.c_int)]
+                ("parity_spmm", ctypes.c_int), ("no_hub_block", ctypes.c_int),
+                ("hub_min_degree", ctypes.c_int), ("hub_min_count", ctypes.c_int)]
 
 
 class DeviceProps(ctypes.Structure):
@@ -67,6 +68,23 @@ class Workset(ctypes.Structure):
         ("group_num", ctypes.c_int),
         ("group_size", ctypes.c_int),
         ("order", c_void_p),
+    ]
+
+
+class HubBlock(ctypes.Structure):
+    """ps_hub_block: the dense hub block of a matrix (device pointers)."""
+
+    _fields_ = [
+        ("matrix_rows", ctypes.c_int),
+        ("matrix_cols", ctypes.c_int),
+        ("rows", ctypes.c_int),
+        ("cols", ctypes.c_int),
+        ("hub_rows", c_void_p),
+        ("hub_index", c_void_p),
+        ("hot_cols", c_void_p),
+        ("hot_rank", c_void_p),
+        ("dense", c_void_p),
+        ("stored", c_void_p),
     ]
 
 
@@ -128,6 +146,32 @@ HIP_API = [
     ("ps_task_order_build", ctypes.c_int,
      [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(Workset), c_void_p,
       ctypes.c_uint32, c_void_p]),
+    ("ps_task_order_build_subset", ctypes.c_int,
+     [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(Workset),
+      ctypes.POINTER(c_void_p), c_void_p, ctypes.c_uint32, c_u32_p, c_void_p]),
+    ("ps_hub_histogram", ctypes.c_int,
+     [c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("ps_hub_stored_words", ctypes.c_size_t, [ctypes.POINTER(HubBlock)]),
+    ("ps_hub_dense_build", ctypes.c_int,
+     [ctypes.POINTER(HubBlock), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("ps_hub_kept_counts", ctypes.c_int,
+     [ctypes.POINTER(HubBlock), c_void_p, c_void_p, c_void_p, c_void_p]),
+    ("ps_hub_compact", ctypes.c_int,
+     [ctypes.POINTER(HubBlock), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+      c_void_p]),
+    ("ps_hub_mark_atomic", ctypes.c_int,
+     [ctypes.POINTER(HubBlock), c_void_p, ctypes.c_int, c_void_p, c_void_p]),
+    ("ps_hub_group_flags", ctypes.c_int,
+     [ctypes.POINTER(HubBlock), ctypes.POINTER(Workset), c_void_p, c_void_p]),
+    ("ps_hub_workspace_bytes", ctypes.c_size_t,
+     [ctypes.POINTER(HubBlock), ctypes.c_int, ctypes.c_int]),
+    ("ps_hub_spmm_launch", ctypes.c_int,
+     [ctypes.POINTER(HubBlock), ctypes.c_int, c_void_p, c_void_p, c_void_p, ctypes.c_size_t,
+      c_void_p]),
+    ("ps_hub_sddmm_launch", ctypes.c_int,
+     [ctypes.POINTER(HubBlock), ctypes.c_int, ctypes.POINTER(Workset), ctypes.POINTER(c_void_p),
+      c_u32_p, ctypes.c_int, c_void_p, c_void_p, ctypes.POINTER(c_void_p),
+      ctypes.POINTER(c_void_p), c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
     ("ps_spmm_launch_ordered", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
       ctypes.c_int, c_void_p, c_void_p, ctypes.c_int, c_void_p, ctypes.c_uint32, c_void_p]),
@@ -217,6 +261,7 @@ HOST_API = [
     ("psx_matrix_task_order", ctypes.c_int, [c_void_p, c_int_p, c_double_p, c_double_p]),
     ("psx_matrix_run_order", ctypes.c_int, [c_void_p, c_int_p]),
     ("psx_matrix_spmm_worksets", ctypes.c_int, [c_void_p, c_int_p]),
+    ("psx_matrix_hub_block", ctypes.c_int, [c_void_p, c_int_p, c_int_p]),
     ("psx_matrix_destroy", ctypes.c_int, [c_void_p]),
     ("psx_matrix_info", ctypes.c_int,
      [c_void_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p]),

@@ -24,9 +24,13 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr uint32_t kResidueKey = 0x80000000u;  // after every column id (< 2^31)
+constexpr uint32_t kSkipKey = 0xFFFFFFFFu;     // after everything: tiles left out
 
 struct TaskKeyArgs {
   const int* col_ind[PS_MAX_WORKSETS];
+  const uint8_t* skip[PS_MAX_WORKSETS];  // per group: leave its tiles out (or null)
+  uint64_t nnz[PS_MAX_WORKSETS];         // block workset: group_num * group_size
+  int group_size[PS_MAX_WORKSETS];
   uint32_t task_begin[PS_MAX_WORKSETS + 1];
   int residue[PS_MAX_WORKSETS];  // 1 for the residue workset
   int count;
@@ -36,16 +40,35 @@ struct TaskKeyArgs {
 };
 
 // key[t] = the first column of block tile t (its nonzeros are stored columns
-// ascending within each group), kResidueKey for residue tasks; val[t] = t.
+// ascending within each group), kResidueKey for residue tasks, kSkipKey for a
+// block tile whose groups are all marked in skip; val[t] = t. *skipped counts
+// the kSkipKey tiles.
 __global__ __launch_bounds__(kThreads) void task_keys_kernel(TaskKeyArgs a, uint32_t* keys,
-                                                             uint32_t* vals) {
+                                                             uint32_t* vals,
+                                                             unsigned int* skipped) {
   for (uint32_t t = blockIdx.x * kThreads + threadIdx.x; t < a.total;
        t += gridDim.x * kThreads) {
     int q = 0;
     while (q + 1 < a.count && t >= a.task_begin[q + 1]) ++q;
     const uint32_t local = t - a.task_begin[q];
-    keys[t] = a.residue[q] ? kResidueKey
-                           : uint32_t(a.col_ind[q][size_t(local) * size_t(a.tile_nnz)]);
+    uint32_t key = kResidueKey;
+    if (!a.residue[q]) {
+      const uint64_t first = uint64_t(local) * uint64_t(a.tile_nnz);
+      key = uint32_t(a.col_ind[q][first]);
+      if (a.skip[q]) {
+        const uint64_t end = first + uint64_t(a.tile_nnz) < a.nnz[q] ? first + a.tile_nnz
+                                                                       : a.nnz[q];
+        bool all = true;
+        for (uint64_t g = first / uint64_t(a.group_size[q]);
+             all && g <= (end - 1) / uint64_t(a.group_size[q]); ++g)
+          all = a.skip[q][g] != 0;
+        if (all) {
+          key = kSkipKey;
+          atomicAdd(skipped, 1u);
+        }
+      }
+    }
+    keys[t] = key;
     vals[t] = t;
   }
 }
@@ -91,6 +114,8 @@ int task_table(int op, int N, int workset_count, const ps_workset* worksets, Tas
       t = (uint64_t(w.group_num) + shape.residue_groups - 1) / uint64_t(shape.residue_groups);
     }
     a->col_ind[n] = w.col_ind;
+    a->group_size[n] = w.group_size;
+    a->nnz[n] = s > 0 ? uint64_t(w.group_num) * uint64_t(w.group_size) : 0;
     a->residue[n] = s == 0;
     a->task_begin[n] = uint32_t(total);
     total += t;
@@ -100,6 +125,65 @@ int task_table(int op, int N, int workset_count, const ps_workset* worksets, Tas
   a->count = n;
   a->task_begin[n] = uint32_t(total);
   a->total = uint32_t(total);
+  return PS_OK;
+}
+
+// The locality order of the launch's tasks, those of skipped groups last;
+// *kept = the tasks before them (all of them without skip flags).
+int build_order(int op, int N, int workset_count, const ps_workset* worksets,
+                const uint8_t* const* skip_groups, uint32_t* order, uint32_t count,
+                uint32_t* kept, ps_stream_t stream) {
+  TaskKeyArgs a;
+  const int rc = task_table(op, N, workset_count, worksets, &a);
+  if (rc != PS_OK) return rc;
+  PS_CHECK_ARG(count == a.total, "ps_task_order_build: order holds " + std::to_string(count) +
+                                     " tasks, the launch " + std::to_string(a.total));
+  if (skip_groups) {
+    // task_table lists the non-empty worksets from the largest group size down
+    int n = 0;
+    for (int q = 0; q < workset_count; ++q) {
+      const int s = workset_count - 1 - q;
+      if (worksets[s].group_num <= 0) continue;
+      a.skip[n++] = s > 0 ? skip_groups[s] : nullptr;
+    }
+  }
+  if (kept) *kept = a.total;
+  if (a.total == 0) return PS_OK;
+  PS_CHECK_ARG(order, "ps_task_order_build: null order");
+  const size_t n = a.total;
+  const size_t radix_ws = ps_radix_workspace_bytes(n);
+  auto round = [](size_t b) { return (b + 255) & ~size_t(255); };
+  const size_t bytes = 3 * round(n * 4) + round(radix_ws) + 256;
+  char* base = nullptr;
+  PS_HIP(hipMalloc(&base, bytes));
+  uint32_t* keys = reinterpret_cast<uint32_t*>(base);
+  uint32_t* keys_alt = reinterpret_cast<uint32_t*>(base + round(n * 4));
+  uint32_t* vals = reinterpret_cast<uint32_t*>(base + 2 * round(n * 4));
+  void* ws = base + 3 * round(n * 4);
+  unsigned int* skipped = reinterpret_cast<unsigned int*>(base + 3 * round(n * 4) + round(radix_ws));
+  hipStream_t st = to_hip(stream);
+  hipError_t e = hipMemsetAsync(skipped, 0, sizeof(unsigned int), st);
+  const size_t blocks = (n + kThreads - 1) / kThreads;
+  if (e == hipSuccess) {
+    task_keys_kernel<<<unsigned(blocks < 65536 ? blocks : 65536), kThreads, 0, st>>>(a, keys, vals,
+                                                                                    skipped);
+    e = hipGetLastError();
+  }
+  int alt = 0;
+  int r = PS_OK;
+  // values sort into vals or order (the alternate buffer); stable, 32 key bits
+  if (e == hipSuccess)
+    r = ps_radix_sort_pairs_u32(keys, keys_alt, vals, order, n, 0, 32, ws, &alt, stream);
+  if (e == hipSuccess && r == PS_OK && !alt)
+    e = hipMemcpyAsync(order, vals, n * 4, hipMemcpyDeviceToDevice, st);
+  unsigned int host_skipped = 0;
+  if (e == hipSuccess && r == PS_OK)
+    e = hipMemcpyAsync(&host_skipped, skipped, sizeof(host_skipped), hipMemcpyDeviceToHost, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  (void)hipFree(base);
+  if (r != PS_OK) return r;
+  PS_HIP(e);
+  if (kept) *kept = a.total - host_skipped;
   return PS_OK;
 }
 
@@ -120,40 +204,14 @@ int ps_task_count(int op, int N, int workset_count, const ps_workset* worksets,
 
 int ps_task_order_build(int op, int N, int workset_count, const ps_workset* worksets,
                         uint32_t* order, uint32_t count, ps_stream_t stream) {
-  ps::TaskKeyArgs a;
-  const int rc = ps::task_table(op, N, workset_count, worksets, &a);
-  if (rc != PS_OK) return rc;
-  PS_CHECK_ARG(count == a.total, "ps_task_order_build: order holds " + std::to_string(count) +
-                                     " tasks, the launch " + std::to_string(a.total));
-  if (a.total == 0) return PS_OK;
-  PS_CHECK_ARG(order, "ps_task_order_build: null order");
-  const size_t n = a.total;
-  const size_t radix_ws = ps_radix_workspace_bytes(n);
-  auto round = [](size_t b) { return (b + 255) & ~size_t(255); };
-  const size_t bytes = 3 * round(n * 4) + round(radix_ws);
-  char* base = nullptr;
-  PS_HIP(hipMalloc(&base, bytes));
-  uint32_t* keys = reinterpret_cast<uint32_t*>(base);
-  uint32_t* keys_alt = reinterpret_cast<uint32_t*>(base + round(n * 4));
-  uint32_t* vals = reinterpret_cast<uint32_t*>(base + 2 * round(n * 4));
-  void* ws = base + 3 * round(n * 4);
-  hipStream_t st = ps::to_hip(stream);
-  const size_t blocks = (n + ps::kThreads - 1) / ps::kThreads;
-  ps::task_keys_kernel<<<unsigned(blocks < 65536 ? blocks : 65536), ps::kThreads, 0, st>>>(
-      a, keys, vals);
-  hipError_t e = hipGetLastError();
-  int alt = 0;
-  int r = PS_OK;
-  // values sort into vals or order (the alternate buffer); stable, 32 key bits
-  if (e == hipSuccess)
-    r = ps_radix_sort_pairs_u32(keys, keys_alt, vals, order, n, 0, 32, ws, &alt, stream);
-  if (e == hipSuccess && r == PS_OK && !alt)
-    e = hipMemcpyAsync(order, vals, n * 4, hipMemcpyDeviceToDevice, st);
-  if (e == hipSuccess) e = hipStreamSynchronize(st);
-  (void)hipFree(base);
-  if (r != PS_OK) return r;
-  PS_HIP(e);
-  return PS_OK;
+  return ps::build_order(op, N, workset_count, worksets, nullptr, order, count, nullptr, stream);
+}
+
+int ps_task_order_build_subset(int op, int N, int workset_count, const ps_workset* worksets,
+                               const uint8_t* const* skip_groups, uint32_t* order, uint32_t count,
+                               uint32_t* kept, ps_stream_t stream) {
+  PS_CHECK_ARG(skip_groups && kept, "ps_task_order_build_subset: null argument");
+  return ps::build_order(op, N, workset_count, worksets, skip_groups, order, count, kept, stream);
 }
 
 }  // extern "C"

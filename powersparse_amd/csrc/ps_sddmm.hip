@@ -52,7 +52,8 @@ struct SddmmArgs {
   uint32_t task_begin[PS_MAX_WORKSETS + 1];
   int32_t count;
   int32_t N;
-  uint32_t total_tasks;
+  uint32_t total_tasks;   // tasks of the worksets
+  uint32_t launch_tasks;  // waves with work: total_tasks, or the task map's length
   const int* residue_offset;
   const float* lhs;
   const float* rhs;
@@ -128,8 +129,8 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
   __shared__ float task_out[kWavesPerBlock][kTaskOut];  // residue results of a task
   const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, args.chunk_log2);
   uint32_t task = __builtin_amdgcn_readfirstlane(blk * kWavesPerBlock + threadIdx.x / kWave);
-  if (task >= args.total_tasks) return;
-  if (args.task_map) {  // a permutation of [0, total_tasks)
+  if (task >= args.launch_tasks) return;
+  if (args.task_map) {  // a permutation of [0, total_tasks), or of a subset of it
     task = __builtin_amdgcn_readfirstlane(args.task_map[task]);
     if (task >= args.total_tasks) return;
   }
@@ -375,13 +376,18 @@ int launch(int count, const int* order, const ps_workset* worksets, float* const
   a.count = n;
   a.task_begin[n] = uint32_t(tasks);
   a.total_tasks = uint32_t(tasks);
+  a.launch_tasks = uint32_t(tasks);
   if (task_map) {
-    PS_CHECK_ARG(task_map_len == tasks,
+    // a subset of the tasks runs when the order lists fewer (the others are
+    // computed elsewhere, e.g. by the dense hub block)
+    PS_CHECK_ARG(task_map_len <= tasks,
                  "SDDMM task order holds " + std::to_string(task_map_len) + " tasks, the launch " +
                      std::to_string(tasks));
     a.task_map = task_map;
+    a.launch_tasks = task_map_len;
   }
-  const unsigned grid = unsigned((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
+  if (a.launch_tasks == 0) return PS_OK;
+  const unsigned grid = unsigned((uint64_t(a.launch_tasks) + kWavesPerBlock - 1) / kWavesPerBlock);
   a.chunk_log2 = uint32_t(task_chunk_log2(task_chunk, grid, kAutoChunkMax));
   switch (N / 32) {
     case 1: launch_kq<1>(a, buf, mode, grid, stream); break;

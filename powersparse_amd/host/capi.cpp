@@ -58,7 +58,7 @@ const char* psx_last_error(void) { return g_error.c_str(); }
 
 int psx_matrix_create(int rows, int cols, int nnz, const int* row_ptr, const int* col_ind,
                       const float* sp_data, int cu_count, double* timings_ms, psx_matrix** out) {
-  psx_build_options options{cu_count, PSX_ORDER_AUTO, 0, PSX_TASK_AUTO, 0, 0, 0};
+  psx_build_options options{cu_count, PSX_ORDER_AUTO, 0, PSX_TASK_AUTO, 0, 0, 0, 0, 0, 0};
   return psx_matrix_create_ex(rows, cols, nnz, row_ptr, col_ind, sp_data, &options, timings_ms,
                               out);
 }
@@ -79,6 +79,10 @@ int psx_matrix_create_ex(int rows, int cols, int nnz, const int* row_ptr, const 
       policy.max_group_types = options->max_group_types;
       policy.spmm_partition = options->parity_spmm ? PowerSparse::SpmmPartition::kParity
                                                    : PowerSparse::SpmmPartition::kTuned;
+      policy.hub_block = options->no_hub_block ? PowerSparse::HubBlock::kOff
+                                               : PowerSparse::HubBlock::kAuto;
+      policy.hub_min_degree = options->hub_min_degree;
+      policy.hub_min_count = options->hub_min_count;
     }
     PowerSparse::PreprocessTimings t;
     auto* m = new PowerSparse::PowerSparseMatrixGPU(rows, cols, nnz, row_ptr, col_ind, sp_data,
@@ -120,6 +124,14 @@ int psx_matrix_spmm_worksets(const psx_matrix* m, int* group_type_num) {
   return Guard([&] {
     Need(m && m->m && group_type_num, "psx_matrix_spmm_worksets: null argument");
     *group_type_num = m->m->SpmmMatrix().GroupTypeNum();
+  });
+}
+
+int psx_matrix_hub_block(const psx_matrix* m, int* rows, int* cols) {
+  return Guard([&] {
+    Need(m && m->m, "psx_matrix_hub_block: null matrix");
+    if (rows) *rows = m->m->HubRows();
+    if (cols) *cols = m->m->HubCols();
   });
 }
 

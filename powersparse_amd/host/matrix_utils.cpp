@@ -15,6 +15,8 @@
 #include <algorithm>
 #include <chrono>
 #include <future>
+#include <memory>
+#include <mutex>
 #include <cmath>
 #include <cstring>
 #include <numeric>
@@ -243,12 +245,21 @@ struct PowerSparseMatrixGPU::Prepared {
   Prepared(int rows, int cols, int nnz, const int* host_row_ptr, const int* host_col_ind,
            const float* host_sp_data, PreprocessTimings* timings)
       : clock(timings), row_ptr(size_t(rows) + 1), col_ind(size_t(nnz)), sp_data(size_t(nnz)) {
-    ps_stream_t st = nullptr;
     StagedUpload(row_ptr.data(), host_row_ptr, sizeof(int) * (size_t(rows) + 1));
     StagedUpload(col_ind.data(), host_col_ind, sizeof(int) * size_t(nnz));
     StagedUpload(sp_data.data(), host_sp_data, sizeof(float) * size_t(nnz));
     clock.Mark(&PreprocessTimings::upload_ms);
+    Analyze(rows, cols, nnz);
+  }
+  // From a CSR already on the device (stage times not recorded).
+  Prepared(int rows, int cols, int nnz, DeviceArray<int>&& rp, DeviceArray<int>&& ci,
+           DeviceArray<float>&& sv)
+      : clock(nullptr), row_ptr(std::move(rp)), col_ind(std::move(ci)), sp_data(std::move(sv)) {
+    Analyze(rows, cols, nnz);
+  }
 
+  void Analyze(int rows, int cols, int nnz) {
+    ps_stream_t st = nullptr;
     // Degree sums (AnalyzeMatrix) and the column histogram.
     ThrowOnError(ps_pre_degree_sums(row_ptr.data(), rows, degree_sums, st));
     col_nnz.Allocate(size_t(cols));
@@ -355,7 +366,11 @@ PowerSparseMatrixGPU::PowerSparseMatrixGPU(int row_num, int col_num, int nnz_num
     const bool may_tune =
         policy.spmm_partition == SpmmPartition::kTuned && _task_order != TaskOrder::kRow;
     Build(row_ptr, in, !may_tune);
-    if (may_tune && _task_order == TaskOrder::kSignature &&
+    bool hub = false;
+    if (may_tune && _task_order == TaskOrder::kSignature && _want_run_order &&
+        policy.hub_block == HubBlock::kAuto)
+      hub = BuildHub(row_ptr, in, policy);
+    if (!hub && may_tune && _task_order == TaskOrder::kSignature &&
         _group_type_num > kTunedSpmmGroupTypes) {
       PartitionPolicy tuned;
       tuned.cu_count = _cu_count;
@@ -629,6 +644,260 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, Prepared& in, bool last_par
   clock.Mark(&PreprocessTimings::gather_ms);
 }
 
+// ------------------------------------------------------------ hub block
+
+struct PowerSparseMatrixGPU::HubState {
+  ps_hub_block desc{};
+  DeviceArray<int> hub_rows, hub_index, hot_cols, hot_rank;
+  DeviceArray<float> dense;
+  DeviceArray<uint32_t> stored;
+  // per public workset: the 64-nonzero tiles of its groups inside the block
+  // (SDDMM writes them from the dense product)
+  std::vector<DeviceArray<uint32_t>> tiles;
+  std::vector<uint32_t> tile_count;
+  std::vector<const uint32_t*> tile_ptr;
+  // the operator workspace: one call at a time, in GPU order (`done` is
+  // recorded after each call's hub kernels, the next call waits for it)
+  std::mutex mu;
+  DeviceArray<char> ws;
+  ps_event_t done = nullptr;
+  bool recorded = false;
+  ~HubState() {
+    if (done) ps_event_destroy(done);
+  }
+};
+
+int PowerSparseMatrixGPU::HubRows() const { return _hub ? _hub->desc.rows : 0; }
+int PowerSparseMatrixGPU::HubCols() const { return _hub ? _hub->desc.cols : 0; }
+
+namespace {
+int FloorLog2(long long v) {
+  int b = -1;
+  while (v > 0) {
+    v >>= 1;
+    ++b;
+  }
+  return b;
+}
+}  // namespace
+
+bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
+                                    const PartitionPolicy& policy) {
+  const int rows = _matrix_row, cols = _matrix_col, S = _group_type_num;
+  if (S < 2) return false;  // fine mode: its store rule differs from a capped partition's
+  const std::vector<int>& cnt = in.col_nnz_host;
+  // rows of degree >= 2^a, columns of count >= 2^b
+  std::vector<long long> rows_ge(33, 0), cols_ge(33, 0);
+  for (int r = 0; r < rows; ++r) {
+    const int d = row_ptr[r + 1] - row_ptr[r];
+    if (d > 0) ++rows_ge[size_t(FloorLog2(d))];
+  }
+  for (int c = 0; c < cols; ++c)
+    if (cnt[size_t(c)] > 0) ++cols_ge[size_t(FloorLog2(cnt[size_t(c)]))];
+  for (int k = 31; k >= 0; --k) {
+    rows_ge[size_t(k)] += rows_ge[size_t(k) + 1];
+    cols_ge[size_t(k)] += cols_ge[size_t(k) + 1];
+  }
+  long long min_degree = policy.hub_min_degree, min_count = policy.hub_min_count;
+  const bool forced = min_degree > 0 && min_count > 0;
+  if (!forced) {
+    // nonzeros of rows of degree >= 2^a (a >= 8) in columns of count >= 2^b
+    DeviceArray<unsigned long long> hist(32 * 32);
+    ThrowOnError(ps_hub_histogram(in.row_ptr.data(), rows, in.col_ind.data(), in.col_nnz.data(),
+                                  hist.data(), nullptr));
+    std::vector<unsigned long long> h(32 * 32);
+    hist.Download(h.data(), h.size());
+    std::vector<double> ge(33 * 33, 0.0);
+    for (int a = 31; a >= 0; --a)
+      for (int b = 31; b >= 0; --b)
+        ge[size_t(a) * 33 + size_t(b)] = double(h[size_t(a) * 32 + size_t(b)]) +
+                                         ge[size_t(a + 1) * 33 + size_t(b)] +
+                                         ge[size_t(a) * 33 + size_t(b + 1)] -
+                                         ge[size_t(a + 1) * 33 + size_t(b + 1)];
+    double best = 0.0;
+    for (int a = 8; a < 31; ++a)
+      for (int b = 0; b < 31; ++b) {
+        const long long R = rows_ge[size_t(a)], H = cols_ge[size_t(b)];
+        if (R < kHubMinRows || H < kHubMinCols || R * H > kHubMaxElements) continue;
+        const double gain = ge[size_t(a) * 33 + size_t(b)] - kHubDenseCost * double(R) * double(H);
+        if (gain > best) {
+          best = gain;
+          min_degree = 1LL << a;
+          min_count = 1LL << b;
+        }
+      }
+    if (best < kHubMinGain * double(_matrix_nnz)) return false;
+  }
+
+  auto hub = std::make_unique<HubState>();
+  std::vector<int> hub_rows, hub_index(size_t(rows), -1), hot_cols, hot_rank(size_t(cols), -1);
+  for (int r = 0; r < rows; ++r)
+    if (row_ptr[r + 1] - row_ptr[r] >= min_degree) {
+      hub_index[size_t(r)] = int(hub_rows.size());
+      hub_rows.push_back(r);
+    }
+  for (int c = 0; c < cols; ++c)
+    if (cnt[size_t(c)] >= min_count) {
+      hot_rank[size_t(c)] = int(hot_cols.size());
+      hot_cols.push_back(c);
+    }
+  const long long R = (long long)hub_rows.size(), H = (long long)hot_cols.size();
+  if (R == 0 || H == 0) return false;
+  if (R * H > kHubMaxElements) {
+    if (forced)
+      throw std::invalid_argument("PartitionPolicy hub thresholds give a dense block over " +
+                                  std::to_string(kHubMaxElements) + " elements");
+    return false;
+  }
+  hub->hub_rows.Allocate(size_t(R));
+  hub->hub_rows.Upload(hub_rows.data(), size_t(R));
+  hub->hub_index.Allocate(size_t(rows));
+  hub->hub_index.Upload(hub_index.data(), size_t(rows));
+  hub->hot_cols.Allocate(size_t(H));
+  hub->hot_cols.Upload(hot_cols.data(), size_t(H));
+  hub->hot_rank.Allocate(size_t(cols));
+  hub->hot_rank.Upload(hot_rank.data(), size_t(cols));
+  ps_hub_block& d = hub->desc;
+  d.matrix_rows = rows;
+  d.matrix_cols = cols;
+  d.rows = int(R);
+  d.cols = int(H);
+  d.hub_rows = hub->hub_rows.data();
+  d.hub_index = hub->hub_index.data();
+  d.hot_cols = hub->hot_cols.data();
+  d.hot_rank = hub->hot_rank.data();
+  hub->dense.Allocate(size_t(R) * size_t(H));
+  hub->stored.Allocate(ps_hub_stored_words(&d));
+  d.dense = hub->dense.data();
+  d.stored = hub->stored.data();
+  ThrowOnError(ps_hub_dense_build(&d, in.row_ptr.data(), in.col_ind.data(), in.sp_data.data(),
+                                  hub->dense.data(), hub->stored.data(), nullptr));
+
+  // SpMM: a tuned partition of the matrix without the block.
+  DeviceArray<uint32_t> kept(size_t(rows) + 1);
+  ThrowOnError(ps_memset_async(kept.data() + rows, 0, sizeof(uint32_t), nullptr));
+  ThrowOnError(ps_hub_kept_counts(&d, in.row_ptr.data(), in.col_ind.data(), kept.data(), nullptr));
+  DeviceArray<int> rp(size_t(rows) + 1);
+  {
+    DeviceArray<char> scan_ws(ps_scan_workspace_bytes(size_t(rows) + 1));
+    ThrowOnError(ps_exclusive_scan_u32(kept.data(), reinterpret_cast<uint32_t*>(rp.data()),
+                                       size_t(rows) + 1, scan_ws.data(), nullptr));
+  }
+  std::vector<int> rp_host(size_t(rows) + 1);
+  rp.Download(rp_host.data(), rp_host.size());
+  const int nnz_rest = rp_host[size_t(rows)];
+  if (nnz_rest <= 0) return false;  // the block would hold every nonzero
+  DeviceArray<int> ci{static_cast<size_t>(nnz_rest)};
+  DeviceArray<float> sv{static_cast<size_t>(nnz_rest)};
+  ThrowOnError(ps_hub_compact(&d, in.row_ptr.data(), in.col_ind.data(), in.sp_data.data(),
+                              reinterpret_cast<const uint32_t*>(rp.data()), ci.data(), sv.data(),
+                              nullptr));
+  Prepared rest(rows, cols, nnz_rest, std::move(rp), std::move(ci), std::move(sv));
+  // the rest must keep the public partition's store rule: more than one workset
+  if (std::min(WorksetCount(rest.degree_sums, _cu_count), kTunedSpmmGroupTypes) < 2) return false;
+  PartitionPolicy tuned;
+  tuned.cu_count = _cu_count;
+  tuned.task_order = TaskOrder::kSignature;
+  tuned.run_order = false;
+  tuned.max_group_types = kTunedSpmmGroupTypes;
+  tuned.spmm_partition = SpmmPartition::kParity;
+  tuned.hub_block = HubBlock::kOff;
+  std::unique_ptr<PowerSparseMatrixGPU> part(
+      new PowerSparseMatrixGPU(Unbuilt{}, rows, cols, nnz_rest, _cu_count, tuned));
+  part->Build(rp_host.data(), rest, true);
+  // hub rows add their remaining entries to the block's product
+  ThrowOnError(ps_hub_mark_atomic(&d, part->_group_des[0], part->_group_num[0],
+                                  reinterpret_cast<uint8_t*>(part->_residue_atomic), nullptr));
+
+  // SDDMM: the groups inside the block leave the run order; their outputs come
+  // from the dense product.
+  std::vector<ps_workset> ws = PublicWorksets();
+  std::vector<DeviceArray<uint8_t>> flags(static_cast<size_t>(S));
+  std::vector<const uint8_t*> flag_ptr(static_cast<size_t>(S), nullptr);
+  hub->tiles.resize(size_t(S));
+  hub->tile_count.assign(size_t(S), 0);
+  hub->tile_ptr.assign(size_t(S), nullptr);
+  for (int s = 1; s < S; ++s) {
+    const int G = _group_num[s], GS = GROUP_SIZE(s);
+    if (G == 0 || GS < 64) continue;
+    flags[size_t(s)].Allocate(size_t(G));
+    ThrowOnError(ps_hub_group_flags(&d, &ws[size_t(s)], flags[size_t(s)].data(), nullptr));
+    std::vector<uint8_t> f(static_cast<size_t>(G));
+    flags[size_t(s)].Download(f.data(), f.size());
+    std::vector<uint32_t> t;
+    for (int g = 0; g < G; ++g)
+      if (f[size_t(g)])
+        for (int j = 0; j < GS / 64; ++j) t.push_back(uint32_t(g) * uint32_t(GS / 64) + uint32_t(j));
+    if (t.empty()) continue;
+    hub->tiles[size_t(s)].Allocate(t.size());
+    hub->tiles[size_t(s)].Upload(t.data(), t.size());
+    hub->tile_count[size_t(s)] = uint32_t(t.size());
+    hub->tile_ptr[size_t(s)] = hub->tiles[size_t(s)].data();
+    flag_ptr[size_t(s)] = flags[size_t(s)].data();
+  }
+  const int k = RunOrderSlot(PS_OP_SDDMM, 32);
+  uint32_t count = 0, kept_tasks = 0;
+  ThrowOnError(ps_task_count(PS_OP_SDDMM, 32, S, ws.data(), &count));
+  uint32_t* order = nullptr;
+  if (count > 0) {
+    ThrowOnError(ps_malloc(reinterpret_cast<void**>(&order), sizeof(uint32_t) * count));
+    const int rc = ps_task_order_build_subset(PS_OP_SDDMM, 32, S, ws.data(), flag_ptr.data(),
+                                              order, count, &kept_tasks, nullptr);
+    if (rc != PS_OK) {
+      ps_free(order);
+      ThrowOnError(rc);
+    }
+  }
+  ThrowOnError(ps_event_create(&hub->done));
+  ps_free(_run_order[k]);
+  _run_order[k] = order;
+  _run_order_tasks[k] = kept_tasks;
+  _spmm_tuned = part.release();
+  _hub = hub.release();
+  return true;
+}
+
+void PowerSparseMatrixGPU::HubSpmm(int N, const float* B, float* C, ps_stream_t stream) const {
+  HubState& h = *_hub;
+  std::lock_guard<std::mutex> lock(h.mu);
+  const size_t need = ps_hub_workspace_bytes(&h.desc, PS_OP_SPMM, N);
+  if (h.ws.size() < need) h.ws.Allocate(need);  // synchronises the device first
+  if (h.recorded) ThrowOnError(ps_stream_wait_event(stream, h.done));
+  ThrowOnError(ps_hub_spmm_launch(&h.desc, N, B, C, h.ws.data(), h.ws.size(), stream));
+  ThrowOnError(ps_event_record(h.done, stream));
+  h.recorded = true;
+}
+
+void PowerSparseMatrixGPU::HubSddmm(int N, const float* lhs, const float* rhs, float* const* out,
+                                    float* csr_out, ps_stream_t stream) const {
+  HubState& h = *_hub;
+  const std::vector<ps_workset> ws = PublicWorksets();
+  std::lock_guard<std::mutex> lock(h.mu);
+  const size_t need = ps_hub_workspace_bytes(&h.desc, PS_OP_SDDMM, N);
+  if (h.ws.size() < need) h.ws.Allocate(need);
+  if (h.recorded) ThrowOnError(ps_stream_wait_event(stream, h.done));
+  ThrowOnError(ps_hub_sddmm_launch(&h.desc, _group_type_num, ws.data(), h.tile_ptr.data(),
+                                   h.tile_count.data(), N, lhs, rhs, out,
+                                   csr_out ? _workset_csr_pos : nullptr, csr_out, h.ws.data(),
+                                   h.ws.size(), stream));
+  ThrowOnError(ps_event_record(h.done, stream));
+  h.recorded = true;
+}
+
+std::vector<ps_workset> PowerSparseMatrixGPU::PublicWorksets() const {
+  const int S = _group_type_num;
+  std::vector<ps_workset> ws(static_cast<size_t>(S));
+  for (int s = 0; s < S; ++s) {
+    ws[size_t(s)].col_ind = _workset_col_ind[s];
+    ws[size_t(s)].sp_data = _workset_sp_data[s];
+    ws[size_t(s)].group_des = _group_des[s];
+    ws[size_t(s)].group_num = _group_num[s];
+    ws[size_t(s)].group_size = s == 0 ? 0 : GROUP_SIZE(s);
+    ws[size_t(s)].order = nullptr;
+  }
+  return ws;
+}
+
 // The locality run order of each operator's fused launch over the public
 // (signature-ordered) worksets; see PartitionPolicy::run_order.
 void PowerSparseMatrixGPU::BuildRunOrders() {
@@ -708,6 +977,8 @@ void PowerSparseMatrixGPU::ReleaseExecution() noexcept {
 
 void PowerSparseMatrixGPU::Release() noexcept {
   ReleaseExecution();
+  delete _hub;
+  _hub = nullptr;
   delete _spmm_tuned;
   _spmm_tuned = nullptr;
   for (int k = 0; k < 3; ++k) {

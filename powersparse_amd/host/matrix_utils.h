@@ -13,6 +13,7 @@
 #include <cstdint>
 #include <limits>
 #include <stdexcept>
+#include <vector>
 
 #include "powersparse_hip.h"
 
@@ -68,6 +69,30 @@ enum class TaskOrder { kAuto = 0, kSignature = 1, kRow = 2 };
 // worksets.
 enum class SpmmPartition { kParity = 0, kTuned = 1 };
 constexpr int kTunedSpmmGroupTypes = 3;
+
+// Dense hub block. On power-law graphs the rows of highest degree hold a dense
+// core with the most popular columns (C3: rows of degree >= 4096 x columns
+// with >= 2048 nonzeros, 54 M of the 264 M nonzeros at 43% density). kAuto
+// keeps that block as a dense FP32 matrix and runs it as dense products on
+// the matrix cores (ps_hub_spmm_launch / ps_hub_sddmm_launch), the rest as
+// before: SpMM on a tuned partition of the matrix without the block, SDDMM on
+// the public worksets with the block's groups left out of the run order and
+// their outputs written from the dense product. The block is the pair of
+// power-of-two thresholds (row degree >= 2^a, column count >= 2^b) that
+// maximises block nonzeros - kHubDenseCost * rows * columns, kept when that
+// gain is at least kHubMinGain of the nonzeros (kHubDenseCost: the dense
+// element's cost relative to the sparse nonzero it replaces, measured on
+// MI355X). It is used with the tuned SpMM partition and the locality run
+// order only. Results match the sparse path within FP32 summation order;
+// Inf / NaN in B reach exactly the rows that store their column; rows of the
+// block accumulate into C as the reference's do (they hold more than 32
+// nonzeros). Cost: 4 bytes per block element (dense) plus the tuned
+// partition's own preprocessing (it no longer shares the public one's), and
+// an operator workspace grown on first use (SDDMM: 4 bytes per block element).
+enum class HubBlock { kAuto = 0, kOff = 1 };
+constexpr double kHubDenseCost = 0.12, kHubMinGain = 0.05;
+constexpr int kHubMinRows = 256, kHubMinCols = 1024;
+constexpr long long kHubMaxElements = 1LL << 29;
 constexpr double kRowOrderGain = 0.85;
 // Workgroup -> XCD runs (ps_spmm_launch's task_chunk) per task order: in a
 // row-ordered copy neighbouring groups share columns, so runs of 64 tasks stay
@@ -124,6 +149,12 @@ struct PartitionPolicy {
   // a capped partition is not the reference's when its rule gives more.
   int max_group_types = 0;
   SpmmPartition spmm_partition = SpmmPartition::kTuned;
+  HubBlock hub_block = HubBlock::kAuto;
+  // Explicit block thresholds (both > 0): rows of degree >= hub_min_degree,
+  // columns with >= hub_min_count nonzeros, whatever the cost rule says (the
+  // block is still dropped when it would hold every nonzero, or when the
+  // matrix has a single workset).
+  int hub_min_degree = 0, hub_min_count = 0;
 };
 
 // Wall-clock milliseconds of the preprocessing stages (host timer, the stream
@@ -182,11 +213,23 @@ class PowerSparseMatrixGPU {
   const PowerSparseMatrixGPU& SpmmMatrix() const { return _spmm_tuned ? *_spmm_tuned : *this; }
   // What the operators launch on.
   ExecutionLayout Execution() const;
+  // The dense hub block in use (HubBlock), as rows x columns; 0 x 0 when none.
+  bool HubBlockUsed() const { return _hub != nullptr; }
+  int HubRows() const;
+  int HubCols() const;
+  // The hub block's part of an operator call, enqueued on `stream` after the
+  // sparse part (SpMM: C += block * B; SDDMM: the block groups' outputs, into
+  // out[s] or, with csr_out, into csr_out at the CSR positions). Calls on one
+  // matrix share its operator workspace and run one after another on the GPU.
+  void HubSpmm(int N, const float* B, float* C, ps_stream_t stream) const;
+  void HubSddmm(int N, const float* lhs, const float* rhs, float* const* out, float* csr_out,
+                ps_stream_t stream) const;
 
  private:
   // The stages that do not depend on the partition (upload, column counts,
   // signature bits, per-row ranking), shared by the partitions of one matrix.
   struct Prepared;
+  struct HubState;
   struct Unbuilt {};
   // A partition of the same matrix whose Build() the caller runs.
   PowerSparseMatrixGPU(Unbuilt, int row_num, int col_num, int nnz_num, int cu_count,
@@ -199,6 +242,10 @@ class PowerSparseMatrixGPU {
   void Release() noexcept;
   void ReleaseExecution() noexcept;
   void BuildRunOrders();
+  // Chooses and builds the dense hub block and the tuned SpMM partition of
+  // the rest; false (nothing built) when no block qualifies.
+  bool BuildHub(const int* row_ptr, Prepared& in, const PartitionPolicy& policy);
+  std::vector<ps_workset> PublicWorksets() const;
 
   int _matrix_row, _matrix_col, _matrix_nnz;
   int _group_type_num = 0, _group_fine_size = 16;
@@ -229,6 +276,7 @@ class PowerSparseMatrixGPU {
   uint32_t _run_order_tasks[3] = {0, 0, 0};
   int _max_group_types = 0;
   PowerSparseMatrixGPU* _spmm_tuned = nullptr;  // SpmmPartition::kTuned
+  HubState* _hub = nullptr;                      // HubBlock
 };
 
 // The kernels use signed 32-bit dense element offsets (matrix_utils.h:71-76).

@@ -93,6 +93,8 @@ void SpMMAsync(const PowerSparseMatrixGPU& matrix, int N, const float* B, float*
     ThrowOnError(ps_spmm_launch(m.GroupTypeNum(), ws.data(), e.residue_offset,
                                 reinterpret_cast<const uint8_t*>(e.residue_atomic),
                                 m.MatrixRow(), m.MatrixCol(), N, B, C, e.task_chunk, stream));
+  // the dense hub block's rows (the tuned partition holds the rest)
+  if (matrix.HubBlockUsed()) matrix.HubSpmm(N, B, C, stream);
 }
 
 void SpMM(const PowerSparseMatrixGPU& m, int N, const float* B, float* C, int stream_count,
@@ -129,6 +131,8 @@ void SDDMMAsync(const PowerSparseMatrixGPU& m, int N, const float* lhs, const fl
   else
     ThrowOnError(ps_sddmm_launch(m.GroupTypeNum(), ws.data(), e.residue_offset, m.MatrixRow(),
                                  m.MatrixCol(), N, lhs, rhs, out, e.task_chunk, stream));
+  // the groups inside the dense hub block (left out of the run order)
+  if (m.HubBlockUsed()) m.HubSddmm(N, lhs, rhs, out, nullptr, stream);
 }
 
 void SDDMMToCSR(const PowerSparseMatrixGPU& m, int N, const float* lhs, const float* rhs,
@@ -149,6 +153,7 @@ void SDDMMToCSR(const PowerSparseMatrixGPU& m, int N, const float* lhs, const fl
     ThrowOnError(ps_sddmm_csr_launch(m.GroupTypeNum(), ws.data(), e.residue_offset, e.csr_pos,
                                      m.MatrixRow(), m.MatrixCol(), N, lhs, rhs, out_csr,
                                      e.task_chunk, stream));
+  if (m.HubBlockUsed()) m.HubSddmm(N, lhs, rhs, nullptr, out_csr, stream);
 }
 
 void WorksetToCSR(const PowerSparseMatrixGPU& m, const float* const* values, float* out_csr,

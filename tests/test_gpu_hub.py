@@ -1,0 +1,215 @@
+"""The dense hub block (PartitionPolicy::hub_block) on the GPU.
+
+A matrix built with a hub block runs the block's rows x hot columns as dense
+products and the rest on the sparse paths; the results must equal those of
+the same matrix without the block. On the golden fixtures' exact inputs
+(sparse values k/64, dense values k/16: every FP32 partial sum exact) the
+comparison is bit for bit, for SpMM over repeated calls (the block's rows
+accumulate), SDDMM in workset and CSR order, and SpMM with Inf / NaN in B."""
+import numpy as np
+import pytest
+
+import golden_data as gd
+import oracle
+import powersparse_amd as ps
+import tolerance
+from gpu_util import say, setup
+
+pytestmark = pytest.mark.gpu
+
+
+def csr_of(g):
+    return ps.HostCsr(g.rows, g.cols, g.row_ptr, g.col_ind, g.values)
+
+
+def thresholds(csr, cu, shares=((0.25, 0.5), (0.25, 0.3), (0.1, 0.3), (0.1, 0.15))):
+    """Explicit block thresholds: the heaviest rows (a share of the rows with 64+
+    nonzeros) and the columns whose count reaches a share of the hub rows'
+    entries, the first pair for which the matrix without the block still has
+    more than one workset at `cu` CUs (the build drops the block otherwise)."""
+    deg = np.diff(csr.row_ptr.astype(np.int64))
+    heavy = np.sort(deg[deg >= 64])[::-1]
+    assert heavy.size, "no heavy rows"
+    cnt = np.bincount(csr.col_ind, minlength=csr.cols)
+    rowof = np.repeat(np.arange(csr.rows), deg)
+    cu = cu or 256
+    for hub_share, hot_share in shares:
+        min_degree = int(heavy[max(0, int(heavy.size * hub_share) - 1)])
+        hub_cnt = np.sort(cnt[csr.col_ind[deg[rowof] >= min_degree]])
+        min_count = max(int(hub_cnt[int(hub_cnt.size * (1 - hot_share))]), 1)
+        block = (deg[rowof] >= min_degree) & (cnt[csr.col_ind] >= min_count)
+        rest = np.bincount(rowof[~block], minlength=csr.rows)
+        rp = np.concatenate([[0], np.cumsum(rest)]).astype(np.int32)
+        if rp[-1] > 0 and oracle.analyze_group_type_num(rp, cu) >= 2:
+            return min_degree, min_count
+    raise AssertionError("no block keeps two worksets in the rest")
+
+
+def run_ops(m, g, N, B, X, Y, calls=1):
+    S = m.GroupTypeNum()
+    streams = [ps.Stream() for _ in range(S)] if S > 1 else None
+    dB = ps.DeviceBuffer(host=B)
+    dC = ps.DeviceBuffer.zeros(g.rows * N * 4)
+    for _ in range(calls):
+        ps.SpMM(m, N, dB, dC, S, streams)
+    ps.synchronize()
+    C = dC.download(np.float32).reshape(g.rows, N)
+    dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
+    sizes = m.sddmm_output_sizes()
+    outs = [ps.DeviceBuffer.zeros(max(n, 1) * 4) for n in sizes]
+    ps.SDDMM(m, N, dX, dY, outs, S, streams)
+    ps.synchronize()
+    W = [outs[s].download(np.float32, sizes[s]) for s in range(S)]
+    csr_out = ps.DeviceBuffer(max(g.nnz, 1) * 4)
+    ps.SDDMMToCSR(m, N, dX, dY, csr_out)
+    ps.synchronize()
+    return C, W, csr_out.download(np.float32, g.nnz)
+
+
+@pytest.mark.parametrize("name", ["hubs", "skewed", "duplicates"])
+def test_hub_block_exact_on_golden(name):
+    setup()
+    g = gd.load(name)
+    p = g.parts[0]
+    csr = csr_of(g)
+    min_degree, min_count = thresholds(csr, p.cu)
+    kw = dict(cu_count=p.cu, csr_positions=True)
+    on = ps.PowerSparseMatrixGPU.from_csr(csr, hub_min_degree=min_degree,
+                                          hub_min_count=min_count, **kw)
+    off = ps.PowerSparseMatrixGPU.from_csr(csr, hub_block="off", **kw)
+    say(f"golden {name}: hub block {on.hub_block} (degree >= {min_degree}, count >= "
+        f"{min_count}), S={on.GroupTypeNum()}, SpMM worksets {on.spmm_worksets}")
+    assert on.hub_block[0] > 0 and on.hub_block[1] > 0, "the block was not built"
+    assert off.hub_block == (0, 0)
+    # the public worksets are the reference's either way
+    assert on.GroupNum() == off.GroupNum() == p.group_num
+    for N in (32, 64, 128, 256):
+        B, X, Y = (gd.dense(g.cols, N, gd.SALT_B), gd.dense(g.rows, N, gd.SALT_X),
+                   gd.dense(g.cols, N, gd.SALT_Y))
+        for calls in (1, 2):
+            a = run_ops(on, g, N, B, X, Y, calls)
+            b = run_ops(off, g, N, B, X, Y, calls)
+            np.testing.assert_array_equal(a[0], b[0], err_msg=f"SpMM N={N} calls={calls}")
+            for s in range(on.GroupTypeNum()):
+                np.testing.assert_array_equal(a[1][s], b[1][s], err_msg=f"SDDMM N={N} ws {s}")
+            np.testing.assert_array_equal(a[2], b[2], err_msg=f"SDDMMToCSR N={N}")
+        if N == g.n:
+            np.testing.assert_array_equal(a[2], g.sddmm_csr)
+    on.close()
+    off.close()
+
+
+def test_hub_block_nonfinite_b():
+    """Inf and NaN in B rows of hot and cold columns reach exactly the rows
+    that store those columns, as without the block (0 * Inf never leaks into
+    rows that do not store the column)."""
+    setup()
+    g = gd.load("hubs")
+    csr = csr_of(g)
+    min_degree, min_count = thresholds(csr, 1)
+    on = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=1, hub_min_degree=min_degree,
+                                          hub_min_count=min_count, csr_positions=True)
+    off = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=1, hub_block="off", csr_positions=True)
+    assert on.hub_block[0] > 0
+    cnt = np.bincount(csr.col_ind, minlength=csr.cols)
+    hot = np.flatnonzero(cnt >= min_count)
+    cold = np.flatnonzero((cnt > 0) & (cnt < min_count))
+    N = 64
+    for pattern in range(3):
+        B = gd.dense(g.cols, N, gd.SALT_B).copy()
+        rng = np.random.default_rng(pattern)
+        for c in rng.choice(hot, 3, replace=False):
+            B[c, rng.integers(0, N, 4)] = [np.inf, -np.inf, np.nan, np.inf][: 4]
+        for c in rng.choice(cold, 2, replace=False):
+            B[c, rng.integers(0, N)] = np.inf
+        X = gd.dense(g.rows, N, gd.SALT_X)
+        Y = gd.dense(g.cols, N, gd.SALT_Y)
+        a = run_ops(on, g, N, B, X, Y)
+        b = run_ops(off, g, N, B, X, Y)
+        assert np.isnan(a[0]).any() and np.isinf(a[0]).any()
+        np.testing.assert_array_equal(np.isnan(a[0]), np.isnan(b[0]))
+        np.testing.assert_array_equal(a[0], b[0])
+    on.close()
+    off.close()
+
+
+@pytest.mark.parametrize("cfg,scale", [("C3", 40), ("C1", 20)])
+def test_hub_block_on_power_law_graphs(cfg, scale):
+    """Scaled power-law graphs with an explicit block against the oracle's
+    double-precision results (stated FP32 tolerance)."""
+    setup()
+    csr = ps.synth(cfg, seed=3, scale=scale)
+    min_degree, min_count = thresholds(csr, 0, shares=((0.5, 0.5), (0.25, 0.3)))
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, hub_min_degree=min_degree, hub_min_count=min_count)
+    say(f"{cfg}/{scale}: nnz={csr.nnz} hub block {m.hub_block} S={m.GroupTypeNum()}")
+    assert m.hub_block[0] > 0
+    rng = np.random.default_rng(5)
+    for N in (32, 128):
+        B = rng.uniform(-1, 1, (csr.cols, N)).astype(np.float32)
+        dB = ps.DeviceBuffer(host=B)
+        dC = ps.DeviceBuffer.zeros(csr.rows * N * 4)
+        S = m.GroupTypeNum()
+        ps.SpMM(m, N, dB, dC, S, [ps.Stream() for _ in range(S)] if S > 1 else None)
+        ps.synchronize()
+        E, M = oracle.spmm(csr.row_ptr, csr.col_ind, csr.values, N, B, with_mag=True)
+        say("  ", tolerance.check(dC.download(np.float32).reshape(csr.rows, N), E, M,
+                                  f"SpMM {cfg} N={N}"))
+    N = 128
+    X = rng.normal(size=(csr.rows, N)).astype(np.float32)
+    Y = rng.normal(size=(csr.cols, N)).astype(np.float32)
+    dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
+    sizes = m.sddmm_output_sizes()
+    outs = [ps.DeviceBuffer.zeros(max(n, 1) * 4) for n in sizes]
+    ps.SDDMMAsync(m, N, dX, dY, outs)
+    ps.synchronize()
+    offs0 = m.residue_offset()
+    for s in range(m.GroupTypeNum()):
+        if sizes[s] == 0:
+            continue
+        col, val, des = m.download_workset(s)
+        offs = offs0 if s == 0 else np.arange(m.GroupNum()[s] + 1) * ps.GROUP_SIZE(s)
+        E, Mg = oracle.sddmm(des, offs, col, val, N, X, Y, with_mag=True)
+        tolerance.check(outs[s].download(np.float32, sizes[s]), E, Mg, f"SDDMM {cfg} ws {s}")
+    m.close()
+
+
+def test_hub_block_concurrent_calls_and_memory():
+    """Calls on one matrix from two streams share its workspace in turn and
+    give the sequential results; constructions and their operator workspaces
+    are released."""
+    setup()
+    g = gd.load("hubs")
+    csr = csr_of(g)
+    min_degree, min_count = thresholds(csr, 1)
+    kw = dict(cu_count=1, hub_min_degree=min_degree, hub_min_count=min_count)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, **kw)
+    assert m.hub_block[0] > 0
+    N = 128
+    B1, B2 = gd.dense(g.cols, N, 11), gd.dense(g.cols, N, 12)
+    d1, d2 = ps.DeviceBuffer(host=B1), ps.DeviceBuffer(host=B2)
+    c1, c2 = ps.DeviceBuffer.zeros(g.rows * N * 4), ps.DeviceBuffer.zeros(g.rows * N * 4)
+    s1, s2 = ps.Stream(), ps.Stream()
+    for _ in range(3):
+        ps.SpMMAsync(m, N, d1, c1, s1)
+        ps.SpMMAsync(m, N, d2, c2, s2)
+    ps.synchronize()
+    row_of = np.repeat(np.arange(g.rows), np.diff(g.row_ptr))
+    for b, c in ((B1, c1), (B2, c2)):
+        want = np.zeros((g.rows, N))
+        np.add.at(want, row_of, g.values.astype(np.float64)[:, None] * b.astype(np.float64)[g.col_ind])
+        got = c.download(np.float32).reshape(g.rows, N)
+        # three calls: every row here accumulates except rows stored by the residue
+        stored = g.parts[0].des[0][g.parts[0].residue_atomic == 0]
+        want3 = 3 * want
+        want3[stored] = want[stored]
+        np.testing.assert_array_equal(got, want3)
+    m.close()
+    ps.synchronize()
+    free0, _ = ps.mem_get_info()  # the GEMM library is loaded by now
+    for _ in range(3):
+        m = ps.PowerSparseMatrixGPU.from_csr(csr, **kw)
+        ps.SpMMAsync(m, N, d1, c1)
+        m.close()
+    ps.synchronize()
+    free1, _ = ps.mem_get_info()
+    assert free1 >= free0 - (4 << 20), (free0, free1)
