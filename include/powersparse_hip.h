@@ -326,16 +326,22 @@ size_t ps_hub_workspace_bytes(const ps_hub_block* hb, int op, int N);
  * workspace race. */
 int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, void* workspace,
                        size_t workspace_bytes, ps_stream_t stream);
-/* For every listed tile (hot_tiles[s][0 .. hot_tile_count[s]), 64-nonzero tiles
- * of block workset s, groups >= 64 nonzeros, inside the block):
- * out[s][p] = sp_data[p] * dot(lhs[group_des[g], :], rhs[col_ind[p], :]) for
- * its 64 nonzeros p, computed as one dense product of the hub rows of lhs
- * with the hot rows of rhs; with out_csr, out_csr[out_pos[s][p]] instead. */
+/* The SDDMM tile list of a hub block: tiles[t] = (s << 27) | j names the j-th
+ * 64-nonzero tile of block workset s (groups >= 64 nonzeros, every entry
+ * inside the block). ps_hub_sort_tiles orders a list by hub row, then by the
+ * tile's first column (device memory; allocates temporaries and synchronises
+ * the stream). */
+int ps_hub_sort_tiles(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
+                      uint32_t* tiles, uint32_t tile_count, ps_stream_t stream);
+/* For every listed tile: out[s][p] = sp_data[p] * dot(lhs[group_des[g], :],
+ * rhs[col_ind[p], :]) for its 64 nonzeros p, computed as one dense product of
+ * the hub rows of lhs with the hot rows of rhs; with out_csr,
+ * out_csr[out_pos[s][p]] instead. */
 int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
-                        const uint32_t* const* hot_tiles, const uint32_t* hot_tile_count, int N,
-                        const float* lhs, const float* rhs, float* const* out,
-                        const int* const* out_pos, float* out_csr, void* workspace,
-                        size_t workspace_bytes, ps_stream_t stream);
+                        const uint32_t* tiles, uint32_t tile_count, int N, const float* lhs,
+                        const float* rhs, float* const* out, const int* const* out_pos,
+                        float* out_csr, void* workspace, size_t workspace_bytes,
+                        ps_stream_t stream);
 
 /* ---------------------------------------------------------- primitives */
 /* Device-wide exclusive prefix sum of n uint32 values (out may alias in).

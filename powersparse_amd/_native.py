@@ -168,9 +168,12 @@ HIP_API = [
     ("ps_hub_spmm_launch", ctypes.c_int,
      [ctypes.POINTER(HubBlock), ctypes.c_int, c_void_p, c_void_p, c_void_p, ctypes.c_size_t,
       c_void_p]),
+    ("ps_hub_sort_tiles", ctypes.c_int,
+     [ctypes.POINTER(HubBlock), ctypes.c_int, ctypes.POINTER(Workset), c_void_p,
+      ctypes.c_uint32, c_void_p]),
     ("ps_hub_sddmm_launch", ctypes.c_int,
-     [ctypes.POINTER(HubBlock), ctypes.c_int, ctypes.POINTER(Workset), ctypes.POINTER(c_void_p),
-      c_u32_p, ctypes.c_int, c_void_p, c_void_p, ctypes.POINTER(c_void_p),
+     [ctypes.POINTER(HubBlock), ctypes.c_int, ctypes.POINTER(Workset), c_void_p,
+      ctypes.c_uint32, ctypes.c_int, c_void_p, c_void_p, ctypes.POINTER(c_void_p),
       ctypes.POINTER(c_void_p), c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
     ("ps_spmm_launch_ordered", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,

@@ -336,35 +336,82 @@ __global__ __launch_bounds__(kThreads) void fixup_kernel(ps_hub_block hb, const 
   }
 }
 
+// A listed tile: (workset << kTileBits) | tile index within the workset.
+constexpr int kTileBits = 27;
+constexpr uint32_t kTileMask = (1u << kTileBits) - 1u;
+constexpr int kSampleChunkMax = 256;  // XCD runs of the sample kernel (workgroups)
+
 struct SampleArgs {
-  ps_workset ws[PS_MAX_WORKSETS];
-  const uint32_t* tiles[PS_MAX_WORKSETS];  // 64-nonzero tiles of hot groups
-  uint32_t tile_begin[PS_MAX_WORKSETS + 1];
+  ps_workset ws[PS_MAX_WORKSETS];  // indexed by workset
   float* out[PS_MAX_WORKSETS];
   const int* out_pos[PS_MAX_WORKSETS];
   float* out_csr;
-  int count;
+  const uint32_t* tiles;
+  uint32_t count;
+  uint32_t chunk_log2;
 };
 
 // out[s][p] (or out_csr[out_pos[s][p]]) = sp_data[p] * D[hub_index[row], hot_rank[col]]
-// for the 64 nonzeros p of every listed tile; one wave per tile.
+// for the 64 nonzeros p of every listed tile; one wave per kSampleTiles
+// consecutive tiles, each step's loads issued for all of them before any is
+// used (a tile alone leaves the wave waiting on a chain of dependent loads).
+// The list is sorted by hub row and first column, and consecutive workgroups
+// go to one XCD in runs, so each L2 reads a stretch of one D row.
+constexpr int kSampleTiles = 4;
 __global__ __launch_bounds__(kThreads) void sample_kernel(ps_hub_block hb, SampleArgs a,
                                                            const float* __restrict__ D) {
-  const int waves = kThreads / kWave;
-  const uint32_t total = a.tile_begin[a.count];
-  for (uint32_t t = blockIdx.x * waves + threadIdx.x / kWave; t < total;
-       t += gridDim.x * waves) {
-    int q = 0;
-    while (q + 1 < a.count && t >= a.tile_begin[q + 1]) ++q;
-    const ps_workset& w = a.ws[q];
-    const size_t p = size_t(a.tiles[q][t - a.tile_begin[q]]) * 64 + size_t(lane_id());
-    const int g = int(p / size_t(w.group_size));
-    const int i = hb.hub_index[w.group_des[g]];
-    const int h = hb.hot_rank[w.col_ind[p]];
-    if (i < 0 || h < 0) continue;  // not a block entry (never listed)
-    const float v = w.sp_data[p] * D[size_t(i) * size_t(hb.cols) + size_t(h)];
-    if (a.out_csr) a.out_csr[a.out_pos[q][p]] = v;
-    else a.out[q][p] = v;
+  const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, a.chunk_log2);
+  const uint32_t t0 = (blk * uint32_t(kThreads / kWave) + threadIdx.x / kWave) * kSampleTiles;
+  if (t0 >= a.count) return;
+  int q[kSampleTiles];
+  size_t p[kSampleTiles];
+  bool on[kSampleTiles];
+#pragma unroll
+  for (int k = 0; k < kSampleTiles; ++k) {
+    on[k] = t0 + k < a.count;
+    const uint32_t code = on[k] ? a.tiles[t0 + k] : 0u;
+    q[k] = int(code >> kTileBits);
+    p[k] = size_t(code & kTileMask) * 64 + size_t(lane_id());
+  }
+  int c[kSampleTiles], row[kSampleTiles];
+  float val[kSampleTiles];
+#pragma unroll
+  for (int k = 0; k < kSampleTiles; ++k) {
+    const ps_workset& w = a.ws[q[k]];
+    c[k] = on[k] ? w.col_ind[p[k]] : 0;
+    val[k] = on[k] ? w.sp_data[p[k]] : 0.f;
+    row[k] = on[k] ? w.group_des[int(p[k] / size_t(w.group_size))] : 0;
+  }
+  size_t at[kSampleTiles];
+#pragma unroll
+  for (int k = 0; k < kSampleTiles; ++k) {
+    const int i = on[k] ? hb.hub_index[row[k]] : -1;
+    const int h = on[k] ? hb.hot_rank[c[k]] : -1;
+    on[k] = on[k] && i >= 0 && h >= 0;  // listed tiles lie inside the block
+    at[k] = on[k] ? size_t(i) * size_t(hb.cols) + size_t(h) : 0;
+  }
+  float v[kSampleTiles];
+#pragma unroll
+  for (int k = 0; k < kSampleTiles; ++k) v[k] = on[k] ? val[k] * D[at[k]] : 0.f;
+#pragma unroll
+  for (int k = 0; k < kSampleTiles; ++k) {
+    if (!on[k]) continue;
+    if (a.out_csr) a.out_csr[a.out_pos[q[k]][p[k]]] = v[k];
+    else a.out[q[k]][p[k]] = v[k];
+  }
+}
+
+// keys[t] = (hub index of the tile's row << 32) | its first column; vals[t] = code.
+__global__ __launch_bounds__(kThreads) void tile_keys_kernel(ps_hub_block hb, SampleArgs a,
+                                                              uint64_t* __restrict__ keys,
+                                                              uint32_t* __restrict__ vals) {
+  for (uint32_t t = blockIdx.x * kThreads + threadIdx.x; t < a.count; t += gridDim.x * kThreads) {
+    const uint32_t code = a.tiles[t];
+    const ps_workset& w = a.ws[code >> kTileBits];
+    const size_t p = size_t(code & kTileMask) * 64;
+    const int i = hb.hub_index[w.group_des[int(p / size_t(w.group_size))]];
+    keys[t] = (uint64_t(uint32_t(i)) << 32) | uint32_t(w.col_ind[p]);
+    vals[t] = code;
   }
 }
 
@@ -519,48 +566,75 @@ int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, 
   return PS_OK;
 }
 
+// SampleArgs over the worksets and a tile list, checked.
+static int sample_args(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
+                const uint32_t* tiles, uint32_t tile_count, ps::SampleArgs* a) {
+  (void)hb;
+  PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets,
+               "hub block: invalid worksets");
+  PS_CHECK_ARG(tile_count == 0 || tiles, "hub block: missing tile list");
+  *a = ps::SampleArgs{};
+  for (int s = 0; s < workset_count; ++s) a->ws[s] = worksets[s];
+  a->tiles = tiles;
+  a->count = tile_count;
+  return PS_OK;
+}
+
+int ps_hub_sort_tiles(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
+                      uint32_t* tiles, uint32_t tile_count, ps_stream_t stream) {
+  int rc = ps::check_block(hb);
+  if (rc != PS_OK) return rc;
+  ps::SampleArgs a;
+  rc = sample_args(hb, workset_count, worksets, tiles, tile_count, &a);
+  if (rc != PS_OK) return rc;
+  if (tile_count == 0) return PS_OK;
+  const size_t n = tile_count;
+  const size_t bytes = 2 * ps::round256(n * 8) + ps::round256(n * 4) +
+                       ps::round256(ps_radix_workspace_bytes(n));
+  char* base = nullptr;
+  PS_HIP(hipMalloc(&base, bytes));
+  uint64_t* keys = reinterpret_cast<uint64_t*>(base);
+  uint64_t* keys_alt = reinterpret_cast<uint64_t*>(base + ps::round256(n * 8));
+  uint32_t* vals = reinterpret_cast<uint32_t*>(base + 2 * ps::round256(n * 8));
+  void* ws = base + 2 * ps::round256(n * 8) + ps::round256(n * 4);
+  hipStream_t st = ps::to_hip(stream);
+  ps::tile_keys_kernel<<<ps::grid_for(n, ps::kThreads), ps::kThreads, 0, st>>>(*hb, a, keys, vals);
+  hipError_t e = hipGetLastError();
+  int alt = 0, r = PS_OK;
+  if (e == hipSuccess)
+    r = ps_radix_sort_pairs_u64(keys, keys_alt, vals, tiles, n, 0, 64, ws, &alt, stream);
+  if (e == hipSuccess && r == PS_OK && !alt)
+    e = hipMemcpyAsync(tiles, vals, n * 4, hipMemcpyDeviceToDevice, st);
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  (void)hipFree(base);
+  if (r != PS_OK) return r;
+  PS_HIP(e);
+  return PS_OK;
+}
+
 int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
-                        const uint32_t* const* hot_tiles, const uint32_t* hot_tile_count, int N,
-                        const float* lhs, const float* rhs, float* const* out,
-                        const int* const* out_pos, float* out_csr, void* workspace,
-                        size_t workspace_bytes, ps_stream_t stream) {
-  const int rc = ps::check_block(hb);
+                        const uint32_t* tiles, uint32_t tile_count, int N, const float* lhs,
+                        const float* rhs, float* const* out, const int* const* out_pos,
+                        float* out_csr, void* workspace, size_t workspace_bytes,
+                        ps_stream_t stream) {
+  int rc = ps::check_block(hb);
   if (rc != PS_OK) return rc;
   PS_CHECK_ARG(N > 0 && N % 32 == 0 && N <= 512,
                "SDDMM requires N to be a multiple of 32 between 32 and 512");
   PS_CHECK_ARG(lhs && rhs && ps::aligned16(lhs) && ps::aligned16(rhs),
                "ps_hub_sddmm_launch: dense buffers must be 16-byte aligned");
-  PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets && hot_tiles &&
-                   hot_tile_count,
-               "ps_hub_sddmm_launch: invalid worksets");
   PS_CHECK_ARG(out_csr ? (out_pos != nullptr) : (out != nullptr),
                "ps_hub_sddmm_launch: missing outputs");
   PS_CHECK_ARG(workspace && workspace_bytes >= ps_hub_workspace_bytes(hb, PS_OP_SDDMM, N),
                "ps_hub_sddmm_launch: workspace too small");
-  ps::SampleArgs a{};
-  uint64_t total = 0;
-  int n = 0;
+  ps::SampleArgs a;
+  rc = sample_args(hb, workset_count, worksets, tiles, tile_count, &a);
+  if (rc != PS_OK) return rc;
+  if (tile_count == 0) return PS_OK;
   for (int s = 1; s < workset_count; ++s) {
-    if (!hot_tile_count[s]) continue;
-    const ps_workset& w = worksets[s];
-    PS_CHECK_ARG(w.group_size >= 64 && hot_tiles[s] && w.col_ind && w.sp_data && w.group_des,
-                 "ps_hub_sddmm_launch: listed tiles need a block workset of groups >= 64");
-    PS_CHECK_ARG(out_csr ? (out_pos[s] != nullptr) : (out[s] != nullptr),
-                 "ps_hub_sddmm_launch: missing output workset");
-    PS_CHECK_ARG(uint64_t(hot_tile_count[s]) * 64 <= uint64_t(w.group_num) * uint64_t(w.group_size),
-                 "ps_hub_sddmm_launch: more tiles than the workset holds");
-    a.ws[n] = w;
-    a.tiles[n] = hot_tiles[s];
-    a.out[n] = out ? out[s] : nullptr;
-    a.out_pos[n] = out_pos ? out_pos[s] : nullptr;
-    a.tile_begin[n] = uint32_t(total);
-    total += hot_tile_count[s];
-    ++n;
+    a.out[s] = out ? out[s] : nullptr;
+    a.out_pos[s] = out_pos ? out_pos[s] : nullptr;
   }
-  PS_CHECK_ARG(total < (1ull << 31), "ps_hub_sddmm_launch: too many tiles");
-  if (n == 0) return PS_OK;
-  a.tile_begin[n] = uint32_t(total);
-  a.count = n;
   a.out_csr = out_csr;
   const size_t R = size_t(hb->rows), H = size_t(hb->cols), k = size_t(N);
   char* w = static_cast<char*>(workspace);
@@ -579,8 +653,11 @@ int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_work
   int r = ps::gemm_f32(st, true, false, hb->cols, hb->rows, N, Yh, N, Xh, N, D, hb->cols, blas_ws,
                        ps::kBlasWorkspace);
   if (r != PS_OK) return r;
-  ps::sample_kernel<<<ps::grid_for(total, ps::kThreads / ps::kWave), ps::kThreads, 0, st>>>(*hb, a,
-                                                                                             D);
+  const uint64_t per_block = uint64_t(ps::kThreads / ps::kWave) * ps::kSampleTiles;
+  const uint64_t grid = (uint64_t(tile_count) + per_block - 1) / per_block;
+  PS_CHECK_ARG(grid < (1ull << 31), "ps_hub_sddmm_launch: too many tiles");
+  a.chunk_log2 = uint32_t(ps::task_chunk_log2(PS_TASK_CHUNK_AUTO, grid, ps::kSampleChunkMax));
+  ps::sample_kernel<<<unsigned(grid), ps::kThreads, 0, st>>>(*hb, a, D);
   PS_LAUNCHED();
   return PS_OK;
 }

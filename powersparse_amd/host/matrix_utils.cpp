@@ -651,11 +651,10 @@ struct PowerSparseMatrixGPU::HubState {
   DeviceArray<int> hub_rows, hub_index, hot_cols, hot_rank;
   DeviceArray<float> dense;
   DeviceArray<uint32_t> stored;
-  // per public workset: the 64-nonzero tiles of its groups inside the block
-  // (SDDMM writes them from the dense product)
-  std::vector<DeviceArray<uint32_t>> tiles;
-  std::vector<uint32_t> tile_count;
-  std::vector<const uint32_t*> tile_ptr;
+  // the 64-nonzero tiles of the public block groups inside the block, as
+  // (workset << 27) | tile, sorted by hub row and first column (SDDMM writes
+  // them from the dense product)
+  DeviceArray<uint32_t> tiles;
   // the operator workspace: one call at a time, in GPU order (`done` is
   // recorded after each call's hub kernels, the next call waits for it)
   std::mutex mu;
@@ -814,9 +813,7 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
   std::vector<ps_workset> ws = PublicWorksets();
   std::vector<DeviceArray<uint8_t>> flags(static_cast<size_t>(S));
   std::vector<const uint8_t*> flag_ptr(static_cast<size_t>(S), nullptr);
-  hub->tiles.resize(size_t(S));
-  hub->tile_count.assign(size_t(S), 0);
-  hub->tile_ptr.assign(size_t(S), nullptr);
+  std::vector<uint32_t> tiles;
   for (int s = 1; s < S; ++s) {
     const int G = _group_num[s], GS = GROUP_SIZE(s);
     if (G == 0 || GS < 64) continue;
@@ -824,16 +821,20 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
     ThrowOnError(ps_hub_group_flags(&d, &ws[size_t(s)], flags[size_t(s)].data(), nullptr));
     std::vector<uint8_t> f(static_cast<size_t>(G));
     flags[size_t(s)].Download(f.data(), f.size());
-    std::vector<uint32_t> t;
+    bool any = false;
     for (int g = 0; g < G; ++g)
-      if (f[size_t(g)])
-        for (int j = 0; j < GS / 64; ++j) t.push_back(uint32_t(g) * uint32_t(GS / 64) + uint32_t(j));
-    if (t.empty()) continue;
-    hub->tiles[size_t(s)].Allocate(t.size());
-    hub->tiles[size_t(s)].Upload(t.data(), t.size());
-    hub->tile_count[size_t(s)] = uint32_t(t.size());
-    hub->tile_ptr[size_t(s)] = hub->tiles[size_t(s)].data();
-    flag_ptr[size_t(s)] = flags[size_t(s)].data();
+      if (f[size_t(g)]) {
+        any = true;
+        for (int j = 0; j < GS / 64; ++j)
+          tiles.push_back((uint32_t(s) << 27) | (uint32_t(g) * uint32_t(GS / 64) + uint32_t(j)));
+      }
+    if (any) flag_ptr[size_t(s)] = flags[size_t(s)].data();
+  }
+  if (!tiles.empty()) {
+    hub->tiles.Allocate(tiles.size());
+    hub->tiles.Upload(tiles.data(), tiles.size());
+    ThrowOnError(ps_hub_sort_tiles(&d, S, ws.data(), hub->tiles.data(), uint32_t(tiles.size()),
+                                   nullptr));
   }
   const int k = RunOrderSlot(PS_OP_SDDMM, 32);
   uint32_t count = 0, kept_tasks = 0;
@@ -876,8 +877,8 @@ void PowerSparseMatrixGPU::HubSddmm(int N, const float* lhs, const float* rhs, f
   const size_t need = ps_hub_workspace_bytes(&h.desc, PS_OP_SDDMM, N);
   if (h.ws.size() < need) h.ws.Allocate(need);
   if (h.recorded) ThrowOnError(ps_stream_wait_event(stream, h.done));
-  ThrowOnError(ps_hub_sddmm_launch(&h.desc, _group_type_num, ws.data(), h.tile_ptr.data(),
-                                   h.tile_count.data(), N, lhs, rhs, out,
+  ThrowOnError(ps_hub_sddmm_launch(&h.desc, _group_type_num, ws.data(), h.tiles.data(),
+                                   uint32_t(h.tiles.size()), N, lhs, rhs, out,
                                    csr_out ? _workset_csr_pos : nullptr, csr_out, h.ws.data(),
                                    h.ws.size(), stream));
   ThrowOnError(ps_event_record(h.done, stream));

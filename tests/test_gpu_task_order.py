@@ -30,8 +30,10 @@ def sddmm_public(m, N, dX, dY, calls=1):
 def test_row_order_matches_signature_order(cfg, scale, cu, N):
     setup()
     csr = ps.synth(cfg, seed=31, scale=scale)
+    # without a dense hub block: its outputs come from a GEMM, whose summation
+    # order differs from the sparse kernels' (test_gpu_hub.py covers it)
     a = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=cu, task_order="signature",
-                                         csr_positions=True)
+                                         csr_positions=True, hub_block="off")
     b = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=cu, task_order="row",
                                          csr_positions=True)
     assert a.task_order == "signature" and b.task_order == "row"
@@ -75,7 +77,8 @@ def test_row_order_random(seed):
     csr = random_graph(rng, int(rng.integers(100, 500)), int(rng.integers(50, 3000)), 120,
                        hubs=3, hub_deg=int(rng.integers(300, 2500)), dup=(seed == 2))
     cu = int(rng.choice([1, 2, 64]))
-    a = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=cu, task_order="signature")
+    a = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=cu, task_order="signature",
+                                         hub_block="off")
     b = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=cu, task_order="row")
     N = 32
     X = rng.normal(size=(csr.rows, N)).astype(np.float32)
