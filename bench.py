@@ -14,15 +14,18 @@ between calls, as in the reference harness (benchmarks/benchmark.cu:179-187).
 
 Prints one JSON line: value = total FLOP of the timed steps (2 * nnz * N per
 operator, benchmark.cu:189) / wall time between two events, in GFLOPS; the
-`roofline` object is for the dominant kernel (algorithmic bytes per launch /
-its mean launch time, HIP events on its stream); `cpu_baseline` is the OpenMP
+`roofline` object is for the dominant operator (algorithmic bytes per call /
+its mean call time, HIP events around the call on its stream: the fused
+sparse launch, plus the dense hub block's kernels when the matrix keeps one,
+`config.hub_block` = its rows x columns); `cpu_baseline` is the OpenMP
 double-precision restatement of the reference's check path (the oracle) timed
 on this host over a bounded row sample of the same graph and operators.
-`roofline.traffic` is the bytes per launch the kernel's L2 exchanges with the
-memory fabric (Infinity Cache and HBM; calibrated FETCH_SIZE + WRITE_SIZE),
-taken from the committed rocprofv3 summary of the same workload when that
-summary was made from the current kernel sources (else null);
-`traffic_GBps` is that byte count over this run's launch time.
+`roofline.traffic` is the bytes per launch the operator's sparse kernel's L2
+exchanges with the memory fabric (Infinity Cache and HBM; calibrated
+FETCH_SIZE + WRITE_SIZE; the hub block's GEMM and sampling kernels are not
+counted), taken from the committed rocprofv3 summary of the same workload
+when that summary was made from the current kernel sources (else null);
+`traffic_GBps` is that byte count over this run's call time.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3]
 """
@@ -267,6 +270,7 @@ def main():
                                             f" N={o['N']}" for o in ops),
                    "graph": args.config, "rows": rows,
                    "nnz": nnz, "worksets": S, "group_num": m.GroupNum(),
+                   "hub_block": list(m.hub_block),
                    "preprocess_ms": preprocess_ms, "parallelism": "single GPU",
                    "device": (f"{props['name']} " if props["name"].strip() else "")
                              + f"({props['arch'].split(':')[0]}, {props['cu_count']} CUs)"},
@@ -278,7 +282,8 @@ def main():
                      # (Infinity Cache hits and HBM together), over this run's
                      # launch time
                      "traffic_scope": "L2 to memory fabric (Infinity Cache and HBM), "
-                                      "calibrated FETCH_SIZE + WRITE_SIZE",
+                                      "calibrated FETCH_SIZE + WRITE_SIZE, of the "
+                                      "operator's sparse kernel",
                      "traffic_GBps": traffic / (dom["ms"] * 1e-3) / 1e9 if traffic else None,
                      "l2_hit_pct": counters.get("l2_hit_pct"),
                      "valu_busy_pct": counters.get("valu_busy_pct"),
