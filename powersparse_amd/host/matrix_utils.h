@@ -209,7 +209,8 @@ class PowerSparseMatrixGPU {
   // Whether the operators run in the locality run order (see PartitionPolicy).
   bool RunOrderUsed() const { return _run_order[0] != nullptr || _run_order[2] != nullptr; }
   // The partition SpMM runs on: the tuned one (SpmmPartition::kTuned), or
-  // this matrix itself when none was built.
+  // this matrix itself when none was built. With a dense hub block it holds
+  // the matrix without the block (SpMM adds the block's product to it).
   const PowerSparseMatrixGPU& SpmmMatrix() const { return _spmm_tuned ? *_spmm_tuned : *this; }
   // What the operators launch on.
   ExecutionLayout Execution() const;
