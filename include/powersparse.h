@@ -46,6 +46,8 @@ int psx_matrix_create(int rows, int cols, int nnz, const int* row_ptr, const int
  * sorts of the groups x L/32 signature bitmaps) or PSX_ORDER_BIT_LISTS (sorted
  * bit lists, memory bounded by nnz). */
 enum { PSX_ORDER_AUTO = 0, PSX_ORDER_BITMAP_WORDS = 1, PSX_ORDER_BIT_LISTS = 2 };
+/* Tiers of the dense hub block (PowerSparse::kHubMaxTiers). */
+#define PSX_HUB_MAX_TIERS 3
 typedef struct psx_build_options {
   int cu_count;
   int signature_order;
@@ -55,8 +57,10 @@ typedef struct psx_build_options {
   int max_group_types; /* cap on the workset count S (0: none) */
   int parity_spmm;   /* nonzero: SpMM on the public worksets (SpmmPartition::kParity) */
   int no_hub_block;  /* nonzero: no dense hub block (HubBlock::kOff) */
-  int hub_min_degree; /* with hub_min_count > 0: explicit block thresholds */
-  int hub_min_count;
+  /* explicit hub block tiers (PartitionPolicy::hub_min_degree / hub_min_count):
+   * the leading pairs with both values > 0, degrees decreasing */
+  int hub_min_degree[PSX_HUB_MAX_TIERS];
+  int hub_min_count[PSX_HUB_MAX_TIERS];
 } psx_build_options;
 /* Group order the operators run in (same results; TaskOrder in matrix_utils.h):
  * the public signature order, or a row-ordered execution copy kept when it
@@ -80,9 +84,10 @@ int psx_matrix_run_order(const psx_matrix* m, int* used);
  * GroupTypeNum() when SpMM runs on the public worksets). No reference
  * counterpart. */
 int psx_matrix_spmm_worksets(const psx_matrix* m, int* group_type_num);
-/* The dense hub block the build chose (HubRows() x HubCols(); 0 x 0 when
- * none); outputs may be NULL. No reference counterpart. */
-int psx_matrix_hub_block(const psx_matrix* m, int* rows, int* cols);
+/* The dense hub block the build chose: its number of tiers (HubTiers()) and
+ * tier `tier`'s rows x columns (0 x 0 beyond the last); outputs may be NULL.
+ * No reference counterpart. */
+int psx_matrix_hub_block(const psx_matrix* m, int* tiers, int tier, int* rows, int* cols);
 /* Replaces: ~PowerSparseMatrixGPU (matrix_utils.h:24). */
 int psx_matrix_destroy(psx_matrix* m);
 /* Replaces: MatrixRow/MatrixCol/MatrixNNZ/GroupTypeNum/GroupFineSize (matrix_utils.h:30-34);

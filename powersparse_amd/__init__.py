@@ -350,10 +350,11 @@ class PowerSparseMatrixGPU:
     ("auto", "signature" or "row") picks the group order the operators run in
     (same results); `.task_order` and `.locality` report the choice and the
     scores compared. hub_block ("auto" or "off") keeps the dense hub block
-    (rows of highest degree x most popular columns) as a dense matrix run on
-    the matrix cores when the cost rule finds one, and hub_min_degree /
-    hub_min_count (both > 0) set its thresholds explicitly; `.hub_block`
-    reports its (rows, columns), (0, 0) when none. With timings=True the stage
+    (rows of highest degree x most popular columns, in up to three tiers of
+    row ranges) as dense matrices run on the matrix cores when the cost rule
+    finds one, and hub_thresholds = [(min_degree, min_count), ...] (degrees
+    decreasing) sets its tiers explicitly; `.hub_block` lists the tiers'
+    (rows, columns), [] when none. With timings=True the stage
     times (ms) are kept in `.timings` (the task-order step counts into
     "gather").
     """
@@ -366,7 +367,7 @@ class PowerSparseMatrixGPU:
     def __init__(self, row_num, col_num, nnz_num, row_ptr, col_ind, sp_data, cu_count=0,
                  timings=False, signature_order="auto", csr_positions=False,
                  task_order="auto", run_order=True, max_group_types=0,
-                 spmm_partition="tuned", hub_block="auto", hub_min_degree=0, hub_min_count=0):
+                 spmm_partition="tuned", hub_block="auto", hub_thresholds=()):
         row_ptr = np.ascontiguousarray(row_ptr, dtype=np.int32)
         col_ind = np.ascontiguousarray(col_ind, dtype=np.int32)
         sp_data = np.ascontiguousarray(sp_data, dtype=np.float32)
@@ -381,11 +382,15 @@ class PowerSparseMatrixGPU:
             raise ValueError("spmm_partition must be 'tuned' or 'parity'")
         if hub_block not in ("auto", "off"):
             raise ValueError("hub_block must be 'auto' or 'off'")
+        if len(hub_thresholds) > 3:
+            raise ValueError("at most 3 hub block tiers")
+        degs = (ctypes.c_int * 3)(*[int(d) for d, _ in hub_thresholds])
+        cnts = (ctypes.c_int * 3)(*[int(c) for _, c in hub_thresholds])
         opts = _native.BuildOptions(int(cu_count), self.ORDER_METHODS.index(signature_order),
                                     int(bool(csr_positions)), self.TASK_ORDERS.index(task_order),
                                     int(not run_order), int(max_group_types),
                                     int(spmm_partition == "parity"), int(hub_block == "off"),
-                                    int(hub_min_degree), int(hub_min_count))
+                                    degs, cnts)
         _host_call(_native.host().psx_matrix_create_ex(
             int(row_num), int(col_num), int(nnz_num),
             row_ptr.ctypes.data if row_ptr.size else None,
@@ -406,9 +411,13 @@ class PowerSparseMatrixGPU:
         self.run_order = bool(used.value)
         _host_call(_native.host().psx_matrix_spmm_worksets(self._h, ctypes.byref(used)))
         self.spmm_worksets = used.value  # workset count of the partition SpMM runs on
-        hr, hc = ctypes.c_int(), ctypes.c_int()
-        _host_call(_native.host().psx_matrix_hub_block(self._h, ctypes.byref(hr), ctypes.byref(hc)))
-        self.hub_block = (hr.value, hc.value)
+        tiers, hr, hc = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        self.hub_block = []
+        _host_call(_native.host().psx_matrix_hub_block(self._h, ctypes.byref(tiers), 0, None, None))
+        for k in range(tiers.value):
+            _host_call(_native.host().psx_matrix_hub_block(self._h, None, k, ctypes.byref(hr),
+                                                           ctypes.byref(hc)))
+            self.hub_block.append((hr.value, hc.value))
         self.timings = dict(zip(self.TIMING_KEYS, list(t))) if timings else None
         rows, cols, nnz, S, fine, L, cu = (ctypes.c_int() for _ in range(7))
         _host_call(_native.host().psx_matrix_info(
@@ -423,13 +432,12 @@ class PowerSparseMatrixGPU:
     @classmethod
     def from_csr(cls, csr, cu_count=0, timings=False, signature_order="auto",
                  csr_positions=False, task_order="auto", run_order=True, max_group_types=0,
-                 spmm_partition="tuned", hub_block="auto", hub_min_degree=0, hub_min_count=0):
+                 spmm_partition="tuned", hub_block="auto", hub_thresholds=()):
         return cls(csr.rows, csr.cols, csr.nnz, csr.row_ptr, csr.col_ind, csr.values,
                    cu_count=cu_count, timings=timings, signature_order=signature_order,
                    csr_positions=csr_positions, task_order=task_order, run_order=run_order,
                    max_group_types=max_group_types, spmm_partition=spmm_partition,
-                   hub_block=hub_block, hub_min_degree=hub_min_degree,
-                   hub_min_count=hub_min_count)
+                   hub_block=hub_block, hub_thresholds=hub_thresholds)
 
     def close(self):
         if self._h:

@@ -39,7 +39,7 @@ class BuildOptions(ctypes.Structure):
                 ("csr_positions", ctypes.c_int), ("task_order", ctypes.c_int),
                 ("stored_order", ctypes.c_int), ("max_group_types", ctypes.c_int),
                 ("parity_spmm", ctypes.c_int), ("no_hub_block", ctypes.c_int),
-                ("hub_min_degree", ctypes.c_int), ("hub_min_count", ctypes.c_int)]
+                ("hub_min_degree", ctypes.c_int * 3), ("hub_min_count", ctypes.c_int * 3)]
 
 
 class DeviceProps(ctypes.Structure):
@@ -264,7 +264,7 @@ HOST_API = [
     ("psx_matrix_task_order", ctypes.c_int, [c_void_p, c_int_p, c_double_p, c_double_p]),
     ("psx_matrix_run_order", ctypes.c_int, [c_void_p, c_int_p]),
     ("psx_matrix_spmm_worksets", ctypes.c_int, [c_void_p, c_int_p]),
-    ("psx_matrix_hub_block", ctypes.c_int, [c_void_p, c_int_p, c_int_p]),
+    ("psx_matrix_hub_block", ctypes.c_int, [c_void_p, c_int_p, ctypes.c_int, c_int_p, c_int_p]),
     ("psx_matrix_destroy", ctypes.c_int, [c_void_p]),
     ("psx_matrix_info", ctypes.c_int,
      [c_void_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p, c_int_p]),

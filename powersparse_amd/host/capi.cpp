@@ -58,7 +58,7 @@ const char* psx_last_error(void) { return g_error.c_str(); }
 
 int psx_matrix_create(int rows, int cols, int nnz, const int* row_ptr, const int* col_ind,
                       const float* sp_data, int cu_count, double* timings_ms, psx_matrix** out) {
-  psx_build_options options{cu_count, PSX_ORDER_AUTO, 0, PSX_TASK_AUTO, 0, 0, 0, 0, 0, 0};
+  psx_build_options options{cu_count, PSX_ORDER_AUTO, 0, PSX_TASK_AUTO, 0, 0, 0, 0, {}, {}};
   return psx_matrix_create_ex(rows, cols, nnz, row_ptr, col_ind, sp_data, &options, timings_ms,
                               out);
 }
@@ -81,8 +81,10 @@ int psx_matrix_create_ex(int rows, int cols, int nnz, const int* row_ptr, const 
                                                    : PowerSparse::SpmmPartition::kTuned;
       policy.hub_block = options->no_hub_block ? PowerSparse::HubBlock::kOff
                                                : PowerSparse::HubBlock::kAuto;
-      policy.hub_min_degree = options->hub_min_degree;
-      policy.hub_min_count = options->hub_min_count;
+      for (int k = 0; k < PSX_HUB_MAX_TIERS && k < PowerSparse::kHubMaxTiers; ++k) {
+        policy.hub_min_degree[k] = options->hub_min_degree[k];
+        policy.hub_min_count[k] = options->hub_min_count[k];
+      }
     }
     PowerSparse::PreprocessTimings t;
     auto* m = new PowerSparse::PowerSparseMatrixGPU(rows, cols, nnz, row_ptr, col_ind, sp_data,
@@ -127,11 +129,12 @@ int psx_matrix_spmm_worksets(const psx_matrix* m, int* group_type_num) {
   });
 }
 
-int psx_matrix_hub_block(const psx_matrix* m, int* rows, int* cols) {
+int psx_matrix_hub_block(const psx_matrix* m, int* tiers, int tier, int* rows, int* cols) {
   return Guard([&] {
     Need(m && m->m, "psx_matrix_hub_block: null matrix");
-    if (rows) *rows = m->m->HubRows();
-    if (cols) *cols = m->m->HubCols();
+    if (tiers) *tiers = m->m->HubTiers();
+    if (rows) *rows = m->m->HubRows(tier);
+    if (cols) *cols = m->m->HubCols(tier);
   });
 }
 

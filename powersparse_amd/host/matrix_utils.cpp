@@ -646,15 +646,20 @@ void PowerSparseMatrixGPU::Build(const int* row_ptr, Prepared& in, bool last_par
 
 // ------------------------------------------------------------ hub block
 
-struct PowerSparseMatrixGPU::HubState {
+// One tier of the hub block: a row range x its hot columns.
+struct HubTier {
   ps_hub_block desc{};
   DeviceArray<int> hub_rows, hub_index, hot_cols, hot_rank;
   DeviceArray<float> dense;
   DeviceArray<uint32_t> stored;
-  // the 64-nonzero tiles of the public block groups inside the block, as
+  // the 64-nonzero tiles of the public block groups inside this tier, as
   // (workset << 27) | tile, sorted by hub row and first column (SDDMM writes
   // them from the dense product)
   DeviceArray<uint32_t> tiles;
+};
+
+struct PowerSparseMatrixGPU::HubState {
+  std::vector<std::unique_ptr<HubTier>> tiers;
   // the operator workspace: one call at a time, in GPU order (`done` is
   // recorded after each call's hub kernels, the next call waits for it)
   std::mutex mu;
@@ -664,10 +669,22 @@ struct PowerSparseMatrixGPU::HubState {
   ~HubState() {
     if (done) ps_event_destroy(done);
   }
+  size_t Workspace(int op, int N) const {
+    size_t need = 0;
+    for (const auto& t : tiers)
+      if (op == PS_OP_SPMM || t->tiles.size())
+        need = std::max(need, ps_hub_workspace_bytes(&t->desc, op, N));
+    return need;
+  }
 };
 
-int PowerSparseMatrixGPU::HubRows() const { return _hub ? _hub->desc.rows : 0; }
-int PowerSparseMatrixGPU::HubCols() const { return _hub ? _hub->desc.cols : 0; }
+int PowerSparseMatrixGPU::HubTiers() const { return _hub ? int(_hub->tiers.size()) : 0; }
+int PowerSparseMatrixGPU::HubRows(int tier) const {
+  return tier >= 0 && tier < HubTiers() ? _hub->tiers[size_t(tier)]->desc.rows : 0;
+}
+int PowerSparseMatrixGPU::HubCols(int tier) const {
+  return tier >= 0 && tier < HubTiers() ? _hub->tiers[size_t(tier)]->desc.cols : 0;
+}
 
 namespace {
 int FloorLog2(long long v) {
@@ -678,6 +695,9 @@ int FloorLog2(long long v) {
   }
   return b;
 }
+struct TierSpec {
+  long long min_degree, max_degree, min_count;  // rows in [min_degree, max_degree)
+};
 }  // namespace
 
 bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
@@ -685,8 +705,8 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
   const int rows = _matrix_row, cols = _matrix_col, S = _group_type_num;
   if (S < 2) return false;  // fine mode: its store rule differs from a capped partition's
   const std::vector<int>& cnt = in.col_nnz_host;
-  // rows of degree >= 2^a, columns of count >= 2^b
-  std::vector<long long> rows_ge(33, 0), cols_ge(33, 0);
+  // rows of degree >= 2^a, columns of count >= 2^b (index 32: none)
+  std::vector<long long> rows_ge(34, 0), cols_ge(34, 0);
   for (int r = 0; r < rows; ++r) {
     const int d = row_ptr[r + 1] - row_ptr[r];
     if (d > 0) ++rows_ge[size_t(FloorLog2(d))];
@@ -697,9 +717,18 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
     rows_ge[size_t(k)] += rows_ge[size_t(k) + 1];
     cols_ge[size_t(k)] += cols_ge[size_t(k) + 1];
   }
-  long long min_degree = policy.hub_min_degree, min_count = policy.hub_min_count;
-  const bool forced = min_degree > 0 && min_count > 0;
-  if (!forced) {
+  std::vector<TierSpec> specs;
+  const bool forced = policy.hub_min_degree[0] > 0 && policy.hub_min_count[0] > 0;
+  if (forced) {
+    for (int k = 0; k < kHubMaxTiers; ++k) {
+      if (policy.hub_min_degree[k] <= 0 || policy.hub_min_count[k] <= 0) break;
+      const long long hi = specs.empty() ? std::numeric_limits<long long>::max()
+                                         : specs.back().min_degree;
+      if (policy.hub_min_degree[k] >= hi)
+        throw std::invalid_argument("PartitionPolicy hub tiers need decreasing row degrees");
+      specs.push_back({policy.hub_min_degree[k], hi, policy.hub_min_count[k]});
+    }
+  } else {
     // nonzeros of rows of degree >= 2^a (a >= 8) in columns of count >= 2^b
     DeviceArray<unsigned long long> hist(32 * 32);
     ThrowOnError(ps_hub_histogram(in.row_ptr.data(), rows, in.col_ind.data(), in.col_nnz.data(),
@@ -713,84 +742,112 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
                                          ge[size_t(a + 1) * 33 + size_t(b)] +
                                          ge[size_t(a) * 33 + size_t(b + 1)] -
                                          ge[size_t(a + 1) * 33 + size_t(b + 1)];
-    double best = 0.0;
-    for (int a = 8; a < 31; ++a)
-      for (int b = 0; b < 31; ++b) {
-        const long long R = rows_ge[size_t(a)], H = cols_ge[size_t(b)];
-        if (R < kHubMinRows || H < kHubMinCols || R * H > kHubMaxElements) continue;
-        const double gain = ge[size_t(a) * 33 + size_t(b)] - kHubDenseCost * double(R) * double(H);
-        if (gain > best) {
-          best = gain;
-          min_degree = 1LL << a;
-          min_count = 1LL << b;
+    int top = 32;  // the rows of earlier tiers have degree >= 2^top
+    for (int k = 0; k < kHubMaxTiers; ++k) {
+      double best = 0.0;
+      int ba = -1, bb = -1;
+      for (int a = 8; a < top; ++a)
+        for (int b = 0; b < 31; ++b) {
+          const long long R = rows_ge[size_t(a)] - rows_ge[size_t(top)], H = cols_ge[size_t(b)];
+          if (R < kHubMinRows || H < kHubMinCols || R * H > kHubMaxElements) continue;
+          const double nz = ge[size_t(a) * 33 + size_t(b)] - ge[size_t(top) * 33 + size_t(b)];
+          const double gain = nz - kHubDenseCost * double(R) * double(H);
+          if (gain > best) {
+            best = gain;
+            ba = a;
+            bb = b;
+          }
         }
-      }
-    if (best < kHubMinGain * double(_matrix_nnz)) return false;
+      if (ba < 0 || best < (k == 0 ? kHubMinGain : kHubMinTierGain) * double(_matrix_nnz)) break;
+      specs.push_back({1LL << ba, top < 32 ? (1LL << top) : std::numeric_limits<long long>::max(),
+                       1LL << bb});
+      top = ba;
+    }
+    if (specs.empty()) return false;
   }
 
   auto hub = std::make_unique<HubState>();
-  std::vector<int> hub_rows, hub_index(size_t(rows), -1), hot_cols, hot_rank(size_t(cols), -1);
-  for (int r = 0; r < rows; ++r)
-    if (row_ptr[r + 1] - row_ptr[r] >= min_degree) {
-      hub_index[size_t(r)] = int(hub_rows.size());
-      hub_rows.push_back(r);
+  for (const TierSpec& spec : specs) {
+    auto t = std::make_unique<HubTier>();
+    std::vector<int> hub_rows, hub_index(size_t(rows), -1), hot_cols, hot_rank(size_t(cols), -1);
+    for (int r = 0; r < rows; ++r) {
+      const long long d = row_ptr[r + 1] - row_ptr[r];
+      if (d >= spec.min_degree && d < spec.max_degree) {
+        hub_index[size_t(r)] = int(hub_rows.size());
+        hub_rows.push_back(r);
+      }
     }
-  for (int c = 0; c < cols; ++c)
-    if (cnt[size_t(c)] >= min_count) {
-      hot_rank[size_t(c)] = int(hot_cols.size());
-      hot_cols.push_back(c);
+    for (int c = 0; c < cols; ++c)
+      if (cnt[size_t(c)] >= spec.min_count) {
+        hot_rank[size_t(c)] = int(hot_cols.size());
+        hot_cols.push_back(c);
+      }
+    const long long R = (long long)hub_rows.size(), H = (long long)hot_cols.size();
+    if (R == 0 || H == 0) continue;
+    if (R * H > kHubMaxElements) {
+      if (forced)
+        throw std::invalid_argument("PartitionPolicy hub thresholds give a dense block over " +
+                                    std::to_string(kHubMaxElements) + " elements");
+      continue;
     }
-  const long long R = (long long)hub_rows.size(), H = (long long)hot_cols.size();
-  if (R == 0 || H == 0) return false;
-  if (R * H > kHubMaxElements) {
-    if (forced)
-      throw std::invalid_argument("PartitionPolicy hub thresholds give a dense block over " +
-                                  std::to_string(kHubMaxElements) + " elements");
-    return false;
+    t->hub_rows.Allocate(size_t(R));
+    t->hub_rows.Upload(hub_rows.data(), size_t(R));
+    t->hub_index.Allocate(size_t(rows));
+    t->hub_index.Upload(hub_index.data(), size_t(rows));
+    t->hot_cols.Allocate(size_t(H));
+    t->hot_cols.Upload(hot_cols.data(), size_t(H));
+    t->hot_rank.Allocate(size_t(cols));
+    t->hot_rank.Upload(hot_rank.data(), size_t(cols));
+    ps_hub_block& d = t->desc;
+    d.matrix_rows = rows;
+    d.matrix_cols = cols;
+    d.rows = int(R);
+    d.cols = int(H);
+    d.hub_rows = t->hub_rows.data();
+    d.hub_index = t->hub_index.data();
+    d.hot_cols = t->hot_cols.data();
+    d.hot_rank = t->hot_rank.data();
+    t->dense.Allocate(size_t(R) * size_t(H));
+    t->stored.Allocate(ps_hub_stored_words(&d));
+    d.dense = t->dense.data();
+    d.stored = t->stored.data();
+    ThrowOnError(ps_hub_dense_build(&d, in.row_ptr.data(), in.col_ind.data(), in.sp_data.data(),
+                                    t->dense.data(), t->stored.data(), nullptr));
+    hub->tiers.push_back(std::move(t));
   }
-  hub->hub_rows.Allocate(size_t(R));
-  hub->hub_rows.Upload(hub_rows.data(), size_t(R));
-  hub->hub_index.Allocate(size_t(rows));
-  hub->hub_index.Upload(hub_index.data(), size_t(rows));
-  hub->hot_cols.Allocate(size_t(H));
-  hub->hot_cols.Upload(hot_cols.data(), size_t(H));
-  hub->hot_rank.Allocate(size_t(cols));
-  hub->hot_rank.Upload(hot_rank.data(), size_t(cols));
-  ps_hub_block& d = hub->desc;
-  d.matrix_rows = rows;
-  d.matrix_cols = cols;
-  d.rows = int(R);
-  d.cols = int(H);
-  d.hub_rows = hub->hub_rows.data();
-  d.hub_index = hub->hub_index.data();
-  d.hot_cols = hub->hot_cols.data();
-  d.hot_rank = hub->hot_rank.data();
-  hub->dense.Allocate(size_t(R) * size_t(H));
-  hub->stored.Allocate(ps_hub_stored_words(&d));
-  d.dense = hub->dense.data();
-  d.stored = hub->stored.data();
-  ThrowOnError(ps_hub_dense_build(&d, in.row_ptr.data(), in.col_ind.data(), in.sp_data.data(),
-                                  hub->dense.data(), hub->stored.data(), nullptr));
+  if (hub->tiers.empty()) return false;
 
-  // SpMM: a tuned partition of the matrix without the block.
-  DeviceArray<uint32_t> kept(size_t(rows) + 1);
-  ThrowOnError(ps_memset_async(kept.data() + rows, 0, sizeof(uint32_t), nullptr));
-  ThrowOnError(ps_hub_kept_counts(&d, in.row_ptr.data(), in.col_ind.data(), kept.data(), nullptr));
-  DeviceArray<int> rp(size_t(rows) + 1);
-  {
-    DeviceArray<char> scan_ws(ps_scan_workspace_bytes(size_t(rows) + 1));
-    ThrowOnError(ps_exclusive_scan_u32(kept.data(), reinterpret_cast<uint32_t*>(rp.data()),
-                                       size_t(rows) + 1, scan_ws.data(), nullptr));
-  }
+  // SpMM: a tuned partition of the matrix without the block, the tiers taken
+  // out one after another (their rows are disjoint).
+  DeviceArray<int> rp, ci;
+  DeviceArray<float> sv;
   std::vector<int> rp_host(size_t(rows) + 1);
+  int nnz_rest = _matrix_nnz;
+  for (const auto& t : hub->tiers) {
+    const int* cur_rp = rp.size() ? rp.data() : in.row_ptr.data();
+    const int* cur_ci = ci.size() ? ci.data() : in.col_ind.data();
+    const float* cur_sv = sv.size() ? sv.data() : in.sp_data.data();
+    DeviceArray<uint32_t> kept(size_t(rows) + 1);
+    ThrowOnError(ps_memset_async(kept.data() + rows, 0, sizeof(uint32_t), nullptr));
+    ThrowOnError(ps_hub_kept_counts(&t->desc, cur_rp, cur_ci, kept.data(), nullptr));
+    DeviceArray<int> next_rp(size_t(rows) + 1);
+    {
+      DeviceArray<char> scan_ws(ps_scan_workspace_bytes(size_t(rows) + 1));
+      ThrowOnError(ps_exclusive_scan_u32(kept.data(), reinterpret_cast<uint32_t*>(next_rp.data()),
+                                         size_t(rows) + 1, scan_ws.data(), nullptr));
+    }
+    ThrowOnError(ps_memcpy_dtoh(&nnz_rest, next_rp.data() + rows, sizeof(int)));
+    if (nnz_rest <= 0) return false;  // the block would hold every nonzero
+    DeviceArray<int> next_ci{static_cast<size_t>(nnz_rest)};
+    DeviceArray<float> next_sv{static_cast<size_t>(nnz_rest)};
+    ThrowOnError(ps_hub_compact(&t->desc, cur_rp, cur_ci, cur_sv,
+                                reinterpret_cast<const uint32_t*>(next_rp.data()), next_ci.data(),
+                                next_sv.data(), nullptr));
+    rp = std::move(next_rp);
+    ci = std::move(next_ci);
+    sv = std::move(next_sv);
+  }
   rp.Download(rp_host.data(), rp_host.size());
-  const int nnz_rest = rp_host[size_t(rows)];
-  if (nnz_rest <= 0) return false;  // the block would hold every nonzero
-  DeviceArray<int> ci{static_cast<size_t>(nnz_rest)};
-  DeviceArray<float> sv{static_cast<size_t>(nnz_rest)};
-  ThrowOnError(ps_hub_compact(&d, in.row_ptr.data(), in.col_ind.data(), in.sp_data.data(),
-                              reinterpret_cast<const uint32_t*>(rp.data()), ci.data(), sv.data(),
-                              nullptr));
   Prepared rest(rows, cols, nnz_rest, std::move(rp), std::move(ci), std::move(sv));
   // the rest must keep the public partition's store rule: more than one workset
   if (std::min(WorksetCount(rest.degree_sums, _cu_count), kTunedSpmmGroupTypes) < 2) return false;
@@ -805,36 +862,64 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
       new PowerSparseMatrixGPU(Unbuilt{}, rows, cols, nnz_rest, _cu_count, tuned));
   part->Build(rp_host.data(), rest, true);
   // hub rows add their remaining entries to the block's product
-  ThrowOnError(ps_hub_mark_atomic(&d, part->_group_des[0], part->_group_num[0],
-                                  reinterpret_cast<uint8_t*>(part->_residue_atomic), nullptr));
+  for (const auto& t : hub->tiers)
+    ThrowOnError(ps_hub_mark_atomic(&t->desc, part->_group_des[0], part->_group_num[0],
+                                    reinterpret_cast<uint8_t*>(part->_residue_atomic), nullptr));
 
   // SDDMM: the groups inside the block leave the run order; their outputs come
-  // from the dense product.
+  // from the dense products.
+  // A tier the cost rule chose serves SDDMM only when its groups inside the
+  // block hold at least kHubSddmmMinFill nonzeros per dense element (its D is
+  // computed whole); explicit tiers serve both operators.
   std::vector<ps_workset> ws = PublicWorksets();
-  std::vector<DeviceArray<uint8_t>> flags(static_cast<size_t>(S));
-  std::vector<const uint8_t*> flag_ptr(static_cast<size_t>(S), nullptr);
-  std::vector<uint32_t> tiles;
+  const size_t T = hub->tiers.size();
+  std::vector<std::vector<uint32_t>> tiles(T);
+  std::vector<std::vector<std::vector<uint8_t>>> flags(T, std::vector<std::vector<uint8_t>>(size_t(S)));
+  DeviceArray<uint8_t> f_dev;
   for (int s = 1; s < S; ++s) {
     const int G = _group_num[s], GS = GROUP_SIZE(s);
     if (G == 0 || GS < 64) continue;
-    flags[size_t(s)].Allocate(size_t(G));
-    ThrowOnError(ps_hub_group_flags(&d, &ws[size_t(s)], flags[size_t(s)].data(), nullptr));
-    std::vector<uint8_t> f(static_cast<size_t>(G));
-    flags[size_t(s)].Download(f.data(), f.size());
-    bool any = false;
-    for (int g = 0; g < G; ++g)
-      if (f[size_t(g)]) {
-        any = true;
-        for (int j = 0; j < GS / 64; ++j)
-          tiles.push_back((uint32_t(s) << 27) | (uint32_t(g) * uint32_t(GS / 64) + uint32_t(j)));
-      }
-    if (any) flag_ptr[size_t(s)] = flags[size_t(s)].data();
+    f_dev.Allocate(size_t(G));
+    for (size_t k = 0; k < T; ++k) {
+      ThrowOnError(ps_hub_group_flags(&hub->tiers[k]->desc, &ws[size_t(s)], f_dev.data(), nullptr));
+      std::vector<uint8_t>& f = flags[k][size_t(s)];
+      f.resize(size_t(G));
+      f_dev.Download(f.data(), f.size());
+      for (int g = 0; g < G; ++g)
+        if (f[size_t(g)])
+          for (int j = 0; j < GS / 64; ++j)
+            tiles[k].push_back((uint32_t(s) << 27) |
+                               (uint32_t(g) * uint32_t(GS / 64) + uint32_t(j)));
+    }
   }
-  if (!tiles.empty()) {
-    hub->tiles.Allocate(tiles.size());
-    hub->tiles.Upload(tiles.data(), tiles.size());
-    ThrowOnError(ps_hub_sort_tiles(&d, S, ws.data(), hub->tiles.data(), uint32_t(tiles.size()),
-                                   nullptr));
+  for (size_t k = 0; k < T && !forced; ++k) {
+    const ps_hub_block& d = hub->tiers[k]->desc;
+    if (double(tiles[k].size()) * 64.0 < kHubSddmmMinFill * double(d.rows) * double(d.cols))
+      tiles[k].clear();
+  }
+  std::vector<DeviceArray<uint8_t>> skip(static_cast<size_t>(S));
+  std::vector<const uint8_t*> skip_ptr(static_cast<size_t>(S), nullptr);
+  for (int s = 1; s < S; ++s) {
+    const int G = _group_num[s];
+    std::vector<uint8_t> any(static_cast<size_t>(G), 0);
+    bool flagged = false;
+    for (size_t k = 0; k < T; ++k) {
+      if (tiles[k].empty() || flags[k][size_t(s)].empty()) continue;
+      for (int g = 0; g < G; ++g)
+        if (flags[k][size_t(s)][size_t(g)]) any[size_t(g)] = 1, flagged = true;
+    }
+    if (!flagged) continue;
+    skip[size_t(s)].Allocate(size_t(G));
+    skip[size_t(s)].Upload(any.data(), any.size());  // groups inside an SDDMM tier
+    skip_ptr[size_t(s)] = skip[size_t(s)].data();
+  }
+  for (size_t k = 0; k < T; ++k) {
+    if (tiles[k].empty()) continue;
+    HubTier& t = *hub->tiers[k];
+    t.tiles.Allocate(tiles[k].size());
+    t.tiles.Upload(tiles[k].data(), tiles[k].size());
+    ThrowOnError(ps_hub_sort_tiles(&t.desc, S, ws.data(), t.tiles.data(),
+                                   uint32_t(tiles[k].size()), nullptr));
   }
   const int k = RunOrderSlot(PS_OP_SDDMM, 32);
   uint32_t count = 0, kept_tasks = 0;
@@ -842,7 +927,7 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
   uint32_t* order = nullptr;
   if (count > 0) {
     ThrowOnError(ps_malloc(reinterpret_cast<void**>(&order), sizeof(uint32_t) * count));
-    const int rc = ps_task_order_build_subset(PS_OP_SDDMM, 32, S, ws.data(), flag_ptr.data(),
+    const int rc = ps_task_order_build_subset(PS_OP_SDDMM, 32, S, ws.data(), skip_ptr.data(),
                                               order, count, &kept_tasks, nullptr);
     if (rc != PS_OK) {
       ps_free(order);
@@ -861,10 +946,11 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
 void PowerSparseMatrixGPU::HubSpmm(int N, const float* B, float* C, ps_stream_t stream) const {
   HubState& h = *_hub;
   std::lock_guard<std::mutex> lock(h.mu);
-  const size_t need = ps_hub_workspace_bytes(&h.desc, PS_OP_SPMM, N);
+  const size_t need = h.Workspace(PS_OP_SPMM, N);
   if (h.ws.size() < need) h.ws.Allocate(need);  // synchronises the device first
   if (h.recorded) ThrowOnError(ps_stream_wait_event(stream, h.done));
-  ThrowOnError(ps_hub_spmm_launch(&h.desc, N, B, C, h.ws.data(), h.ws.size(), stream));
+  for (const auto& t : h.tiers)
+    ThrowOnError(ps_hub_spmm_launch(&t->desc, N, B, C, h.ws.data(), h.ws.size(), stream));
   ThrowOnError(ps_event_record(h.done, stream));
   h.recorded = true;
 }
@@ -874,13 +960,15 @@ void PowerSparseMatrixGPU::HubSddmm(int N, const float* lhs, const float* rhs, f
   HubState& h = *_hub;
   const std::vector<ps_workset> ws = PublicWorksets();
   std::lock_guard<std::mutex> lock(h.mu);
-  const size_t need = ps_hub_workspace_bytes(&h.desc, PS_OP_SDDMM, N);
+  const size_t need = h.Workspace(PS_OP_SDDMM, N);
   if (h.ws.size() < need) h.ws.Allocate(need);
   if (h.recorded) ThrowOnError(ps_stream_wait_event(stream, h.done));
-  ThrowOnError(ps_hub_sddmm_launch(&h.desc, _group_type_num, ws.data(), h.tiles.data(),
-                                   uint32_t(h.tiles.size()), N, lhs, rhs, out,
-                                   csr_out ? _workset_csr_pos : nullptr, csr_out, h.ws.data(),
-                                   h.ws.size(), stream));
+  for (const auto& t : h.tiers)
+    if (t->tiles.size())
+      ThrowOnError(ps_hub_sddmm_launch(&t->desc, _group_type_num, ws.data(), t->tiles.data(),
+                                       uint32_t(t->tiles.size()), N, lhs, rhs, out,
+                                       csr_out ? _workset_csr_pos : nullptr, csr_out, h.ws.data(),
+                                       h.ws.size(), stream));
   ThrowOnError(ps_event_record(h.done, stream));
   h.recorded = true;
 }

@@ -77,12 +77,18 @@ constexpr int kTunedSpmmGroupTypes = 3;
 // the matrix cores (ps_hub_spmm_launch / ps_hub_sddmm_launch), the rest as
 // before: SpMM on a tuned partition of the matrix without the block, SDDMM on
 // the public worksets with the block's groups left out of the run order and
-// their outputs written from the dense product. The block is the pair of
-// power-of-two thresholds (row degree >= 2^a, column count >= 2^b) that
-// maximises block nonzeros - kHubDenseCost * rows * columns, kept when that
-// gain is at least kHubMinGain of the nonzeros (kHubDenseCost: the dense
-// element's cost relative to the sparse nonzero it replaces, measured on
-// MI355X). It is used with the tuned SpMM partition and the locality run
+// their outputs written from the dense product. The block comes in up to
+// kHubMaxTiers tiers of disjoint row ranges, each with its own columns: the
+// first tier is the pair of power-of-two thresholds (row degree >= 2^a,
+// column count >= 2^b) that maximises block nonzeros - kHubDenseCost * rows
+// * columns, kept when that gain is at least kHubMinGain of the nonzeros; the
+// next tier takes the rows below 2^a the same way, kept from kHubMinTierGain
+// (kHubDenseCost: the dense element's cost relative to the sparse nonzero it
+// replaces, measured on MI355X). SDDMM computes a tier's dense dots whole and
+// takes from it only the groups lying inside it, so it uses a tier when those
+// hold at least kHubSddmmMinFill nonzeros per dense element (C3: the first
+// tier, 2526 x 72840; the second, rows of degree 1024..16383 x 3578 columns,
+// serves SpMM alone). It is used with the tuned SpMM partition and the locality run
 // order only. Results match the sparse path within FP32 summation order;
 // Inf / NaN in B reach exactly the rows that store their column; rows of the
 // block accumulate into C as the reference's do (they hold more than 32
@@ -90,7 +96,9 @@ constexpr int kTunedSpmmGroupTypes = 3;
 // partition's own preprocessing (it no longer shares the public one's), and
 // an operator workspace grown on first use (SDDMM: 4 bytes per block element).
 enum class HubBlock { kAuto = 0, kOff = 1 };
-constexpr double kHubDenseCost = 0.12, kHubMinGain = 0.05;
+constexpr int kHubMaxTiers = 3;
+constexpr double kHubDenseCost = 0.12, kHubMinGain = 0.05, kHubMinTierGain = 0.02;
+constexpr double kHubSddmmMinFill = 0.25;
 constexpr int kHubMinRows = 256, kHubMinCols = 1024;
 constexpr long long kHubMaxElements = 1LL << 29;
 constexpr double kRowOrderGain = 0.85;
@@ -150,11 +158,14 @@ struct PartitionPolicy {
   int max_group_types = 0;
   SpmmPartition spmm_partition = SpmmPartition::kTuned;
   HubBlock hub_block = HubBlock::kAuto;
-  // Explicit block thresholds (both > 0): rows of degree >= hub_min_degree,
-  // columns with >= hub_min_count nonzeros, whatever the cost rule says (the
+  // Explicit tiers, whatever the cost rule says: tier k holds the rows of
+  // degree >= hub_min_degree[k] (and below tier k-1's) and the columns with
+  // >= hub_min_count[k] nonzeros; the leading pairs with both values > 0 are
+  // used, degrees decreasing; they serve SDDMM too, whatever their fill. The
   // block is still dropped when it would hold every nonzero, or when the
-  // matrix has a single workset).
-  int hub_min_degree = 0, hub_min_count = 0;
+  // matrix has a single workset.
+  int hub_min_degree[kHubMaxTiers] = {};
+  int hub_min_count[kHubMaxTiers] = {};
 };
 
 // Wall-clock milliseconds of the preprocessing stages (host timer, the stream
@@ -214,10 +225,12 @@ class PowerSparseMatrixGPU {
   const PowerSparseMatrixGPU& SpmmMatrix() const { return _spmm_tuned ? *_spmm_tuned : *this; }
   // What the operators launch on.
   ExecutionLayout Execution() const;
-  // The dense hub block in use (HubBlock), as rows x columns; 0 x 0 when none.
+  // The dense hub block in use (HubBlock): its tiers, each rows x columns
+  // (0 x 0 beyond the last).
   bool HubBlockUsed() const { return _hub != nullptr; }
-  int HubRows() const;
-  int HubCols() const;
+  int HubTiers() const;
+  int HubRows(int tier = 0) const;
+  int HubCols(int tier = 0) const;
   // The hub block's part of an operator call, enqueued on `stream` after the
   // sparse part (SpMM: C += block * B; SDDMM: the block groups' outputs, into
   // out[s] or, with csr_out, into csr_out at the CSR positions). Calls on one

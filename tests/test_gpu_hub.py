@@ -22,11 +22,13 @@ def csr_of(g):
     return ps.HostCsr(g.rows, g.cols, g.row_ptr, g.col_ind, g.values)
 
 
-def thresholds(csr, cu, shares=((0.25, 0.5), (0.25, 0.3), (0.1, 0.3), (0.1, 0.15))):
-    """Explicit block thresholds: the heaviest rows (a share of the rows with 64+
-    nonzeros) and the columns whose count reaches a share of the hub rows'
-    entries, the first pair for which the matrix without the block still has
-    more than one workset at `cu` CUs (the build drops the block otherwise)."""
+def thresholds(csr, cu, tiers=1,
+               shares=((0.25, 0.5), (0.25, 0.3), (0.1, 0.3), (0.1, 0.15))):
+    """Explicit block tiers [(min_degree, min_count), ...]: tier k takes the
+    next share of the rows with 64+ nonzeros (heaviest first) and the columns
+    whose count reaches a share of those rows' entries; the first shares for
+    which the matrix without the block still has more than one workset at
+    `cu` CUs (the build drops the block otherwise)."""
     deg = np.diff(csr.row_ptr.astype(np.int64))
     heavy = np.sort(deg[deg >= 64])[::-1]
     assert heavy.size, "no heavy rows"
@@ -34,14 +36,22 @@ def thresholds(csr, cu, shares=((0.25, 0.5), (0.25, 0.3), (0.1, 0.3), (0.1, 0.15
     rowof = np.repeat(np.arange(csr.rows), deg)
     cu = cu or 256
     for hub_share, hot_share in shares:
-        min_degree = int(heavy[max(0, int(heavy.size * hub_share) - 1)])
-        hub_cnt = np.sort(cnt[csr.col_ind[deg[rowof] >= min_degree]])
-        min_count = max(int(hub_cnt[int(hub_cnt.size * (1 - hot_share))]), 1)
-        block = (deg[rowof] >= min_degree) & (cnt[csr.col_ind] >= min_count)
+        out, block, hi = [], np.zeros(csr.nnz, bool), np.inf
+        for k in range(tiers):
+            d = int(heavy[max(0, int(heavy.size * hub_share * (k + 1)) - 1)])
+            if d >= hi:
+                break
+            rows_k = (deg[rowof] >= d) & (deg[rowof] < hi)
+            c = max(int(np.sort(cnt[csr.col_ind[rows_k]])[int(rows_k.sum() * (1 - hot_share))]), 1)
+            block |= rows_k & (cnt[csr.col_ind] >= c)
+            out.append((d, c))
+            hi = d
+        if len(out) < tiers:
+            continue
         rest = np.bincount(rowof[~block], minlength=csr.rows)
         rp = np.concatenate([[0], np.cumsum(rest)]).astype(np.int32)
         if rp[-1] > 0 and oracle.analyze_group_type_num(rp, cu) >= 2:
-            return min_degree, min_count
+            return out
     raise AssertionError("no block keeps two worksets in the rest")
 
 
@@ -66,21 +76,22 @@ def run_ops(m, g, N, B, X, Y, calls=1):
     return C, W, csr_out.download(np.float32, g.nnz)
 
 
-@pytest.mark.parametrize("name", ["hubs", "skewed", "duplicates"])
-def test_hub_block_exact_on_golden(name):
+@pytest.mark.parametrize("name,tiers", [("hubs", 1), ("skewed", 1), ("duplicates", 1),
+                                        ("skewed", 2), ("duplicates", 2)])
+def test_hub_block_exact_on_golden(name, tiers):
     setup()
     g = gd.load(name)
     p = g.parts[0]
     csr = csr_of(g)
-    min_degree, min_count = thresholds(csr, p.cu)
+    th = thresholds(csr, p.cu, tiers)
     kw = dict(cu_count=p.cu, csr_positions=True)
-    on = ps.PowerSparseMatrixGPU.from_csr(csr, hub_min_degree=min_degree,
-                                          hub_min_count=min_count, **kw)
+    on = ps.PowerSparseMatrixGPU.from_csr(csr, hub_thresholds=th, **kw)
     off = ps.PowerSparseMatrixGPU.from_csr(csr, hub_block="off", **kw)
-    say(f"golden {name}: hub block {on.hub_block} (degree >= {min_degree}, count >= "
-        f"{min_count}), S={on.GroupTypeNum()}, SpMM worksets {on.spmm_worksets}")
-    assert on.hub_block[0] > 0 and on.hub_block[1] > 0, "the block was not built"
-    assert off.hub_block == (0, 0)
+    say(f"golden {name}: hub block {on.hub_block} (tiers {th}), S={on.GroupTypeNum()}, "
+        f"SpMM worksets {on.spmm_worksets}")
+    assert len(on.hub_block) == tiers and all(r > 0 and c > 0 for r, c in on.hub_block), \
+        "the block was not built"
+    assert off.hub_block == []
     # the public worksets are the reference's either way
     assert on.GroupNum() == off.GroupNum() == p.group_num
     for N in (32, 64, 128, 256):
@@ -106,11 +117,11 @@ def test_hub_block_nonfinite_b():
     setup()
     g = gd.load("hubs")
     csr = csr_of(g)
-    min_degree, min_count = thresholds(csr, 1)
-    on = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=1, hub_min_degree=min_degree,
-                                          hub_min_count=min_count, csr_positions=True)
+    th = thresholds(csr, 1)
+    min_count = th[0][1]
+    on = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=1, hub_thresholds=th, csr_positions=True)
     off = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=1, hub_block="off", csr_positions=True)
-    assert on.hub_block[0] > 0
+    assert on.hub_block
     cnt = np.bincount(csr.col_ind, minlength=csr.cols)
     hot = np.flatnonzero(cnt >= min_count)
     cold = np.flatnonzero((cnt > 0) & (cnt < min_count))
@@ -139,10 +150,10 @@ def test_hub_block_on_power_law_graphs(cfg, scale):
     double-precision results (stated FP32 tolerance)."""
     setup()
     csr = ps.synth(cfg, seed=3, scale=scale)
-    min_degree, min_count = thresholds(csr, 0, shares=((0.5, 0.5), (0.25, 0.3)))
-    m = ps.PowerSparseMatrixGPU.from_csr(csr, hub_min_degree=min_degree, hub_min_count=min_count)
-    say(f"{cfg}/{scale}: nnz={csr.nnz} hub block {m.hub_block} S={m.GroupTypeNum()}")
-    assert m.hub_block[0] > 0
+    th = thresholds(csr, 0, tiers=2, shares=((0.25, 0.5), (0.1, 0.3)))
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, hub_thresholds=th)
+    say(f"{cfg}/{scale}: nnz={csr.nnz} hub block {m.hub_block} (tiers {th}) S={m.GroupTypeNum()}")
+    assert len(m.hub_block) == 2
     rng = np.random.default_rng(5)
     for N in (32, 128):
         B = rng.uniform(-1, 1, (csr.cols, N)).astype(np.float32)
@@ -180,10 +191,9 @@ def test_hub_block_concurrent_calls_and_memory():
     setup()
     g = gd.load("hubs")
     csr = csr_of(g)
-    min_degree, min_count = thresholds(csr, 1)
-    kw = dict(cu_count=1, hub_min_degree=min_degree, hub_min_count=min_count)
+    kw = dict(cu_count=1, hub_thresholds=thresholds(csr, 1))
     m = ps.PowerSparseMatrixGPU.from_csr(csr, **kw)
-    assert m.hub_block[0] > 0
+    assert m.hub_block
     N = 128
     B1, B2 = gd.dense(g.cols, N, 11), gd.dense(g.cols, N, 12)
     d1, d2 = ps.DeviceBuffer(host=B1), ps.DeviceBuffer(host=B2)
