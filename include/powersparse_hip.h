@@ -333,15 +333,22 @@ int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, 
  * the stream). */
 int ps_hub_sort_tiles(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
                       uint32_t* tiles, uint32_t tile_count, ps_stream_t stream);
+/* doff[64 t + j] = the dense-element offset (hub index * cols + hot rank) of
+ * the j-th nonzero of listed tile t, in the list's order (run it after
+ * ps_hub_sort_tiles); rows * cols must be below 2^32. */
+int ps_hub_tile_offsets(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
+                        const uint32_t* tiles, uint32_t tile_count, uint32_t* doff,
+                        ps_stream_t stream);
 /* For every listed tile: out[s][p] = sp_data[p] * dot(lhs[group_des[g], :],
  * rhs[col_ind[p], :]) for its 64 nonzeros p, computed as one dense product of
- * the hub rows of lhs with the hot rows of rhs; with out_csr,
+ * the hub rows of lhs with the hot rows of rhs and read back at the tile's
+ * offsets (ps_hub_tile_offsets of the same list); with out_csr,
  * out_csr[out_pos[s][p]] instead. */
 int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
-                        const uint32_t* tiles, uint32_t tile_count, int N, const float* lhs,
-                        const float* rhs, float* const* out, const int* const* out_pos,
-                        float* out_csr, void* workspace, size_t workspace_bytes,
-                        ps_stream_t stream);
+                        const uint32_t* tiles, const uint32_t* doff, uint32_t tile_count, int N,
+                        const float* lhs, const float* rhs, float* const* out,
+                        const int* const* out_pos, float* out_csr, void* workspace,
+                        size_t workspace_bytes, ps_stream_t stream);
 
 /* ---------------------------------------------------------- primitives */
 /* Device-wide exclusive prefix sum of n uint32 values (out may alias in).

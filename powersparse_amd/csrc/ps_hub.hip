@@ -351,53 +351,60 @@ struct SampleArgs {
   uint32_t chunk_log2;
 };
 
-// out[s][p] (or out_csr[out_pos[s][p]]) = sp_data[p] * D[hub_index[row], hot_rank[col]]
-// for the 64 nonzeros p of every listed tile; one wave per kSampleTiles
-// consecutive tiles, each step's loads issued for all of them before any is
-// used (a tile alone leaves the wave waiting on a chain of dependent loads).
-// The list is sorted by hub row and first column, and consecutive workgroups
-// go to one XCD in runs, so each L2 reads a stretch of one D row.
+// out[s][p] (or out_csr[out_pos[s][p]]) = sp_data[p] * D[doff[e]] for the 64
+// nonzeros p of every listed tile t (entry e = 64 t + lane); one wave per
+// kSampleTiles consecutive tiles. The tile codes and the D offsets are
+// independent loads, the values and the D elements the second and last level
+// of the wave's dependent loads (the offsets replace a chain column id ->
+// hot rank and group row -> hub index). The list is sorted by hub row and
+// first column, and consecutive workgroups go to one XCD in runs, so each L2
+// reads a stretch of one D row.
 constexpr int kSampleTiles = 4;
-__global__ __launch_bounds__(kThreads) void sample_kernel(ps_hub_block hb, SampleArgs a,
-                                                           const float* __restrict__ D) {
+__global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a, const float* __restrict__ D,
+                                                           const uint32_t* __restrict__ doff,
+                                                           uint32_t d_elems) {
   const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, a.chunk_log2);
   const uint32_t t0 = (blk * uint32_t(kThreads / kWave) + threadIdx.x / kWave) * kSampleTiles;
   if (t0 >= a.count) return;
-  int q[kSampleTiles];
-  size_t p[kSampleTiles];
-  bool on[kSampleTiles];
+  uint32_t code[kSampleTiles], off[kSampleTiles];
 #pragma unroll
   for (int k = 0; k < kSampleTiles; ++k) {
-    on[k] = t0 + k < a.count;
-    const uint32_t code = on[k] ? a.tiles[t0 + k] : 0u;
-    q[k] = int(code >> kTileBits);
-    p[k] = size_t(code & kTileMask) * 64 + size_t(lane_id());
-  }
-  int c[kSampleTiles], row[kSampleTiles];
-  float val[kSampleTiles];
-#pragma unroll
-  for (int k = 0; k < kSampleTiles; ++k) {
-    const ps_workset& w = a.ws[q[k]];
-    c[k] = on[k] ? w.col_ind[p[k]] : 0;
-    val[k] = on[k] ? w.sp_data[p[k]] : 0.f;
-    row[k] = on[k] ? w.group_des[int(p[k] / size_t(w.group_size))] : 0;
-  }
-  size_t at[kSampleTiles];
-#pragma unroll
-  for (int k = 0; k < kSampleTiles; ++k) {
-    const int i = on[k] ? hb.hub_index[row[k]] : -1;
-    const int h = on[k] ? hb.hot_rank[c[k]] : -1;
-    on[k] = on[k] && i >= 0 && h >= 0;  // listed tiles lie inside the block
-    at[k] = on[k] ? size_t(i) * size_t(hb.cols) + size_t(h) : 0;
+    const bool on = t0 + k < a.count;
+    code[k] = on ? a.tiles[t0 + k] : 0u;
+    off[k] = on ? doff[size_t(t0 + k) * 64 + size_t(lane_id())] : d_elems;
   }
   float v[kSampleTiles];
-#pragma unroll
-  for (int k = 0; k < kSampleTiles; ++k) v[k] = on[k] ? val[k] * D[at[k]] : 0.f;
+  size_t p[kSampleTiles];
 #pragma unroll
   for (int k = 0; k < kSampleTiles; ++k) {
-    if (!on[k]) continue;
-    if (a.out_csr) a.out_csr[a.out_pos[q[k]][p[k]]] = v[k];
-    else a.out[q[k]][p[k]] = v[k];
+    p[k] = size_t(code[k] & kTileMask) * 64 + size_t(lane_id());
+    const bool on = off[k] < d_elems;  // past the list, or not inside the block
+    v[k] = on ? a.ws[code[k] >> kTileBits].sp_data[p[k]] * D[off[k]] : 0.f;
+  }
+#pragma unroll
+  for (int k = 0; k < kSampleTiles; ++k) {
+    if (off[k] >= d_elems) continue;
+    const int q = int(code[k] >> kTileBits);
+    if (a.out_csr) a.out_csr[a.out_pos[q][p[k]]] = v[k];
+    else a.out[q][p[k]] = v[k];
+  }
+}
+
+// doff[64 t + j] = hub_index[row] * cols + hot_rank[col_ind[p]] for the j-th
+// nonzero p of listed tile t (its group's row), or d_elems when that entry
+// lies outside the block.
+__global__ __launch_bounds__(kThreads) void tile_offsets_kernel(ps_hub_block hb, SampleArgs a,
+                                                                 uint32_t* __restrict__ doff,
+                                                                 uint32_t d_elems) {
+  const size_t n = size_t(a.count) * 64;
+  for (size_t e = size_t(blockIdx.x) * kThreads + threadIdx.x; e < n;
+       e += size_t(gridDim.x) * kThreads) {
+    const uint32_t code = a.tiles[e / 64];
+    const ps_workset& w = a.ws[code >> kTileBits];
+    const size_t p = size_t(code & kTileMask) * 64 + e % 64;
+    const int i = hb.hub_index[w.group_des[p / size_t(w.group_size)]];
+    const int h = hb.hot_rank[w.col_ind[p]];
+    doff[e] = i >= 0 && h >= 0 ? uint32_t(i) * uint32_t(hb.cols) + uint32_t(h) : d_elems;
   }
 }
 
@@ -612,13 +619,35 @@ int ps_hub_sort_tiles(const ps_hub_block* hb, int workset_count, const ps_workse
   return PS_OK;
 }
 
-int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
-                        const uint32_t* tiles, uint32_t tile_count, int N, const float* lhs,
-                        const float* rhs, float* const* out, const int* const* out_pos,
-                        float* out_csr, void* workspace, size_t workspace_bytes,
+int ps_hub_tile_offsets(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
+                        const uint32_t* tiles, uint32_t tile_count, uint32_t* doff,
                         ps_stream_t stream) {
   int rc = ps::check_block(hb);
   if (rc != PS_OK) return rc;
+  PS_CHECK_ARG(size_t(hb->rows) * size_t(hb->cols) < (size_t(1) << 32),
+               "hub block: more dense elements than 32-bit offsets address");
+  ps::SampleArgs a;
+  rc = sample_args(hb, workset_count, worksets, tiles, tile_count, &a);
+  if (rc != PS_OK) return rc;
+  if (tile_count == 0) return PS_OK;
+  PS_CHECK_ARG(doff, "ps_hub_tile_offsets: null output");
+  hipStream_t st = ps::to_hip(stream);
+  ps::tile_offsets_kernel<<<ps::grid_for(size_t(tile_count) * 64, ps::kThreads), ps::kThreads, 0,
+                            st>>>(*hb, a, doff, uint32_t(hb->rows) * uint32_t(hb->cols));
+  PS_LAUNCHED();
+  return PS_OK;
+}
+
+int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
+                        const uint32_t* tiles, const uint32_t* doff, uint32_t tile_count, int N,
+                        const float* lhs, const float* rhs, float* const* out,
+                        const int* const* out_pos, float* out_csr, void* workspace,
+                        size_t workspace_bytes, ps_stream_t stream) {
+  int rc = ps::check_block(hb);
+  if (rc != PS_OK) return rc;
+  PS_CHECK_ARG(size_t(hb->rows) * size_t(hb->cols) < (size_t(1) << 32),
+               "hub block: more dense elements than 32-bit offsets address");
+  PS_CHECK_ARG(tile_count == 0 || doff, "ps_hub_sddmm_launch: missing tile offsets");
   PS_CHECK_ARG(N > 0 && N % 32 == 0 && N <= 512,
                "SDDMM requires N to be a multiple of 32 between 32 and 512");
   PS_CHECK_ARG(lhs && rhs && ps::aligned16(lhs) && ps::aligned16(rhs),
@@ -657,7 +686,8 @@ int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_work
   const uint64_t grid = (uint64_t(tile_count) + per_block - 1) / per_block;
   PS_CHECK_ARG(grid < (1ull << 31), "ps_hub_sddmm_launch: too many tiles");
   a.chunk_log2 = uint32_t(ps::task_chunk_log2(PS_TASK_CHUNK_AUTO, grid, ps::kSampleChunkMax));
-  ps::sample_kernel<<<unsigned(grid), ps::kThreads, 0, st>>>(*hb, a, D);
+  ps::sample_kernel<<<unsigned(grid), ps::kThreads, 0, st>>>(a, D, doff,
+                                                              uint32_t(hb->rows) * uint32_t(hb->cols));
   PS_LAUNCHED();
   return PS_OK;
 }

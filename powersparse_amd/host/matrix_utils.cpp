@@ -654,8 +654,8 @@ struct HubTier {
   DeviceArray<uint32_t> stored;
   // the 64-nonzero tiles of the public block groups inside this tier, as
   // (workset << 27) | tile, sorted by hub row and first column (SDDMM writes
-  // them from the dense product)
-  DeviceArray<uint32_t> tiles;
+  // them from the dense product), and each of their nonzeros' dense offset
+  DeviceArray<uint32_t> tiles, doff;
 };
 
 struct PowerSparseMatrixGPU::HubState {
@@ -920,6 +920,9 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
     t.tiles.Upload(tiles[k].data(), tiles[k].size());
     ThrowOnError(ps_hub_sort_tiles(&t.desc, S, ws.data(), t.tiles.data(),
                                    uint32_t(tiles[k].size()), nullptr));
+    t.doff.Allocate(tiles[k].size() * 64);
+    ThrowOnError(ps_hub_tile_offsets(&t.desc, S, ws.data(), t.tiles.data(),
+                                     uint32_t(tiles[k].size()), t.doff.data(), nullptr));
   }
   const int k = RunOrderSlot(PS_OP_SDDMM, 32);
   uint32_t count = 0, kept_tasks = 0;
@@ -966,7 +969,7 @@ void PowerSparseMatrixGPU::HubSddmm(int N, const float* lhs, const float* rhs, f
   for (const auto& t : h.tiers)
     if (t->tiles.size())
       ThrowOnError(ps_hub_sddmm_launch(&t->desc, _group_type_num, ws.data(), t->tiles.data(),
-                                       uint32_t(t->tiles.size()), N, lhs, rhs, out,
+                                       t->doff.data(), uint32_t(t->tiles.size()), N, lhs, rhs, out,
                                        csr_out ? _workset_csr_pos : nullptr, csr_out, h.ws.data(),
                                        h.ws.size(), stream));
   ThrowOnError(ps_event_record(h.done, stream));
