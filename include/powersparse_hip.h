@@ -328,9 +328,10 @@ int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, 
                        size_t workspace_bytes, ps_stream_t stream);
 /* The SDDMM tile list of a hub block: tiles[t] = (s << 27) | j names the j-th
  * 64-nonzero tile of block workset s (groups >= 64 nonzeros, every entry
- * inside the block). ps_hub_sort_tiles orders a list by hub row, then by the
- * tile's first column (device memory; allocates temporaries and synchronises
- * the stream). */
+ * inside the block); codes that name no such tile are skipped by the kernels
+ * below and sort last. ps_hub_sort_tiles orders a list by hub row, then by
+ * the tile's first column (device memory; allocates temporaries and
+ * synchronises the stream). */
 int ps_hub_sort_tiles(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
                       uint32_t* tiles, uint32_t tile_count, ps_stream_t stream);
 /* doff[64 t + j] = the dense-element offset (hub index * cols + hot rank) of

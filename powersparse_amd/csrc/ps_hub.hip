@@ -343,6 +343,7 @@ constexpr int kSampleChunkMax = 256;  // XCD runs of the sample kernel (workgrou
 
 struct SampleArgs {
   ps_workset ws[PS_MAX_WORKSETS];  // indexed by workset
+  int workset_count;
   float* out[PS_MAX_WORKSETS];
   const int* out_pos[PS_MAX_WORKSETS];
   float* out_csr;
@@ -350,6 +351,16 @@ struct SampleArgs {
   uint32_t count;
   uint32_t chunk_log2;
 };
+
+// Whether a listed tile names a tile of a block workset (groups of 64 or more
+// nonzeros): other codes are skipped.
+__device__ __forceinline__ bool tile_valid(const SampleArgs& a, uint32_t code) {
+  const uint32_t q = code >> kTileBits;
+  if (q == 0 || q >= uint32_t(a.workset_count)) return false;
+  const ps_workset& w = a.ws[q];
+  return w.group_size >= 64 && (w.group_size & 63) == 0 &&
+         uint64_t(code & kTileMask) < uint64_t(w.group_num) * uint64_t(w.group_size / 64);
+}
 
 // out[s][p] (or out_csr[out_pos[s][p]]) = sp_data[p] * D[doff[e]] for the 64
 // nonzeros p of every listed tile t (entry e = 64 t + lane); one wave per
@@ -392,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(SampleArgs a, const fl
 
 // doff[64 t + j] = hub_index[row] * cols + hot_rank[col_ind[p]] for the j-th
 // nonzero p of listed tile t (its group's row), or d_elems when that entry
-// lies outside the block.
+// lies outside the block or the code names no tile.
 __global__ __launch_bounds__(kThreads) void tile_offsets_kernel(ps_hub_block hb, SampleArgs a,
                                                                  uint32_t* __restrict__ doff,
                                                                  uint32_t d_elems) {
@@ -400,6 +411,10 @@ __global__ __launch_bounds__(kThreads) void tile_offsets_kernel(ps_hub_block hb,
   for (size_t e = size_t(blockIdx.x) * kThreads + threadIdx.x; e < n;
        e += size_t(gridDim.x) * kThreads) {
     const uint32_t code = a.tiles[e / 64];
+    if (!tile_valid(a, code)) {
+      doff[e] = d_elems;
+      continue;
+    }
     const ps_workset& w = a.ws[code >> kTileBits];
     const size_t p = size_t(code & kTileMask) * 64 + e % 64;
     const int i = hb.hub_index[w.group_des[p / size_t(w.group_size)]];
@@ -408,17 +423,22 @@ __global__ __launch_bounds__(kThreads) void tile_offsets_kernel(ps_hub_block hb,
   }
 }
 
-// keys[t] = (hub index of the tile's row << 32) | its first column; vals[t] = code.
+// keys[t] = (hub index of the tile's row << 32) | its first column (all ones
+// for a code that names no tile: it sorts last); vals[t] = code.
 __global__ __launch_bounds__(kThreads) void tile_keys_kernel(ps_hub_block hb, SampleArgs a,
                                                               uint64_t* __restrict__ keys,
                                                               uint32_t* __restrict__ vals) {
   for (uint32_t t = blockIdx.x * kThreads + threadIdx.x; t < a.count; t += gridDim.x * kThreads) {
     const uint32_t code = a.tiles[t];
+    vals[t] = code;
+    if (!tile_valid(a, code)) {
+      keys[t] = ~0ull;
+      continue;
+    }
     const ps_workset& w = a.ws[code >> kTileBits];
     const size_t p = size_t(code & kTileMask) * 64;
     const int i = hb.hub_index[w.group_des[int(p / size_t(w.group_size))]];
     keys[t] = (uint64_t(uint32_t(i)) << 32) | uint32_t(w.col_ind[p]);
-    vals[t] = code;
   }
 }
 
@@ -574,14 +594,14 @@ int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, 
 }
 
 // SampleArgs over the worksets and a tile list, checked.
-static int sample_args(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
-                const uint32_t* tiles, uint32_t tile_count, ps::SampleArgs* a) {
-  (void)hb;
+static int sample_args(int workset_count, const ps_workset* worksets, const uint32_t* tiles,
+                       uint32_t tile_count, ps::SampleArgs* a) {
   PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets,
                "hub block: invalid worksets");
   PS_CHECK_ARG(tile_count == 0 || tiles, "hub block: missing tile list");
   *a = ps::SampleArgs{};
   for (int s = 0; s < workset_count; ++s) a->ws[s] = worksets[s];
+  a->workset_count = workset_count;
   a->tiles = tiles;
   a->count = tile_count;
   return PS_OK;
@@ -592,7 +612,7 @@ int ps_hub_sort_tiles(const ps_hub_block* hb, int workset_count, const ps_workse
   int rc = ps::check_block(hb);
   if (rc != PS_OK) return rc;
   ps::SampleArgs a;
-  rc = sample_args(hb, workset_count, worksets, tiles, tile_count, &a);
+  rc = sample_args(workset_count, worksets, tiles, tile_count, &a);
   if (rc != PS_OK) return rc;
   if (tile_count == 0) return PS_OK;
   const size_t n = tile_count;
@@ -627,7 +647,7 @@ int ps_hub_tile_offsets(const ps_hub_block* hb, int workset_count, const ps_work
   PS_CHECK_ARG(size_t(hb->rows) * size_t(hb->cols) < (size_t(1) << 32),
                "hub block: more dense elements than 32-bit offsets address");
   ps::SampleArgs a;
-  rc = sample_args(hb, workset_count, worksets, tiles, tile_count, &a);
+  rc = sample_args(workset_count, worksets, tiles, tile_count, &a);
   if (rc != PS_OK) return rc;
   if (tile_count == 0) return PS_OK;
   PS_CHECK_ARG(doff, "ps_hub_tile_offsets: null output");
@@ -657,12 +677,15 @@ int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_work
   PS_CHECK_ARG(workspace && workspace_bytes >= ps_hub_workspace_bytes(hb, PS_OP_SDDMM, N),
                "ps_hub_sddmm_launch: workspace too small");
   ps::SampleArgs a;
-  rc = sample_args(hb, workset_count, worksets, tiles, tile_count, &a);
+  rc = sample_args(workset_count, worksets, tiles, tile_count, &a);
   if (rc != PS_OK) return rc;
   if (tile_count == 0) return PS_OK;
   for (int s = 1; s < workset_count; ++s) {
     a.out[s] = out ? out[s] : nullptr;
     a.out_pos[s] = out_pos ? out_pos[s] : nullptr;
+    PS_CHECK_ARG(worksets[s].group_num <= 0 || worksets[s].group_size < 64 ||
+                     (out_csr ? a.out_pos[s] != nullptr : a.out[s] != nullptr),
+                 "ps_hub_sddmm_launch: missing outputs of a block workset");
   }
   a.out_csr = out_csr;
   const size_t R = size_t(hb->rows), H = size_t(hb->cols), k = size_t(N);

@@ -223,3 +223,110 @@ def test_hub_block_concurrent_calls_and_memory():
     ps.synchronize()
     free1, _ = ps.mem_get_info()
     assert free1 >= free0 - (4 << 20), (free0, free1)
+
+
+def test_hub_entry_points_through_the_abi():
+    """The block's C entry points on a block built by hand: SpMM adds exactly
+    the stored block entries' products into the hub rows; SDDMM writes exactly
+    the listed tiles' outputs (exact inputs, bit for bit against numpy) and
+    skips codes that name no tile (residue workset, workset past the count,
+    tile past the workset's end, groups under 64 nonzeros), which sort last."""
+    import ctypes
+    from gpu_util import Uploaded
+    from powersparse_amd import _native, _ptr, _workset_array, _out_array, _hip_call
+    setup()
+    hip = _native.hip()
+    g = gd.load("hubs")
+    csr = csr_of(g)
+    p = g.parts[0]
+    w = oracle.preprocess(g.rows, g.cols, g.row_ptr, g.col_ind, g.values, p.cu)
+    (d, c), = thresholds(csr, p.cu)
+    deg = np.diff(g.row_ptr.astype(np.int64))
+    cnt = np.bincount(g.col_ind, minlength=g.cols)
+    hub_rows = np.flatnonzero(deg >= d).astype(np.int32)
+    hot_cols = np.flatnonzero(cnt >= c).astype(np.int32)
+    hub_index = np.full(g.rows, -1, np.int32)
+    hub_index[hub_rows] = np.arange(hub_rows.size)
+    hot_rank = np.full(g.cols, -1, np.int32)
+    hot_rank[hot_cols] = np.arange(hot_cols.size)
+    R, H = hub_rows.size, hot_cols.size
+    say(f"hand-built block {R} x {H} (degree >= {d}, count >= {c}), S={w.S}")
+    bufs = {k: ps.DeviceBuffer(host=v) for k, v in dict(
+        hub_rows=hub_rows, hub_index=hub_index, hot_cols=hot_cols, hot_rank=hot_rank,
+        row_ptr=g.row_ptr, col_ind=g.col_ind, values=g.values).items()}
+    hb = _native.HubBlock(matrix_rows=g.rows, matrix_cols=g.cols, rows=R, cols=H)
+    for k in ("hub_rows", "hub_index", "hot_cols", "hot_rank"):
+        setattr(hb, k, bufs[k].ptr)
+    dense = ps.DeviceBuffer(R * H * 4)
+    stored = ps.DeviceBuffer(max(hip.ps_hub_stored_words(ctypes.byref(hb)), 1) * 4)
+    hb.dense, hb.stored = dense.ptr, stored.ptr
+    _hip_call(hip.ps_hub_dense_build(ctypes.byref(hb), bufs["row_ptr"].ptr, bufs["col_ind"].ptr,
+                                     bufs["values"].ptr, dense.ptr, stored.ptr, None))
+    rowof = np.repeat(np.arange(g.rows), deg)
+    inblock = (hub_index[rowof] >= 0) & (hot_rank[g.col_ind] >= 0)
+
+    # SpMM: C = 0 + block * B on the hub rows, zero elsewhere
+    N = 64
+    B = gd.dense(g.cols, N, gd.SALT_B)
+    want = np.zeros((g.rows, N))
+    np.add.at(want, rowof[inblock],
+              g.values[inblock].astype(np.float64)[:, None] * B[g.col_ind[inblock]])
+    dB, dC = ps.DeviceBuffer(host=B), ps.DeviceBuffer.zeros(g.rows * N * 4)
+    ws = ps.DeviceBuffer(hip.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SPMM, N))
+    _hip_call(hip.ps_hub_spmm_launch(ctypes.byref(hb), N, dB.ptr, dC.ptr, ws.ptr, ws.nbytes,
+                                     None))
+    ps.synchronize()
+    np.testing.assert_array_equal(dC.download(np.float32).reshape(g.rows, N),
+                                  want.astype(np.float32))
+
+    # SDDMM: the tiles of block groups lying inside the block, plus bad codes
+    up = Uploaded(w)
+    tiles, expect = [], {}
+    X, Y = gd.dense(g.rows, N, gd.SALT_X), gd.dense(g.cols, N, gd.SALT_Y)
+    for s in range(1, w.S):
+        gs = 32 << (s - 1)
+        for grp in range(w.group_num[s] if gs >= 64 else 0):
+            cols_g = w.col[s][grp * gs:(grp + 1) * gs]
+            row = w.des[s][grp]
+            if hub_index[row] < 0 or (hot_rank[cols_g] < 0).any():
+                continue
+            for j in range(gs // 64):
+                tiles.append((s << 27) | (grp * (gs // 64) + j))
+                pos = np.arange(grp * gs + 64 * j, grp * gs + 64 * (j + 1))
+                expect.setdefault(s, []).append(pos)
+    assert tiles, "no block group lies inside the hand-built block"
+    bad = [0 << 27, (w.S << 27) | 0,
+           (w.S - 1 << 27) | (w.group_num[w.S - 1] * ((32 << (w.S - 2)) // 64))]
+    if w.group_num[1]:
+        bad.append((1 << 27) | 0)  # groups of 32 nonzeros
+    listed = np.array(bad[:2] + tiles + bad[2:], np.uint32)
+    dt = ps.DeviceBuffer(host=listed)
+    wa = _workset_array(up.worksets)
+    _hip_call(hip.ps_hub_sort_tiles(ctypes.byref(hb), w.S, wa, dt.ptr, listed.size, None))
+    got_order = dt.download(np.uint32, listed.size)
+    assert sorted(got_order[-len(bad):].tolist()) == sorted(bad)
+    assert sorted(got_order[:len(tiles)].tolist()) == sorted(tiles)
+    doff = ps.DeviceBuffer(listed.size * 64 * 4)
+    _hip_call(hip.ps_hub_tile_offsets(ctypes.byref(hb), w.S, wa, dt.ptr, listed.size, doff.ptr,
+                                      None))
+    sentinel = np.float32(7.0)
+    outs = [ps.DeviceBuffer(host=np.full(max(w.col[s].size, 1), sentinel, np.float32))
+            for s in range(w.S)]
+    wsd = ps.DeviceBuffer(hip.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SDDMM, N))
+    dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
+    _hip_call(hip.ps_hub_sddmm_launch(ctypes.byref(hb), w.S, wa, dt.ptr, doff.ptr, listed.size, N,
+                                      dX.ptr, dY.ptr, _out_array(outs, w.S), None, None,
+                                      wsd.ptr, wsd.nbytes, None))
+    ps.synchronize()
+    for s in range(w.S):
+        out = outs[s].download(np.float32, max(w.col[s].size, 1))[:w.col[s].size]
+        mask = np.zeros(w.col[s].size, bool)
+        for pos in expect.get(s, []):
+            mask[pos] = True
+        gs = 32 << (s - 1) if s else 1
+        rows = w.des[s][np.arange(w.col[s].size) // gs] if s else None
+        if mask.any():
+            r, col, val = rows[mask], w.col[s][mask], w.val[s][mask]
+            dots = (X[r].astype(np.float64) * Y[col]).sum(1) * val
+            np.testing.assert_array_equal(out[mask], dots.astype(np.float32), err_msg=f"ws {s}")
+        assert (out[~mask] == sentinel).all(), f"workset {s}: a position outside the list written"
