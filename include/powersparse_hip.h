@@ -218,14 +218,15 @@ int ps_task_count(int op, int N, int workset_count, const ps_workset* worksets,
  * runs each workset's groups in stored order, one kernel per workset). */
 int ps_task_order_build(int op, int N, int workset_count, const ps_workset* worksets,
                         uint32_t* order, uint32_t count, ps_stream_t stream);
-/* The same order with the tiles of marked groups left out: skip_groups[s]
- * (device, group_num bytes, or NULL; ignored for the residue) marks groups of
- * block workset s, and a tile whose groups are all marked goes to the end of
- * order; *kept receives the number of tasks before them, the task count to
- * pass to ps_sddmm_launch_ordered so that only those run. No reference
- * counterpart. */
+/* The same order with marked tiles left out: skip[s] (device,
+ * ceil(group_num * group_size / 64) bytes, or NULL; ignored for the residue)
+ * marks the 64-nonzero stretches of block workset s (stretch j: stored
+ * positions 64 j .. 64 j + 63), and a tile whose stretches are all marked goes
+ * to the end of order; *kept receives the number of tasks before them, the
+ * task count to pass to ps_sddmm_launch_ordered so that only those run (an
+ * SDDMM tile is one stretch). No reference counterpart. */
 int ps_task_order_build_subset(int op, int N, int workset_count, const ps_workset* worksets,
-                               const uint8_t* const* skip_groups, uint32_t* order, uint32_t count,
+                               const uint8_t* const* skip, uint32_t* order, uint32_t count,
                                uint32_t* kept, ps_stream_t stream);
 
 /* ps_spmm_launch, ps_sddmm_launch and ps_sddmm_csr_launch with the tasks run
@@ -313,10 +314,12 @@ int ps_hub_compact(const ps_hub_block* hb, const int* row_ptr, const int* col_in
  * hub row (the rows of a partition without the block keep accumulating). */
 int ps_hub_mark_atomic(const ps_hub_block* hb, const int* group_des, int group_num,
                        uint8_t* residue_atomic, ps_stream_t stream);
-/* flags[g] = 1 when group g of a block workset of groups >= 64 nonzeros
- * belongs to a hub row and all its columns are hot, else 0. */
-int ps_hub_group_flags(const ps_hub_block* hb, const ps_workset* workset, uint8_t* flags,
-                       ps_stream_t stream);
+/* flags[t] = 1 when the t-th 64-nonzero stretch of a block workset of groups
+ * >= 64 nonzeros (stored positions 64 t .. 64 t + 63, group_num * group_size
+ * / 64 flags) lies inside the block: its group's row is a hub row and all its
+ * columns are hot; else 0. */
+int ps_hub_tile_flags(const ps_hub_block* hb, const ps_workset* workset, uint8_t* flags,
+                      ps_stream_t stream);
 /* Device workspace bytes of ps_hub_spmm_launch (op PS_OP_SPMM) or
  * ps_hub_sddmm_launch (PS_OP_SDDMM) at width N. */
 size_t ps_hub_workspace_bytes(const ps_hub_block* hb, int op, int N);

@@ -161,7 +161,7 @@ HIP_API = [
       c_void_p]),
     ("ps_hub_mark_atomic", ctypes.c_int,
      [ctypes.POINTER(HubBlock), c_void_p, ctypes.c_int, c_void_p, c_void_p]),
-    ("ps_hub_group_flags", ctypes.c_int,
+    ("ps_hub_tile_flags", ctypes.c_int,
      [ctypes.POINTER(HubBlock), ctypes.POINTER(Workset), c_void_p, c_void_p]),
     ("ps_hub_workspace_bytes", ctypes.c_size_t,
      [ctypes.POINTER(HubBlock), ctypes.c_int, ctypes.c_int]),

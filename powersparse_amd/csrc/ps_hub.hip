@@ -15,7 +15,7 @@
 //          that store that column, as in the reference's per-nonzero
 //          products.
 //   SDDMM: D = X[hub_rows] * Y[hot_cols]^T, then every listed tile (64
-//          nonzeros of a block group lying in the block) stores
+//          consecutive nonzeros of a block group lying in the block) stores
 //          sp_data[p] * D[hub_index[row], hot_rank[col_ind[p]]].
 //
 // The GEMMs run through hipBLASLt in FP32 (compute type 32F). The callers
@@ -222,19 +222,20 @@ __global__ __launch_bounds__(kThreads) void compact_kernel(ps_hub_block hb,
   }
 }
 
-// flags[g] = 1 when group g of a block workset (group_size >= 64) belongs to
-// a hub row and every column of it is hot. One wave per group.
-__global__ __launch_bounds__(kThreads) void group_flags_kernel(ps_hub_block hb, ps_workset w,
-                                                                uint8_t* __restrict__ flags) {
+// flags[t] = 1 when the t-th 64-nonzero stretch of a block workset (groups of
+// 64 or more nonzeros, so a stretch lies in one group) lies inside the block:
+// its group's row is a hub row and all its 64 columns are hot. One wave per
+// stretch, one nonzero per lane.
+__global__ __launch_bounds__(kThreads) void tile_flags_kernel(ps_hub_block hb, ps_workset w,
+                                                               uint8_t* __restrict__ flags) {
   const int waves = kThreads / kWave;
-  for (int g = blockIdx.x * waves + threadIdx.x / kWave; g < w.group_num;
-       g += gridDim.x * waves) {
-    bool hot = hb.hub_index[w.group_des[g]] >= 0;
-    const size_t base = size_t(g) * size_t(w.group_size);
-    for (int j = lane_id(); hot && j < w.group_size; j += kWave)
-      if (hb.hot_rank[w.col_ind[base + j]] < 0) hot = false;
+  const size_t tiles = size_t(w.group_num) * size_t(w.group_size / 64);
+  for (size_t t = size_t(blockIdx.x) * waves + threadIdx.x / kWave; t < tiles;
+       t += size_t(gridDim.x) * waves) {
+    const bool hub = hb.hub_index[w.group_des[t * 64 / size_t(w.group_size)]] >= 0;
+    const bool hot = hub && hb.hot_rank[w.col_ind[t * 64 + size_t(lane_id())]] >= 0;
     const bool all = __all(hot ? 1 : 0);
-    if (lane_id() == 0) flags[g] = all ? 1 : 0;
+    if (lane_id() == 0) flags[t] = all ? 1 : 0;
   }
 }
 
@@ -530,18 +531,19 @@ int ps_hub_mark_atomic(const ps_hub_block* hb, const int* group_des, int group_n
   return PS_OK;
 }
 
-int ps_hub_group_flags(const ps_hub_block* hb, const ps_workset* workset, uint8_t* flags,
-                       ps_stream_t stream) {
+int ps_hub_tile_flags(const ps_hub_block* hb, const ps_workset* workset, uint8_t* flags,
+                      ps_stream_t stream) {
   const int rc = ps::check_block(hb);
   if (rc != PS_OK) return rc;
-  PS_CHECK_ARG(workset && flags, "ps_hub_group_flags: bad arguments");
+  PS_CHECK_ARG(workset && flags, "ps_hub_tile_flags: bad arguments");
   PS_CHECK_ARG(workset->group_size >= 64 && (workset->group_size & (workset->group_size - 1)) == 0,
-               "ps_hub_group_flags: block groups of at least 64 nonzeros only");
+               "ps_hub_tile_flags: block groups of at least 64 nonzeros only");
   if (workset->group_num <= 0) return PS_OK;
-  PS_CHECK_ARG(workset->col_ind && workset->group_des, "ps_hub_group_flags: missing workset arrays");
+  PS_CHECK_ARG(workset->col_ind && workset->group_des, "ps_hub_tile_flags: missing workset arrays");
   hipStream_t st = ps::to_hip(stream);
-  ps::group_flags_kernel<<<ps::grid_for(size_t(workset->group_num), ps::kThreads / ps::kWave),
-                           ps::kThreads, 0, st>>>(*hb, *workset, flags);
+  const size_t tiles = size_t(workset->group_num) * size_t(workset->group_size / 64);
+  ps::tile_flags_kernel<<<ps::grid_for(tiles, ps::kThreads / ps::kWave), ps::kThreads, 0, st>>>(
+      *hb, *workset, flags);
   PS_LAUNCHED();
   return PS_OK;
 }

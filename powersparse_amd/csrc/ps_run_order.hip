@@ -28,9 +28,8 @@ constexpr uint32_t kSkipKey = 0xFFFFFFFFu;     // after everything: tiles left o
 
 struct TaskKeyArgs {
   const int* col_ind[PS_MAX_WORKSETS];
-  const uint8_t* skip[PS_MAX_WORKSETS];  // per group: leave its tiles out (or null)
+  const uint8_t* skip[PS_MAX_WORKSETS];  // per 64-nonzero stretch: leave it out (or null)
   uint64_t nnz[PS_MAX_WORKSETS];         // block workset: group_num * group_size
-  int group_size[PS_MAX_WORKSETS];
   uint32_t task_begin[PS_MAX_WORKSETS + 1];
   int residue[PS_MAX_WORKSETS];  // 1 for the residue workset
   int count;
@@ -41,8 +40,8 @@ struct TaskKeyArgs {
 
 // key[t] = the first column of block tile t (its nonzeros are stored columns
 // ascending within each group), kResidueKey for residue tasks, kSkipKey for a
-// block tile whose groups are all marked in skip; val[t] = t. *skipped counts
-// the kSkipKey tiles.
+// block tile whose 64-nonzero stretches are all marked in skip; val[t] = t.
+// *skipped counts the kSkipKey tiles.
 __global__ __launch_bounds__(kThreads) void task_keys_kernel(TaskKeyArgs a, uint32_t* keys,
                                                              uint32_t* vals,
                                                              unsigned int* skipped) {
@@ -59,9 +58,7 @@ __global__ __launch_bounds__(kThreads) void task_keys_kernel(TaskKeyArgs a, uint
         const uint64_t end = first + uint64_t(a.tile_nnz) < a.nnz[q] ? first + a.tile_nnz
                                                                        : a.nnz[q];
         bool all = true;
-        for (uint64_t g = first / uint64_t(a.group_size[q]);
-             all && g <= (end - 1) / uint64_t(a.group_size[q]); ++g)
-          all = a.skip[q][g] != 0;
+        for (uint64_t j = first / 64; all && j <= (end - 1) / 64; ++j) all = a.skip[q][j] != 0;
         if (all) {
           key = kSkipKey;
           atomicAdd(skipped, 1u);
@@ -114,7 +111,6 @@ int task_table(int op, int N, int workset_count, const ps_workset* worksets, Tas
       t = (uint64_t(w.group_num) + shape.residue_groups - 1) / uint64_t(shape.residue_groups);
     }
     a->col_ind[n] = w.col_ind;
-    a->group_size[n] = w.group_size;
     a->nnz[n] = s > 0 ? uint64_t(w.group_num) * uint64_t(w.group_size) : 0;
     a->residue[n] = s == 0;
     a->task_begin[n] = uint32_t(total);
@@ -128,23 +124,23 @@ int task_table(int op, int N, int workset_count, const ps_workset* worksets, Tas
   return PS_OK;
 }
 
-// The locality order of the launch's tasks, those of skipped groups last;
+// The locality order of the launch's tasks, the skipped tiles last;
 // *kept = the tasks before them (all of them without skip flags).
 int build_order(int op, int N, int workset_count, const ps_workset* worksets,
-                const uint8_t* const* skip_groups, uint32_t* order, uint32_t count,
+                const uint8_t* const* skip, uint32_t* order, uint32_t count,
                 uint32_t* kept, ps_stream_t stream) {
   TaskKeyArgs a;
   const int rc = task_table(op, N, workset_count, worksets, &a);
   if (rc != PS_OK) return rc;
   PS_CHECK_ARG(count == a.total, "ps_task_order_build: order holds " + std::to_string(count) +
                                      " tasks, the launch " + std::to_string(a.total));
-  if (skip_groups) {
+  if (skip) {
     // task_table lists the non-empty worksets from the largest group size down
     int n = 0;
     for (int q = 0; q < workset_count; ++q) {
       const int s = workset_count - 1 - q;
       if (worksets[s].group_num <= 0) continue;
-      a.skip[n++] = s > 0 ? skip_groups[s] : nullptr;
+      a.skip[n++] = s > 0 ? skip[s] : nullptr;
     }
   }
   if (kept) *kept = a.total;
@@ -208,10 +204,10 @@ int ps_task_order_build(int op, int N, int workset_count, const ps_workset* work
 }
 
 int ps_task_order_build_subset(int op, int N, int workset_count, const ps_workset* worksets,
-                               const uint8_t* const* skip_groups, uint32_t* order, uint32_t count,
+                               const uint8_t* const* skip, uint32_t* order, uint32_t count,
                                uint32_t* kept, ps_stream_t stream) {
-  PS_CHECK_ARG(skip_groups && kept, "ps_task_order_build_subset: null argument");
-  return ps::build_order(op, N, workset_count, worksets, skip_groups, order, count, kept, stream);
+  PS_CHECK_ARG(skip && kept, "ps_task_order_build_subset: null argument");
+  return ps::build_order(op, N, workset_count, worksets, skip, order, count, kept, stream);
 }
 
 }  // extern "C"

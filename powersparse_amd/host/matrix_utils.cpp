@@ -652,7 +652,7 @@ struct HubTier {
   DeviceArray<int> hub_rows, hub_index, hot_cols, hot_rank;
   DeviceArray<float> dense;
   DeviceArray<uint32_t> stored;
-  // the 64-nonzero tiles of the public block groups inside this tier, as
+  // the 64-nonzero tiles of the public block groups lying inside this tier, as
   // (workset << 27) | tile, sorted by hub row and first column (SDDMM writes
   // them from the dense product), and each of their nonzeros' dense offset
   DeviceArray<uint32_t> tiles, doff;
@@ -866,11 +866,11 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
     ThrowOnError(ps_hub_mark_atomic(&t->desc, part->_group_des[0], part->_group_num[0],
                                     reinterpret_cast<uint8_t*>(part->_residue_atomic), nullptr));
 
-  // SDDMM: the groups inside the block leave the run order; their outputs come
-  // from the dense products.
-  // A tier the cost rule chose serves SDDMM only when its groups inside the
-  // block hold at least kHubSddmmMinFill nonzeros per dense element (its D is
-  // computed whole); explicit tiers serve both operators.
+  // SDDMM: the tiles (64 consecutive nonzeros of a block group) inside the
+  // block leave the run order; their outputs come from the dense products.
+  // A tier the cost rule chose serves SDDMM only when its tiles hold at least
+  // kHubSddmmMinFill nonzeros per dense element (its D is computed whole);
+  // explicit tiers serve both operators.
   std::vector<ps_workset> ws = PublicWorksets();
   const size_t T = hub->tiers.size();
   std::vector<std::vector<uint32_t>> tiles(T);
@@ -879,17 +879,15 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
   for (int s = 1; s < S; ++s) {
     const int G = _group_num[s], GS = GROUP_SIZE(s);
     if (G == 0 || GS < 64) continue;
-    f_dev.Allocate(size_t(G));
+    const size_t n = size_t(G) * size_t(GS / 64);  // 64-nonzero stretches
+    f_dev.Allocate(n);
     for (size_t k = 0; k < T; ++k) {
-      ThrowOnError(ps_hub_group_flags(&hub->tiers[k]->desc, &ws[size_t(s)], f_dev.data(), nullptr));
+      ThrowOnError(ps_hub_tile_flags(&hub->tiers[k]->desc, &ws[size_t(s)], f_dev.data(), nullptr));
       std::vector<uint8_t>& f = flags[k][size_t(s)];
-      f.resize(size_t(G));
+      f.resize(n);
       f_dev.Download(f.data(), f.size());
-      for (int g = 0; g < G; ++g)
-        if (f[size_t(g)])
-          for (int j = 0; j < GS / 64; ++j)
-            tiles[k].push_back((uint32_t(s) << 27) |
-                               (uint32_t(g) * uint32_t(GS / 64) + uint32_t(j)));
+      for (size_t t = 0; t < n; ++t)
+        if (f[t]) tiles[k].push_back((uint32_t(s) << 27) | uint32_t(t));
     }
   }
   for (size_t k = 0; k < T && !forced; ++k) {
@@ -900,17 +898,16 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
   std::vector<DeviceArray<uint8_t>> skip(static_cast<size_t>(S));
   std::vector<const uint8_t*> skip_ptr(static_cast<size_t>(S), nullptr);
   for (int s = 1; s < S; ++s) {
-    const int G = _group_num[s];
-    std::vector<uint8_t> any(static_cast<size_t>(G), 0);
-    bool flagged = false;
+    std::vector<uint8_t> any;
     for (size_t k = 0; k < T; ++k) {
-      if (tiles[k].empty() || flags[k][size_t(s)].empty()) continue;
-      for (int g = 0; g < G; ++g)
-        if (flags[k][size_t(s)][size_t(g)]) any[size_t(g)] = 1, flagged = true;
+      const std::vector<uint8_t>& f = flags[k][size_t(s)];
+      if (tiles[k].empty() || f.empty()) continue;
+      any.resize(f.size(), 0);
+      for (size_t t = 0; t < f.size(); ++t) any[t] |= f[t];
     }
-    if (!flagged) continue;
-    skip[size_t(s)].Allocate(size_t(G));
-    skip[size_t(s)].Upload(any.data(), any.size());  // groups inside an SDDMM tier
+    if (std::find(any.begin(), any.end(), uint8_t(1)) == any.end()) continue;
+    skip[size_t(s)].Allocate(any.size());
+    skip[size_t(s)].Upload(any.data(), any.size());  // tiles inside an SDDMM tier
     skip_ptr[size_t(s)] = skip[size_t(s)].data();
   }
   for (size_t k = 0; k < T; ++k) {

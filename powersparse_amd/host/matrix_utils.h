@@ -76,8 +76,9 @@ constexpr int kTunedSpmmGroupTypes = 3;
 // keeps that block as a dense FP32 matrix and runs it as dense products on
 // the matrix cores (ps_hub_spmm_launch / ps_hub_sddmm_launch), the rest as
 // before: SpMM on a tuned partition of the matrix without the block, SDDMM on
-// the public worksets with the block's groups left out of the run order and
-// their outputs written from the dense product. The block comes in up to
+// the public worksets with the block's tiles (64 consecutive nonzeros of a
+// block group) left out of the run order and their outputs written from the
+// dense product. The block comes in up to
 // kHubMaxTiers tiers of disjoint row ranges, each with its own columns: the
 // first tier is the pair of power-of-two thresholds (row degree >= 2^a,
 // column count >= 2^b) that maximises block nonzeros - kHubDenseCost * rows
@@ -85,16 +86,16 @@ constexpr int kTunedSpmmGroupTypes = 3;
 // next tier takes the rows below 2^a the same way, kept from kHubMinTierGain
 // (kHubDenseCost: the dense element's cost relative to the sparse nonzero it
 // replaces, measured on MI355X). SDDMM computes a tier's dense dots whole and
-// takes from it only the groups lying inside it, so it uses a tier when those
-// hold at least kHubSddmmMinFill nonzeros per dense element (C3: the first
-// tier, 2526 x 72840; the second, rows of degree 1024..16383 x 3578 columns,
-// serves SpMM alone). It is used with the tuned SpMM partition and the locality run
-// order only. Results match the sparse path within FP32 summation order;
+// takes from it only the tiles lying inside it, so it uses a tier when those
+// hold at least kHubSddmmMinFill nonzeros per dense element (C3: both tiers,
+// 2526 x 72840 and rows of degree 1024..16383 x 3578 columns). It is used
+// with the tuned SpMM partition and the locality run order only. Results match the sparse path within FP32 summation order;
 // Inf / NaN in B reach exactly the rows that store their column; rows of the
 // block accumulate into C as the reference's do (they hold more than 32
 // nonzeros). Cost: 4 bytes per block element (dense) plus the tuned
 // partition's own preprocessing (it no longer shares the public one's), and
-// an operator workspace grown on first use (SDDMM: 4 bytes per block element).
+// an operator workspace grown on first use (SDDMM: 4 bytes per element of
+// its largest tier).
 enum class HubBlock { kAuto = 0, kOff = 1 };
 constexpr int kHubMaxTiers = 3;
 constexpr double kHubDenseCost = 0.12, kHubMinGain = 0.05, kHubMinTierGain = 0.02;
