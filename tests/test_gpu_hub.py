@@ -110,6 +110,65 @@ def test_hub_block_exact_on_golden(name, tiers):
     off.close()
 
 
+def tiles_inside(g, p, th):
+    """(tiles inside the block, whole groups inside, groups split) of the
+    block workset tiles (64 consecutive nonzeros of a group of 64+) for the
+    explicit tiers th, computed on the host."""
+    deg = np.diff(g.row_ptr.astype(np.int64))
+    cnt = np.bincount(g.col_ind, minlength=g.cols)
+    inside = whole = split = 0
+    for s in range(1, p.S):
+        gs = 32 << (s - 1)
+        if gs < 64:
+            continue
+        for grp in range(p.group_num[s]):
+            r, hi, ok = p.des[s][grp], np.inf, None
+            for d, c in th:
+                if d <= deg[r] < hi:
+                    ok = cnt[p.col[s][grp * gs:(grp + 1) * gs]] >= c
+                    break
+                hi = d
+            if ok is None:
+                continue
+            t = ok.reshape(-1, 64).all(1)
+            inside += int(t.sum())
+            whole += int(t.all())
+            split += int(t.any() and not t.all())
+    return inside, whole, split
+
+
+def test_hub_block_splits_groups_exactly():
+    """SDDMM takes the tiles of a block group that lie inside the block and
+    leaves the group's other tiles to the sparse kernel: on the hubs fixture
+    with a block that splits groups, every output equals the sparse path's
+    bit for bit (workset and CSR order, SpMM alongside)."""
+    setup()
+    g = gd.load("hubs")
+    p = g.parts[0]
+    th = [(1046, 6)]
+    inside, whole, split = tiles_inside(g, p, th)
+    say(f"hubs with tier {th}: {inside} tiles inside, {whole} whole groups, {split} split")
+    assert split >= 1 and whole >= 1
+    csr = csr_of(g)
+    kw = dict(cu_count=p.cu, csr_positions=True)
+    on = ps.PowerSparseMatrixGPU.from_csr(csr, hub_thresholds=th, **kw)
+    off = ps.PowerSparseMatrixGPU.from_csr(csr, hub_block="off", **kw)
+    assert len(on.hub_block) == 1
+    for N in (32, 64, 128, 256):
+        B, X, Y = (gd.dense(g.cols, N, gd.SALT_B), gd.dense(g.rows, N, gd.SALT_X),
+                   gd.dense(g.cols, N, gd.SALT_Y))
+        a = run_ops(on, g, N, B, X, Y)
+        b = run_ops(off, g, N, B, X, Y)
+        np.testing.assert_array_equal(a[0], b[0], err_msg=f"SpMM N={N}")
+        for s in range(on.GroupTypeNum()):
+            np.testing.assert_array_equal(a[1][s], b[1][s], err_msg=f"SDDMM N={N} ws {s}")
+        np.testing.assert_array_equal(a[2], b[2], err_msg=f"SDDMMToCSR N={N}")
+        if N == g.n:
+            np.testing.assert_array_equal(a[2], g.sddmm_csr)
+    on.close()
+    off.close()
+
+
 def test_hub_block_nonfinite_b():
     """Inf and NaN in B rows of hot and cold columns reach exactly the rows
     that store those columns, as without the block (0 * Inf never leaks into
