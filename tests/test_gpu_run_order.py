@@ -3,7 +3,9 @@ the order is a permutation of the launch's tasks with block tiles sorted
 stably by their first column and the residue tasks last as stored; the
 operators give the same results in it as in the stored order (SDDMM bitwise,
 SpMM within the FP32 tolerance) and against the oracle; any permutation gives
-those results; a task count that does not match the launch is rejected."""
+those results; a task count that does not match the launch is rejected; the
+subset order leaves out the tasks of marked stretches and SDDMM on its prefix
+writes exactly the other tasks' outputs."""
 import ctypes
 
 import numpy as np
@@ -203,3 +205,80 @@ def test_any_permutation_gives_the_same_results():
         S, arr, m.ResidueOffset(), m.ResidueAtomic(), csr.rows, csr.cols, 32, dB.ptr, C.ptr,
         -2, perm.ptr, count.value, None)
     assert rc == _native.PS_ERR_INVALID and b"task_chunk" in _native.hip().ps_last_error()
+
+
+@pytest.mark.parametrize("op,N", [("sddmm", 64), ("spmm", 32)])
+def test_subset_order_leaves_out_marked_stretches(op, N):
+    """ps_task_order_build_subset: with random 64-nonzero stretches marked, the
+    tasks whose stretches are all marked go last and the rest keep the full
+    order's sequence; *kept counts them. SDDMM run on that prefix writes
+    exactly the unmarked tasks' outputs, bitwise those of the full launch."""
+    setup()
+    csr = ps.synth("C1", seed=46, scale=100)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=8, task_order="signature",
+                                         run_order=False)
+    S, arr = m.GroupTypeNum(), worksets(m)
+    tile, _ = SHAPES[(op, N)]
+    rng = np.random.default_rng(11)
+    marks, dev = [None] * S, [None] * S
+    for s in range(1, S):
+        nnz = m.GroupNum()[s] * (32 << (s - 1))
+        if nnz == 0:
+            continue
+        f = (rng.random(-(-nnz // 64)) < 0.6).astype(np.uint8)
+        f[: max(1, f.size // 8)] = 1  # a run of marked stretches: whole tiles at any tile size
+        marks[s], dev[s] = f, ps.DeviceBuffer(host=f)
+    skip = (ctypes.c_void_p * S)(*[d.ptr if d is not None else None for d in dev])
+    full, n = build_order(m, op, N)
+    sub = ps.DeviceBuffer(max(n, 1) * 4)
+    kept = ctypes.c_uint32()
+    ps._hip_call(_native.hip().ps_task_order_build_subset(op_code(op), N, S, arr, skip, sub.ptr, n,
+                                                          ctypes.byref(kept), None))
+    tasks = launch_tasks(m, op, N)
+    begin = {}
+    for i, (s, t, _) in enumerate(tasks):
+        begin.setdefault(s, i)
+
+    def left_out(task):
+        s, t, _ = tasks[task]
+        if s == 0 or marks[s] is None:
+            return False
+        first, end = t * tile, min((t + 1) * tile, marks[s].size * 64)
+        return bool(marks[s][first // 64:(end - 1) // 64 + 1].all())
+
+    full_order = full.download(np.uint32, n).tolist()
+    order = sub.download(np.uint32, n).tolist()
+    want_kept = [t for t in full_order if not left_out(t)]
+    say(f"subset {op} N={N}: {n} tasks, {kept.value} kept")
+    assert 0 < kept.value < n and kept.value == len(want_kept)
+    assert order[:kept.value] == want_kept
+    assert sorted(order[kept.value:]) == sorted(t for t in range(n) if left_out(t))
+    if op != "sddmm":
+        return
+    X = rng.normal(size=(csr.rows, N)).astype(np.float32)
+    Y = rng.normal(size=(csr.cols, N)).astype(np.float32)
+    dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
+    sizes = m.sddmm_output_sizes()
+    sentinel = np.float32(-3.5)
+
+    def run(order_buf, count):
+        outs = [ps.DeviceBuffer(host=np.full(max(k, 1), sentinel, np.float32)) for k in sizes]
+        oa = (ctypes.c_void_p * S)(*[o.ptr for o in outs])
+        ps._hip_call(_native.hip().ps_sddmm_launch_ordered(
+            S, arr, m.ResidueOffset(), csr.rows, csr.cols, N, dX.ptr, dY.ptr, oa,
+            _native.PS_TASK_CHUNK_AUTO, order_buf.ptr, count, None))
+        ps.synchronize()
+        return [o.download(np.float32, k) for o, k in zip(outs, sizes)]
+
+    whole, part = run(full, n), run(sub, kept.value)
+    for s in range(S):
+        if sizes[s] == 0:
+            continue
+        written = np.ones(sizes[s], bool)
+        if s > 0 and marks[s] is not None:
+            for i, (q, t, _) in enumerate(tasks):
+                if q == s and left_out(i):
+                    written[t * tile:(t + 1) * tile] = False
+        np.testing.assert_array_equal(part[s][written].view(np.uint32),
+                                      whole[s][written].view(np.uint32), err_msg=f"ws {s}")
+        assert (part[s][~written] == sentinel).all(), f"ws {s}: a left-out task wrote"
