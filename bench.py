@@ -25,7 +25,10 @@ exchanges with the memory fabric (Infinity Cache and HBM; calibrated
 FETCH_SIZE + WRITE_SIZE; the hub block's GEMM and sampling kernels are not
 counted), taken from the committed rocprofv3 summary of the same workload
 when that summary was made from the current kernel sources (else null);
-`traffic_GBps` is that byte count over this run's call time.
+`traffic_GBps` is that byte count over this run's call time;
+`profile_call_kernel_us` is the summed duration of one call's kernels in
+that summary's traced bench run (`profile_call_kernels` of them: the sparse
+launch and the hub block's kernels), to compare with `call_us`.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3]
 """
@@ -80,7 +83,12 @@ def measured_counters(config, op, n):
         return None, {}, rel, "profile summary made from other kernel sources: not used"
     key = f"{op}_N{n}"
     traffic = summary.get("traffic", {}).get(key, {}).get("traffic_bytes")
-    counters = summary.get("counters", {}).get(key, {})
+    counters = dict(summary.get("counters", {}).get(key, {}))
+    # the traced bench run's kernels of one call, summed (the call time this
+    # run measures with events should agree)
+    call = summary.get("operators", {}).get(key, {})
+    counters["profile_call_kernel_us"] = call.get("kernel_us_per_call")
+    counters["profile_call_kernels"] = call.get("kernels_per_call")
     return traffic, counters, rel, "from the profile summary of the same kernel sources"
 
 
@@ -288,6 +296,9 @@ def main():
                      "l2_hit_pct": counters.get("l2_hit_pct"),
                      "valu_busy_pct": counters.get("valu_busy_pct"),
                      "valu_utilization_pct": counters.get("valu_utilization_pct"),
+                     "call_us": dom["ms"] * 1e3,
+                     "profile_call_kernel_us": counters.get("profile_call_kernel_us"),
+                     "profile_call_kernels": counters.get("profile_call_kernels"),
                      "traffic_source": traffic_src, "traffic_note": traffic_note},
         "cpu_baseline": cpu,
     }

@@ -266,6 +266,36 @@ def read_trace(db):
     return sorted(out, key=lambda r: -r[2] * r[3])
 
 
+def read_dispatches(db):
+    """(kernel, grid, duration in us) of every dispatch, in start order."""
+    con = sqlite3.connect(db)
+    cols = [d[0] for d in con.execute("select * from kernels limit 1").description]
+    order = "start" if "start" in cols else "rowid"
+    rows = con.execute(f"select name, grid_x * grid_y * grid_z, duration from kernels "
+                       f"order by {order}").fetchall()
+    return [(short_name(n), int(g), float(d) / 1e3) for n, g, d in rows]
+
+
+def operator_calls(dispatches, ops):
+    """{op_N: (calls, kernels per call, mean summed kernel time per call in us)}.
+    A call is an operator kernel's dispatch with the dispatches after it up to
+    the next operator kernel (the dense hub block's kernels follow the sparse
+    launch); calls take the workload's operators in turn."""
+    calls = []
+    for k, _, d in dispatches:
+        if kernel_op(k) is not None:
+            calls.append([d])
+        elif calls:
+            calls[-1].append(d)
+    out = {}
+    for i, (op, n) in enumerate(ops):
+        mine = calls[i::len(ops)]
+        if mine:
+            out[f"{op}_N{n}"] = (len(mine), max(len(c) for c in mine),
+                                 sum(sum(c) for c in mine) / len(mine))
+    return out
+
+
 def operator_runs(dispatches):
     """Groups operator-kernel dispatches into runs of equal (kernel, grid), in
     order: one run per operator of the workload."""
@@ -298,6 +328,18 @@ def summarize(args):
                                   "mean_us": avg})
     for name, grid, calls, avg in trace[:25]:
         lines.append(f"| `{name}` | {grid} | {calls} | {avg:.1f} |")
+    per_op = operator_calls(read_dispatches(args.trace), CONFIG_OPS[args.config])
+    if per_op:
+        # what bench.py times with events around each call: the sparse launch
+        # and, with the dense hub block, its GEMM, gather and sampling kernels
+        lines += ["", "| operator | calls | kernels per call | summed kernel time per call (us) |",
+                  "|---|---|---|---|"]
+        result["operators"] = {}
+        for key, (calls, kernels, us) in per_op.items():
+            result["operators"][key] = {"calls": calls, "kernels_per_call": kernels,
+                                        "kernel_us_per_call": us}
+            op, n = key.rsplit("_N", 1)
+            lines.append(f"| {op} N={n} | {calls} | {kernels} | {us:.1f} |")
     if args.fetch and args.write:
         fetch = read_counters(args.fetch, "FETCH_SIZE")
         write = read_counters(args.write, "WRITE_SIZE")

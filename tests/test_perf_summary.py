@@ -134,3 +134,19 @@ def test_bench_one_gpu_only():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU only" in r.stderr
+
+
+def test_operator_calls_take_the_hub_kernels_that_follow():
+    """A call is the operator kernel's dispatch plus the dispatches after it up
+    to the next operator kernel; calls take the workload's operators in turn;
+    dispatches before the first operator kernel belong to no call."""
+    GEMM = "Cijk_Ailk_Bljk_S_B"
+    SAMPLE = "void ps::(anonymous namespace)::sample_kernel(ps::SampleArgs, float const*)"
+    seq = [(PRE, 4096, 50.0)]
+    for _ in range(3):  # three steps of C3: SpMM 32, SpMM 128, SDDMM 128
+        seq += [(SPMM32, 1000, 1300.0), (GEMM, 64, 140.0), (GEMM, 64, 60.0),
+                (SPMM128, 4000, 5100.0), (GEMM, 64, 340.0),
+                (SDDMM128, 3000, 5500.0), (GEMM, 64, 430.0), (SAMPLE, 512, 340.0)]
+    got = perf.operator_calls(seq, [("spmm", 32), ("spmm", 128), ("sddmm", 128)])
+    assert got == {"spmm_N32": (3, 3, 1500.0), "spmm_N128": (3, 2, 5440.0),
+                   "sddmm_N128": (3, 3, 6270.0)}
