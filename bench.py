@@ -238,6 +238,9 @@ def main():
             f"{detail[-1]['alg_GBps']:.0f} GB/s ({100 * detail[-1]['roofline_frac']:.1f}% of 8 TB/s)")
     dom = max(detail, key=lambda d: d["ms"])
     kernel = "ps::spmm_kernel" if dom["op"] == "spmm" else "ps::sddmm_kernel"
+    if m.hub_block:
+        kernel += (" + the hub block's row gathers, GEMMs (hipBLASLt) and "
+                   + ("row updates" if dom["op"] == "spmm" else "sampling"))
     traffic, counters, traffic_src, traffic_note = measured_counters(args.config, dom["op"],
                                                                       dom["N"])
 
