@@ -389,3 +389,31 @@ def test_hub_entry_points_through_the_abi():
             dots = (X[r].astype(np.float64) * Y[col]).sum(1) * val
             np.testing.assert_array_equal(out[mask], dots.astype(np.float32), err_msg=f"ws {s}")
         assert (out[~mask] == sentinel).all(), f"workset {s}: a position outside the list written"
+
+
+@pytest.mark.parametrize("th", [[(1, 1)], [(64, 1)]])
+def test_hub_block_falls_back_when_it_would_hold_everything(th):
+    """Explicit tiers that leave no nonzero ((1, 1): every row, every column)
+    or only one workset's worth ((64, 1): 586 nonzeros of the light rows) to
+    the sparse path: the build keeps no block and the operators give the
+    block-free results bit for bit."""
+    setup()
+    g = gd.load("hubs")
+    p = g.parts[0]
+    csr = csr_of(g)
+    on = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=p.cu, hub_thresholds=th,
+                                          csr_positions=True)
+    off = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=p.cu, hub_block="off",
+                                           csr_positions=True)
+    say(f"hubs with tiers {th}: block {on.hub_block}")
+    assert on.hub_block == []
+    N = 64
+    B, X, Y = (gd.dense(g.cols, N, gd.SALT_B), gd.dense(g.rows, N, gd.SALT_X),
+               gd.dense(g.cols, N, gd.SALT_Y))
+    a, b = run_ops(on, g, N, B, X, Y), run_ops(off, g, N, B, X, Y)
+    np.testing.assert_array_equal(a[0], b[0])
+    for s in range(on.GroupTypeNum()):
+        np.testing.assert_array_equal(a[1][s], b[1][s])
+    np.testing.assert_array_equal(a[2], b[2])
+    on.close()
+    off.close()
