@@ -5,7 +5,11 @@ products and the rest on the sparse paths; the results must equal those of
 the same matrix without the block. On the golden fixtures' exact inputs
 (sparse values k/64, dense values k/16: every FP32 partial sum exact) the
 comparison is bit for bit, for SpMM over repeated calls (the block's rows
-accumulate), SDDMM in workset and CSR order, and SpMM with Inf / NaN in B."""
+accumulate), SDDMM in workset and CSR order (also with a block that splits
+block groups between the dense and the sparse path), SpMM with Inf / NaN in
+B, and explicit tiers that would leave the sparse path nothing (no block is
+kept). Scaled power-law graphs are checked against the oracle within the
+FP32 tolerance, and the block's C entry points on a hand-built block."""
 import numpy as np
 import pytest
 
