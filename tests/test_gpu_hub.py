@@ -421,3 +421,49 @@ def test_hub_block_falls_back_when_it_would_hold_everything(th):
     np.testing.assert_array_equal(a[2], b[2])
     on.close()
     off.close()
+
+
+def test_hub_block_matrices_from_several_host_threads():
+    """Four host threads each build a matrix with a hub block and run SpMM
+    and SDDMM on it at once (the GEMM plans and the library handle are shared
+    per device): every thread's outputs equal the same calls made from one
+    thread, bit for bit."""
+    import threading
+    setup()
+    g = gd.load("hubs")
+    p = g.parts[0]
+    csr = csr_of(g)
+    th = thresholds(csr, p.cu)
+    N = 128
+    inputs = [(gd.dense(g.cols, N, 20 + k), gd.dense(g.rows, N, 30 + k),
+               gd.dense(g.cols, N, 40 + k)) for k in range(4)]
+
+    def work(k, out):
+        m = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=p.cu, hub_thresholds=th,
+                                             csr_positions=True)
+        assert m.hub_block
+        out[k] = run_ops(m, g, N, *inputs[k], calls=2)
+        m.close()
+
+    seq = {}
+    for k in range(4):
+        work(k, seq)
+    par, errors = {}, []
+
+    def guarded(k):
+        try:
+            work(k, par)
+        except Exception as e:  # reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=guarded, args=(k,)) for k in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for k in range(4):
+        np.testing.assert_array_equal(par[k][0], seq[k][0], err_msg=f"thread {k} SpMM")
+        for a, b in zip(par[k][1], seq[k][1]):
+            np.testing.assert_array_equal(a, b, err_msg=f"thread {k} SDDMM")
+        np.testing.assert_array_equal(par[k][2], seq[k][2], err_msg=f"thread {k} SDDMMToCSR")
