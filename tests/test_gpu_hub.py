@@ -467,3 +467,37 @@ def test_hub_block_matrices_from_several_host_threads():
         for a, b in zip(par[k][1], seq[k][1]):
             np.testing.assert_array_equal(a, b, err_msg=f"thread {k} SDDMM")
         np.testing.assert_array_equal(par[k][2], seq[k][2], err_msg=f"thread {k} SDDMMToCSR")
+
+
+def test_hub_auto_rule_on_c3():
+    """The cost rule on the full C3 graph keeps two tiers, rows of degree >=
+    16384 x columns >= 512 and rows of degree 1024..16383 x columns >= 8192,
+    and each beats its neighbouring power-of-two thresholds on the rule's
+    gain (block nonzeros - 0.12 x rows x columns), counted directly from the
+    CSR arrays here; both gains clear the rule's 5% / 2% of the nonzeros."""
+    setup()
+    csr = ps.synth("C3", seed=1)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr)
+    say(f"C3 auto hub block: {m.hub_block}")
+    assert m.hub_block == [(2526, 72840), (20713, 3578)]
+    m.close()
+    deg = np.diff(csr.row_ptr.astype(np.int64))
+    cnt = np.bincount(csr.col_ind, minlength=csr.cols)
+    rdeg = np.repeat(deg, deg)   # each nonzero's row degree
+    ccnt = cnt[csr.col_ind]      # each nonzero's column count
+    big = np.iinfo(np.int64).max
+
+    def gain(lo, hi, c):
+        rows = int(((deg >= lo) & (deg < hi)).sum())
+        cols = int((cnt >= c).sum())
+        nz = int(((rdeg >= lo) & (rdeg < hi) & (ccnt >= c)).sum())
+        return nz - 0.12 * rows * cols, rows, cols
+
+    g0, r0, h0 = gain(16384, big, 512)
+    assert (r0, h0) == (2526, 72840) and g0 >= 0.05 * csr.nnz
+    for lo, c in [(8192, 512), (32768, 512), (16384, 256), (16384, 1024)]:
+        assert gain(lo, big, c)[0] <= g0, (lo, c)
+    g1, r1, h1 = gain(1024, 16384, 8192)
+    assert (r1, h1) == (20713, 3578) and g1 >= 0.02 * csr.nnz
+    for lo, c in [(512, 8192), (2048, 8192), (1024, 4096), (1024, 16384)]:
+        assert gain(lo, 16384, c)[0] <= g1, (lo, c)
