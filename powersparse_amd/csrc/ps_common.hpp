@@ -51,6 +51,10 @@ namespace ps {
 
 constexpr int kWave = 64;
 
+// Clang vector types for __builtin_nontemporal_load of 16-byte elements.
+typedef int iv4 __attribute__((ext_vector_type(4)));
+typedef float fv4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
 // Makes one wave's LDS writes visible to its own later LDS reads.

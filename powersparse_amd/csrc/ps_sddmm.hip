@@ -160,8 +160,12 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     const int row = valid ? ws.group_des[g] : 0;
     int4 c0 = make_int4(0, 0, 0, 0), c1 = make_int4(0, 0, 0, 0);
     if (valid) {
-      c0 = *reinterpret_cast<const int4*>(ws.col_ind + p0);
-      c1 = *reinterpret_cast<const int4*>(ws.col_ind + p0 + 4);
+      // column ids and values are read once per launch: non-temporal, so that
+      // they displace fewer of the L2's Y rows (C3 SDDMM N=128 6.71 -> 6.69 ms)
+      const iv4 x0 = __builtin_nontemporal_load(reinterpret_cast<const iv4*>(ws.col_ind + p0));
+      const iv4 x1 = __builtin_nontemporal_load(reinterpret_cast<const iv4*>(ws.col_ind + p0 + 4));
+      c0 = make_int4(x0.x, x0.y, x0.z, x0.w);
+      c1 = make_int4(x1.x, x1.y, x1.z, x1.w);
     }
 #pragma unroll
     for (int q = 0; q < KQ; ++q) x[q] = X.load(Off(uint32_t(row)) * row_bytes + piece + 128u * q);
@@ -172,7 +176,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     const float dot = slot_transpose_sum(p, sub);
     const int pos = local * 64 + lane;
     if (valid) {
-      const float v = dot * ws.sp_data[pos];
+      const float v = dot * __builtin_nontemporal_load(ws.sp_data + pos);
       if constexpr (kMode == 1) {
         out[out_pos[pos]] = v;
       } else if constexpr (kMode == 2) {

@@ -181,8 +181,12 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs ar
       int4 c = make_int4(0, 0, 0, 0);
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (p < total) {
-        c = *reinterpret_cast<const int4*>(ws.col_ind + p);
-        v = *reinterpret_cast<const float4*>(ws.sp_data + p);
+        // read once per launch: non-temporal, so that they displace fewer of
+        // the L2's B rows (C3 SpMM N=32 / 128: 1.645 / 5.671 -> 1.625 / 5.602 ms)
+        const iv4 ci = __builtin_nontemporal_load(reinterpret_cast<const iv4*>(ws.col_ind + p));
+        const fv4 vi = __builtin_nontemporal_load(reinterpret_cast<const fv4*>(ws.sp_data + p));
+        c = make_int4(ci.x, ci.y, ci.z, ci.w);
+        v = make_float4(vi.x, vi.y, vi.z, vi.w);
       }
       const int k = lane * 4, q = k / kPer, j = k % kPer;
       int4* dst = reinterpret_cast<int4*>(my_lds + q * kSlotWords + 2 * j);
