@@ -239,8 +239,9 @@ def main():
     dom = max(detail, key=lambda d: d["ms"])
     kernel = "ps::spmm_kernel" if dom["op"] == "spmm" else "ps::sddmm_kernel"
     if m.hub_block:
-        kernel += (" + the hub block's row gathers, GEMMs (hipBLASLt) and "
-                   + ("row updates" if dom["op"] == "spmm" else "sampling"))
+        kernel += (" + the hub block's MFMA kernels ("
+                   + ("B transpose, ps::hub_spmm_kernel, fix-up" if dom["op"] == "spmm"
+                      else "ps::hub_sddmm_kernel") + ")")
     traffic, counters, traffic_src, traffic_note = measured_counters(args.config, dom["op"],
                                                                       dom["N"])
 

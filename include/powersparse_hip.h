@@ -273,13 +273,15 @@ int ps_workset_to_csr(int workset_count, const long long* lengths, const int* co
 
 /* ------------------------------------------------------- dense hub block */
 /* The hub rows (highest degree) restricted to the hot columns (most nonzeros)
- * of a matrix, run as dense FP32 products (hipBLASLt, compute type 32F).
- * All pointers are device memory. hot_rank / hub_index map a matrix column /
- * row to its position in hot_cols / hub_rows, or -1. dense (rows x cols,
- * row-major) holds the block's stored values (repeated entries summed), 0
- * where nothing is stored; stored has one bit per dense element (rows x
- * ceil(cols / 32) words, bit h % 32 of word h / 32) set where an entry is
- * stored. No reference counterpart. */
+ * of a matrix, run as dense FP32 products on the matrix cores (hand-written
+ * v_mfma_f32_32x32x2f32 kernels). All pointers are device memory. hot_rank /
+ * hub_index map a matrix column / row to its position in hot_cols / hub_rows,
+ * or -1 (hot_cols and hub_rows ascending). dense (rows x ps_hub_dense_ld(cols)
+ * floats, row-major, 16-byte aligned) holds the value of every slot stored
+ * exactly once, 0 elsewhere (padding included); stored has one bit per such
+ * slot (rows x ceil(cols / 32) words, bit h % 32 of word h / 32). A slot
+ * stored more than once is left out of the block (no bit, value 0), so its
+ * entries stay on the sparse SpMM path. No reference counterpart. */
 typedef struct ps_hub_block {
   int matrix_rows, matrix_cols;
   int rows;              /* R: hub rows */
@@ -288,7 +290,7 @@ typedef struct ps_hub_block {
   const int* hub_index;  /* [matrix_rows] */
   const int* hot_cols;   /* [H] */
   const int* hot_rank;   /* [matrix_cols] */
-  const float* dense;    /* [R * H] */
+  const float* dense;    /* [R * ps_hub_dense_ld(H)] */
   const uint32_t* stored;
 } ps_hub_block;
 
@@ -299,14 +301,18 @@ int ps_hub_histogram(const int* row_ptr, int rows, const int* col_ind, const int
                      unsigned long long* hist, ps_stream_t stream);
 /* Words of the stored bit mask. */
 size_t ps_hub_stored_words(const ps_hub_block* hb);
-/* Fills dense (rows x cols floats) and stored from the matrix CSR. */
+/* Floats per dense row: cols rounded up to a multiple of 16 (0 for cols <= 0). */
+size_t ps_hub_dense_ld(int cols);
+/* Fills dense and stored from the matrix CSR (finite values), slots stored
+ * more than once left out; the same block on every build. */
 int ps_hub_dense_build(const ps_hub_block* hb, const int* row_ptr, const int* col_ind,
                        const float* sp_data, float* dense, uint32_t* stored, ps_stream_t stream);
-/* counts[r] = stored entries of row r outside the block (matrix_rows values). */
+/* counts[r] = stored entries of row r outside the block's stored slots
+ * (matrix_rows values; run after ps_hub_dense_build). */
 int ps_hub_kept_counts(const ps_hub_block* hb, const int* row_ptr, const int* col_ind,
                        uint32_t* counts, ps_stream_t stream);
-/* The CSR without the block's entries (order within rows kept); new_row_ptr is
- * the exclusive scan of ps_hub_kept_counts. */
+/* The CSR without the entries of the block's stored slots (order within rows
+ * kept); new_row_ptr is the exclusive scan of ps_hub_kept_counts. */
 int ps_hub_compact(const ps_hub_block* hb, const int* row_ptr, const int* col_ind,
                    const float* sp_data, const uint32_t* new_row_ptr, int* new_col,
                    float* new_val, ps_stream_t stream);
@@ -320,39 +326,37 @@ int ps_hub_mark_atomic(const ps_hub_block* hb, const int* group_des, int group_n
  * columns are hot; else 0. */
 int ps_hub_tile_flags(const ps_hub_block* hb, const ps_workset* workset, uint8_t* flags,
                       ps_stream_t stream);
-/* Device workspace bytes of ps_hub_spmm_launch (op PS_OP_SPMM) or
- * ps_hub_sddmm_launch (PS_OP_SDDMM) at width N. */
+/* Device workspace bytes of ps_hub_spmm_launch (op PS_OP_SPMM) at width N:
+ * one feature slice (up to 128) of B's hot rows transposed, and flags. 0 for
+ * PS_OP_SDDMM, which needs none. */
 size_t ps_hub_workspace_bytes(const ps_hub_block* hb, int op, int N);
-/* C[hub_rows[i], :] += sum over stored block entries (i, h) of value * B[hot_cols[h], :],
- * B (matrix_cols x N) and C (matrix_rows x N) row-major; Inf / NaN in B reach
+/* C[hub_rows[i], :] += sum over stored block slots (i, h) of value * B[hot_cols[h], :],
+ * B (matrix_cols x N) and C (matrix_rows x N) row-major, added with float
+ * atomics (other writers of C may run at the same time); Inf / NaN in B reach
  * exactly the rows that store their column. Calls overlapping on one
  * workspace race. */
 int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, void* workspace,
                        size_t workspace_bytes, ps_stream_t stream);
 /* The SDDMM tile list of a hub block: tiles[t] = (s << 27) | j names the j-th
  * 64-nonzero tile of block workset s (groups >= 64 nonzeros, every entry
- * inside the block); codes that name no such tile are skipped by the kernels
- * below and sort last. ps_hub_sort_tiles orders a list by hub row, then by
- * the tile's first column (device memory; allocates temporaries and
- * synchronises the stream). */
-int ps_hub_sort_tiles(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
-                      uint32_t* tiles, uint32_t tile_count, ps_stream_t stream);
-/* doff[64 t + j] = the dense-element offset (hub index * cols + hot rank) of
- * the j-th nonzero of listed tile t, in the list's order (run it after
- * ps_hub_sort_tiles); rows * cols must be below 2^32. */
-int ps_hub_tile_offsets(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
-                        const uint32_t* tiles, uint32_t tile_count, uint32_t* doff,
-                        ps_stream_t stream);
-/* For every listed tile: out[s][p] = sp_data[p] * dot(lhs[group_des[g], :],
- * rhs[col_ind[p], :]) for its 64 nonzeros p, computed as one dense product of
- * the hub rows of lhs with the hot rows of rhs and read back at the tile's
- * offsets (ps_hub_tile_offsets of the same list); with out_csr,
- * out_csr[out_pos[s][p]] instead. */
+ * inside the block); codes that name no such tile, and entries outside the
+ * block, are left out of the plan. The plan (ps_hub_sddmm_plan_bytes bytes of
+ * device memory) groups the listed nonzeros by the dense tile (64 hub rows x
+ * 256 hot columns) they fall in, each with its output position and sp_data;
+ * ps_hub_sddmm_plan allocates temporaries and synchronises the stream. */
+size_t ps_hub_sddmm_plan_bytes(const ps_hub_block* hb, uint32_t tile_count);
+int ps_hub_sddmm_plan(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
+                      const uint32_t* tiles, uint32_t tile_count, void* plan, size_t plan_bytes,
+                      ps_stream_t stream);
+/* For every planned nonzero p of workset s (row group_des[g], column col_ind[p]):
+ * out[s][p] = sp_data[p] * dot(lhs[row, :], rhs[col, :]), the dots taken from
+ * dense tiles of X[hub_rows] * Y[hot_cols]^T computed in registers (never
+ * stored); with out_csr, out_csr[out_pos[s][p]] instead. tile_count is the
+ * plan's list length. No workspace. */
 int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
-                        const uint32_t* tiles, const uint32_t* doff, uint32_t tile_count, int N,
-                        const float* lhs, const float* rhs, float* const* out,
-                        const int* const* out_pos, float* out_csr, void* workspace,
-                        size_t workspace_bytes, ps_stream_t stream);
+                        const void* plan, uint32_t tile_count, int N, const float* lhs,
+                        const float* rhs, float* const* out, const int* const* out_pos,
+                        float* out_csr, ps_stream_t stream);
 
 /* ---------------------------------------------------------- primitives */
 /* Device-wide exclusive prefix sum of n uint32 values (out may alias in).

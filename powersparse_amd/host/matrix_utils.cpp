@@ -652,16 +652,19 @@ struct HubTier {
   DeviceArray<int> hub_rows, hub_index, hot_cols, hot_rank;
   DeviceArray<float> dense;
   DeviceArray<uint32_t> stored;
-  // the 64-nonzero tiles of the public block groups lying inside this tier, as
-  // (workset << 27) | tile, sorted by hub row and first column (SDDMM writes
-  // them from the dense product), and each of their nonzeros' dense offset
-  DeviceArray<uint32_t> tiles, doff;
+  // the SDDMM plan of the 64-nonzero tiles of the public block groups lying
+  // inside this tier (SDDMM writes their outputs from the dense tiles), and
+  // the number of tiles it was built from (0: the tier serves SpMM only)
+  DeviceArray<char> plan;
+  uint32_t plan_tiles = 0;
 };
 
 struct PowerSparseMatrixGPU::HubState {
   std::vector<std::unique_ptr<HubTier>> tiers;
-  // the operator workspace: one call at a time, in GPU order (`done` is
-  // recorded after each call's hub kernels, the next call waits for it)
+  // the SpMM workspace (allocated with the block, sized for the widest
+  // feature slice, so calls allocate nothing): one call at a time, in GPU
+  // order (`done` is recorded after each call's hub kernels, the next call
+  // waits for it). SDDMM needs no workspace.
   std::mutex mu;
   DeviceArray<char> ws;
   ps_event_t done = nullptr;
@@ -669,11 +672,9 @@ struct PowerSparseMatrixGPU::HubState {
   ~HubState() {
     if (done) ps_event_destroy(done);
   }
-  size_t Workspace(int op, int N) const {
+  size_t SpmmWorkspace(int N) const {
     size_t need = 0;
-    for (const auto& t : tiers)
-      if (op == PS_OP_SPMM || t->tiles.size())
-        need = std::max(need, ps_hub_workspace_bytes(&t->desc, op, N));
+    for (const auto& t : tiers) need = std::max(need, ps_hub_workspace_bytes(&t->desc, PS_OP_SPMM, N));
     return need;
   }
 };
@@ -807,7 +808,7 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
     d.hub_index = t->hub_index.data();
     d.hot_cols = t->hot_cols.data();
     d.hot_rank = t->hot_rank.data();
-    t->dense.Allocate(size_t(R) * size_t(H));
+    t->dense.Allocate(size_t(R) * ps_hub_dense_ld(int(H)));
     t->stored.Allocate(ps_hub_stored_words(&d));
     d.dense = t->dense.data();
     d.stored = t->stored.data();
@@ -913,13 +914,13 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
   for (size_t k = 0; k < T; ++k) {
     if (tiles[k].empty()) continue;
     HubTier& t = *hub->tiers[k];
-    t.tiles.Allocate(tiles[k].size());
-    t.tiles.Upload(tiles[k].data(), tiles[k].size());
-    ThrowOnError(ps_hub_sort_tiles(&t.desc, S, ws.data(), t.tiles.data(),
-                                   uint32_t(tiles[k].size()), nullptr));
-    t.doff.Allocate(tiles[k].size() * 64);
-    ThrowOnError(ps_hub_tile_offsets(&t.desc, S, ws.data(), t.tiles.data(),
-                                     uint32_t(tiles[k].size()), t.doff.data(), nullptr));
+    const uint32_t n = uint32_t(tiles[k].size());
+    DeviceArray<uint32_t> codes(n);
+    codes.Upload(tiles[k].data(), n);
+    t.plan.Allocate(ps_hub_sddmm_plan_bytes(&t.desc, n));
+    ThrowOnError(ps_hub_sddmm_plan(&t.desc, S, ws.data(), codes.data(), n, t.plan.data(),
+                                   t.plan.size(), nullptr));
+    t.plan_tiles = n;
   }
   const int k = RunOrderSlot(PS_OP_SDDMM, 32);
   uint32_t count = 0, kept_tasks = 0;
@@ -934,6 +935,8 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
       ThrowOnError(rc);
     }
   }
+  // SpMM workspace for every width (feature slices of at most 128)
+  hub->ws.Allocate(hub->SpmmWorkspace(128));
   ThrowOnError(ps_event_create(&hub->done));
   ps_free(_run_order[k]);
   _run_order[k] = order;
@@ -946,8 +949,8 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
 void PowerSparseMatrixGPU::HubSpmm(int N, const float* B, float* C, ps_stream_t stream) const {
   HubState& h = *_hub;
   std::lock_guard<std::mutex> lock(h.mu);
-  const size_t need = h.Workspace(PS_OP_SPMM, N);
-  if (h.ws.size() < need) h.ws.Allocate(need);  // synchronises the device first
+  if (h.ws.size() < h.SpmmWorkspace(N))  // allocated for every width with the block
+    throw std::logic_error("Hub block SpMM workspace smaller than the block needs");
   if (h.recorded) ThrowOnError(ps_stream_wait_event(stream, h.done));
   for (const auto& t : h.tiers)
     ThrowOnError(ps_hub_spmm_launch(&t->desc, N, B, C, h.ws.data(), h.ws.size(), stream));
@@ -957,20 +960,12 @@ void PowerSparseMatrixGPU::HubSpmm(int N, const float* B, float* C, ps_stream_t 
 
 void PowerSparseMatrixGPU::HubSddmm(int N, const float* lhs, const float* rhs, float* const* out,
                                     float* csr_out, ps_stream_t stream) const {
-  HubState& h = *_hub;
   const std::vector<ps_workset> ws = PublicWorksets();
-  std::lock_guard<std::mutex> lock(h.mu);
-  const size_t need = h.Workspace(PS_OP_SDDMM, N);
-  if (h.ws.size() < need) h.ws.Allocate(need);
-  if (h.recorded) ThrowOnError(ps_stream_wait_event(stream, h.done));
-  for (const auto& t : h.tiers)
-    if (t->tiles.size())
-      ThrowOnError(ps_hub_sddmm_launch(&t->desc, _group_type_num, ws.data(), t->tiles.data(),
-                                       t->doff.data(), uint32_t(t->tiles.size()), N, lhs, rhs, out,
-                                       csr_out ? _workset_csr_pos : nullptr, csr_out, h.ws.data(),
-                                       h.ws.size(), stream));
-  ThrowOnError(ps_event_record(h.done, stream));
-  h.recorded = true;
+  for (const auto& t : _hub->tiers)
+    if (t->plan_tiles)
+      ThrowOnError(ps_hub_sddmm_launch(&t->desc, _group_type_num, ws.data(), t->plan.data(),
+                                       t->plan_tiles, N, lhs, rhs, out,
+                                       csr_out ? _workset_csr_pos : nullptr, csr_out, stream));
 }
 
 std::vector<ps_workset> PowerSparseMatrixGPU::PublicWorksets() const {

@@ -71,14 +71,15 @@ enum class SpmmPartition { kParity = 0, kTuned = 1 };
 constexpr int kTunedSpmmGroupTypes = 3;
 
 // Dense hub block. On power-law graphs the rows of highest degree hold a dense
-// core with the most popular columns (C3: rows of degree >= 4096 x columns
-// with >= 2048 nonzeros, 54 M of the 264 M nonzeros at 43% density). kAuto
-// keeps that block as a dense FP32 matrix and runs it as dense products on
-// the matrix cores (ps_hub_spmm_launch / ps_hub_sddmm_launch), the rest as
-// before: SpMM on a tuned partition of the matrix without the block, SDDMM on
-// the public worksets with the block's tiles (64 consecutive nonzeros of a
-// block group) left out of the run order and their outputs written from the
-// dense product. The block comes in up to
+// core with the most popular columns (C3: rows of degree >= 16384 x columns
+// with >= 512 nonzeros, 70 M of the 264 M nonzeros at 38% density). kAuto
+// keeps that block as a dense FP32 matrix and runs it on the matrix cores
+// with hand-written MFMA kernels (ps_hub_spmm_launch / ps_hub_sddmm_launch),
+// the rest as before: SpMM on a tuned partition of the matrix without the
+// block, SDDMM on the public worksets with the block's tiles (64 consecutive
+// nonzeros of a block group) left out of the run order and their outputs
+// written from dense tiles of the product computed in registers. The block
+// comes in up to
 // kHubMaxTiers tiers of disjoint row ranges, each with its own columns: the
 // first tier is the pair of power-of-two thresholds (row degree >= 2^a,
 // column count >= 2^b) that maximises block nonzeros - kHubDenseCost * rows
@@ -92,10 +93,11 @@ constexpr int kTunedSpmmGroupTypes = 3;
 // with the tuned SpMM partition and the locality run order only. Results match the sparse path within FP32 summation order;
 // Inf / NaN in B reach exactly the rows that store their column; rows of the
 // block accumulate into C as the reference's do (they hold more than 32
-// nonzeros). Cost: 4 bytes per block element (dense) plus the tuned
-// partition's own preprocessing (it no longer shares the public one's), and
-// an operator workspace grown on first use (SDDMM: 4 bytes per element of
-// its largest tier).
+// nonzeros); a (row, column) slot stored more than once stays on the sparse
+// SpMM path. Cost: 4 bytes per block element (dense), 12 bytes per planned
+// SDDMM nonzero, the tuned partition's own preprocessing (it no longer
+// shares the public one's), and an SpMM workspace allocated with the block
+// (128 floats per hot column of the widest tier).
 enum class HubBlock { kAuto = 0, kOff = 1 };
 constexpr int kHubMaxTiers = 3;
 constexpr double kHubDenseCost = 0.12, kHubMinGain = 0.05, kHubMinTierGain = 0.02;
@@ -234,8 +236,9 @@ class PowerSparseMatrixGPU {
   int HubCols(int tier = 0) const;
   // The hub block's part of an operator call, enqueued on `stream` after the
   // sparse part (SpMM: C += block * B; SDDMM: the block groups' outputs, into
-  // out[s] or, with csr_out, into csr_out at the CSR positions). Calls on one
-  // matrix share its operator workspace and run one after another on the GPU.
+  // out[s] or, with csr_out, into csr_out at the CSR positions). SpMM calls on
+  // one matrix share its workspace and run one after another on the GPU;
+  // neither allocates.
   void HubSpmm(int N, const float* B, float* C, ps_stream_t stream) const;
   void HubSddmm(int N, const float* lhs, const float* rhs, float* const* out, float* csr_out,
                 ps_stream_t stream) const;

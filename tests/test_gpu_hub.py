@@ -290,10 +290,11 @@ def test_hub_block_concurrent_calls_and_memory():
 
 def test_hub_entry_points_through_the_abi():
     """The block's C entry points on a block built by hand: SpMM adds exactly
-    the stored block entries' products into the hub rows; SDDMM writes exactly
-    the listed tiles' outputs (exact inputs, bit for bit against numpy) and
-    skips codes that name no tile (residue workset, workset past the count,
-    tile past the workset's end, groups under 64 nonzeros), which sort last."""
+    the products of the block entries whose (row, column) slot is stored once
+    into the hub rows; SDDMM, from a plan of the listed tiles, writes exactly
+    those tiles' outputs (exact inputs, bit for bit against numpy) and skips
+    codes that name no tile (residue workset, workset past the count, tile
+    past the workset's end, groups under 64 nonzeros)."""
     import ctypes
     from gpu_util import Uploaded
     from powersparse_amd import _native, _ptr, _workset_array, _out_array, _hip_call
@@ -320,13 +321,26 @@ def test_hub_entry_points_through_the_abi():
     hb = _native.HubBlock(matrix_rows=g.rows, matrix_cols=g.cols, rows=R, cols=H)
     for k in ("hub_rows", "hub_index", "hot_cols", "hot_rank"):
         setattr(hb, k, bufs[k].ptr)
-    dense = ps.DeviceBuffer(R * H * 4)
+    ld = hip.ps_hub_dense_ld(H)
+    assert ld % 16 == 0 and H <= ld < H + 16
+    dense = ps.DeviceBuffer(R * ld * 4)
     stored = ps.DeviceBuffer(max(hip.ps_hub_stored_words(ctypes.byref(hb)), 1) * 4)
     hb.dense, hb.stored = dense.ptr, stored.ptr
     _hip_call(hip.ps_hub_dense_build(ctypes.byref(hb), bufs["row_ptr"].ptr, bufs["col_ind"].ptr,
                                      bufs["values"].ptr, dense.ptr, stored.ptr, None))
     rowof = np.repeat(np.arange(g.rows), deg)
     inblock = (hub_index[rowof] >= 0) & (hot_rank[g.col_ind] >= 0)
+    # a slot stored more than once stays out of the block
+    slot = rowof.astype(np.int64) * g.cols + g.col_ind
+    _, inv, times = np.unique(slot, return_inverse=True, return_counts=True)
+    once = times[inv] == 1
+    say(f"block entries {int(inblock.sum())}, of them in repeated slots {int((inblock & ~once).sum())}")
+    # the dense rows: stored-once values, zeros elsewhere (padding included)
+    want_dense = np.zeros((R, ld), np.float32)
+    sel = inblock & once
+    want_dense[hub_index[rowof[sel]], hot_rank[g.col_ind[sel]]] = g.values[sel]
+    np.testing.assert_array_equal(dense.download(np.float32, R * ld).reshape(R, ld), want_dense)
+    inblock = sel
 
     # SpMM: C = 0 + block * B on the hub rows, zero elsewhere
     N = 64
@@ -365,21 +379,22 @@ def test_hub_entry_points_through_the_abi():
     listed = np.array(bad[:2] + tiles + bad[2:], np.uint32)
     dt = ps.DeviceBuffer(host=listed)
     wa = _workset_array(up.worksets)
-    _hip_call(hip.ps_hub_sort_tiles(ctypes.byref(hb), w.S, wa, dt.ptr, listed.size, None))
-    got_order = dt.download(np.uint32, listed.size)
-    assert sorted(got_order[-len(bad):].tolist()) == sorted(bad)
-    assert sorted(got_order[:len(tiles)].tolist()) == sorted(tiles)
-    doff = ps.DeviceBuffer(listed.size * 64 * 4)
-    _hip_call(hip.ps_hub_tile_offsets(ctypes.byref(hb), w.S, wa, dt.ptr, listed.size, doff.ptr,
-                                      None))
+    assert hip.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SDDMM, N) == 0
+    plan_bytes = hip.ps_hub_sddmm_plan_bytes(ctypes.byref(hb), listed.size)
+    plan = ps.DeviceBuffer(plan_bytes)
+    _hip_call(hip.ps_hub_sddmm_plan(ctypes.byref(hb), w.S, wa, dt.ptr, listed.size, plan.ptr,
+                                    plan_bytes, None))
+    # the plan's tile table: 64 x 256 dense tiles, the listed entries counted once each
+    T = -(-R // 64) * -(-H // 256)
+    begin = plan.download(np.uint32, T + 1)
+    assert begin[0] == 0 and (np.diff(begin.astype(np.int64)) >= 0).all()
+    assert begin[T] == 64 * len(tiles), (begin[T], len(tiles))
     sentinel = np.float32(7.0)
     outs = [ps.DeviceBuffer(host=np.full(max(w.col[s].size, 1), sentinel, np.float32))
             for s in range(w.S)]
-    wsd = ps.DeviceBuffer(hip.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SDDMM, N))
     dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
-    _hip_call(hip.ps_hub_sddmm_launch(ctypes.byref(hb), w.S, wa, dt.ptr, doff.ptr, listed.size, N,
-                                      dX.ptr, dY.ptr, _out_array(outs, w.S), None, None,
-                                      wsd.ptr, wsd.nbytes, None))
+    _hip_call(hip.ps_hub_sddmm_launch(ctypes.byref(hb), w.S, wa, plan.ptr, listed.size, N,
+                                      dX.ptr, dY.ptr, _out_array(outs, w.S), None, None, None))
     ps.synchronize()
     for s in range(w.S):
         out = outs[s].download(np.float32, max(w.col[s].size, 1))[:w.col[s].size]

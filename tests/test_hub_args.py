@@ -9,7 +9,6 @@ import pytest
 from powersparse_amd import _native
 
 FAKE = 0x10000  # a non-null, 16-byte aligned stand-in address
-BLAS_WS = 32 << 20
 
 
 def r256(b):
@@ -29,17 +28,34 @@ def last_error():
     return _native.hip().ps_last_error().decode()
 
 
+def test_dense_ld_rounds_to_16():
+    lib = _native.hip()
+    assert [lib.ps_hub_dense_ld(c) for c in (0, -3, 1, 15, 16, 17, 70)] == [0, 0, 16, 16, 16, 32, 80]
+
+
 def test_workspace_and_stored_words():
     lib = _native.hip()
     hb = block(rows=5, cols=70)
     assert lib.ps_hub_stored_words(ctypes.byref(hb)) == 5 * 3
     assert lib.ps_hub_stored_words(None) == 0
-    N = 32
-    spmm = r256(70 * N * 4) + r256(5 * N * 4) + r256(70 * 4) + 256 + BLAS_WS
-    sddmm = r256(5 * N * 4) + r256(70 * N * 4) + r256(5 * 70 * 4) + BLAS_WS
-    assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SPMM, N) == spmm
-    assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SDDMM, N) == sddmm
+    ld = 80  # 70 hot columns padded to a multiple of 16
+    for N, slice_ in ((32, 32), (128, 128), (256, 128)):
+        spmm = r256(slice_ * ld * 4) + r256(70 * 4) + 256
+        assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SPMM, N) == spmm
+    # the fused SDDMM kernel keeps its dense tiles in LDS: no workspace
+    assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SDDMM, 32) == 0
     assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SPMM, 0) == 0
+
+
+def test_plan_bytes_follow_the_tile_grid():
+    lib = _native.hip()
+    # 130 hub rows -> 3 row panels of 64; 600 hot columns -> 3 column tiles of 256
+    hb = block(rows=130, cols=600)
+    for tiles in (0, 1, 7):
+        n = 64 * tiles
+        want = r256((3 * 3 + 1) * 4) + r256(n * 8) + r256(n * 4)
+        assert lib.ps_hub_sddmm_plan_bytes(ctypes.byref(hb), tiles) == want
+    assert lib.ps_hub_sddmm_plan_bytes(None, 4) == 0
 
 
 @pytest.mark.parametrize("change,N,ws,msg", [
@@ -63,23 +79,24 @@ def test_spmm_launch_rejects_null_descriptor_and_misaligned_operands():
     hb = block()
     assert lib.ps_hub_spmm_launch(ctypes.byref(hb), 32, FAKE + 4, FAKE, FAKE, 1 << 40, None) == \
         _native.PS_ERR_INVALID and "16-byte aligned" in last_error()
+    hb = block(dense=FAKE + 4)
+    assert lib.ps_hub_spmm_launch(ctypes.byref(hb), 32, FAKE, FAKE, FAKE, 1 << 40, None) == \
+        _native.PS_ERR_INVALID and "16-byte aligned" in last_error()
 
 
-def sddmm(hb, N=32, ws=1 << 40, tiles=FAKE, doff=FAKE, count=1, out=True, worksets=2):
+def sddmm(hb, N=32, plan=FAKE, count=1, out=True, worksets=2):
     lib = _native.hip()
-    w = (_native.Workset * worksets)()
+    w = (_native.Workset * max(worksets, 1))()
     outs = (ctypes.c_void_p * max(worksets, 1))(*([FAKE] * max(worksets, 1)))
-    return lib.ps_hub_sddmm_launch(ctypes.byref(hb), worksets, w, tiles, doff, count, N, FAKE,
-                                   FAKE, outs if out else None, None, None, FAKE, ws, None)
+    return lib.ps_hub_sddmm_launch(ctypes.byref(hb), worksets, w, plan, count, N, FAKE,
+                                   FAKE, outs if out else None, None, None, None)
 
 
 @pytest.mark.parametrize("kw,msg", [
     (dict(N=544), "between 32 and 512"),
     (dict(N=40), "between 32 and 512"),
-    (dict(doff=None), "missing tile offsets"),
-    (dict(tiles=None), "missing tile list"),
+    (dict(plan=None), "missing plan"),
     (dict(out=False), "missing outputs"),
-    (dict(ws=1024), "workspace too small"),
     (dict(worksets=0), "invalid worksets"),
 ])
 def test_sddmm_launch_rejects(kw, msg):
@@ -87,15 +104,18 @@ def test_sddmm_launch_rejects(kw, msg):
     assert rc == _native.PS_ERR_INVALID and msg in last_error()
 
 
-def test_offsets_need_32_bit_dense_elements():
+def test_sddmm_plan_rejects():
     lib = _native.hip()
-    hb = block(rows=1 << 16, cols=1 << 16)  # 2^32 dense elements
-    w = (_native.Workset * 2)()
-    rc = lib.ps_hub_tile_offsets(ctypes.byref(hb), 2, w, FAKE, 1, FAKE, None)
-    assert rc == _native.PS_ERR_INVALID and "32-bit offsets" in last_error()
-    assert sddmm(hb) == _native.PS_ERR_INVALID and "32-bit offsets" in last_error()
     hb = block()
-    assert lib.ps_hub_tile_offsets(ctypes.byref(hb), 2, w, FAKE, 1, None, None) == \
-        _native.PS_ERR_INVALID and "null output" in last_error()
-    # an empty list is a no-op
-    assert lib.ps_hub_tile_offsets(ctypes.byref(hb), 2, w, None, 0, None, None) == _native.PS_OK
+    w = (_native.Workset * 2)()
+    need = lib.ps_hub_sddmm_plan_bytes(ctypes.byref(hb), 1)
+    rc = lib.ps_hub_sddmm_plan(ctypes.byref(hb), 2, w, FAKE, 1, FAKE, need - 1, None)
+    assert rc == _native.PS_ERR_INVALID and "plan buffer too small" in last_error()
+    rc = lib.ps_hub_sddmm_plan(ctypes.byref(hb), 2, w, None, 1, FAKE, need, None)
+    assert rc == _native.PS_ERR_INVALID and "missing tile list" in last_error()
+    rc = lib.ps_hub_sddmm_plan(ctypes.byref(hb), 0, w, FAKE, 1, FAKE, need, None)
+    assert rc == _native.PS_ERR_INVALID and "invalid worksets" in last_error()
+    rc = lib.ps_hub_sddmm_plan(None, 2, w, FAKE, 1, FAKE, need, None)
+    assert rc == _native.PS_ERR_INVALID and "null descriptor" in last_error()
+    # an empty list needs no plan work on the device beyond its empty tile table
+    assert sddmm(hb, plan=None, count=0) == _native.PS_OK
