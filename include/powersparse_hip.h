@@ -276,12 +276,16 @@ int ps_workset_to_csr(int workset_count, const long long* lengths, const int* co
  * of a matrix, run as dense FP32 products on the matrix cores (hand-written
  * v_mfma_f32_32x32x2f32 kernels). All pointers are device memory. hot_rank /
  * hub_index map a matrix column / row to its position in hot_cols / hub_rows,
- * or -1 (hot_cols and hub_rows ascending). dense (rows x ps_hub_dense_ld(cols)
- * floats, row-major, 16-byte aligned) holds the value of every slot stored
- * exactly once, 0 elsewhere (padding included); stored has one bit per such
- * slot (rows x ceil(cols / 32) words, bit h % 32 of word h / 32). A slot
- * stored more than once is left out of the block (no bit, value 0), so its
- * entries stay on the sparse SpMM path. No reference counterpart. */
+ * or -1 (hot_cols and hub_rows ascending). dense (ps_hub_dense_floats(rows,
+ * cols) floats, 16-byte aligned) holds the value of every slot stored exactly
+ * once, 0 elsewhere (padding included), in the matrix cores' fragment order:
+ * with ld = ps_hub_dense_ld(cols), slot (i, h) is element
+ *   ((i / 32) * (ld / 8) + h / 8) * 256 + ((h % 8) / 4) * 128 + (i % 32) * 4 + h % 4
+ * (one 8-column step of 32 rows = 256 consecutive floats, in the order the 64
+ * lanes of a wave load them). stored has one bit per such slot (rows x
+ * ceil(cols / 32) words, bit h % 32 of word h / 32). A slot stored more than
+ * once is left out of the block (no bit, value 0), so its entries stay on the
+ * sparse SpMM path. No reference counterpart. */
 typedef struct ps_hub_block {
   int matrix_rows, matrix_cols;
   int rows;              /* R: hub rows */
@@ -290,7 +294,7 @@ typedef struct ps_hub_block {
   const int* hub_index;  /* [matrix_rows] */
   const int* hot_cols;   /* [H] */
   const int* hot_rank;   /* [matrix_cols] */
-  const float* dense;    /* [R * ps_hub_dense_ld(H)] */
+  const float* dense;    /* [ps_hub_dense_floats(R, H)] */
   const uint32_t* stored;
 } ps_hub_block;
 
@@ -301,8 +305,11 @@ int ps_hub_histogram(const int* row_ptr, int rows, const int* col_ind, const int
                      unsigned long long* hist, ps_stream_t stream);
 /* Words of the stored bit mask. */
 size_t ps_hub_stored_words(const ps_hub_block* hb);
-/* Floats per dense row: cols rounded up to a multiple of 16 (0 for cols <= 0). */
+/* Columns per dense row: cols rounded up to a multiple of 64 (0 for cols <= 0). */
 size_t ps_hub_dense_ld(int cols);
+/* Floats of the dense block: rows rounded up to a multiple of 64, times
+ * ps_hub_dense_ld(cols) (0 for an empty block). */
+size_t ps_hub_dense_floats(int rows, int cols);
 /* Fills dense and stored from the matrix CSR (finite values), slots stored
  * more than once left out; the same block on every build. */
 int ps_hub_dense_build(const ps_hub_block* hb, const int* row_ptr, const int* col_ind,
@@ -326,9 +333,10 @@ int ps_hub_mark_atomic(const ps_hub_block* hb, const int* group_des, int group_n
  * columns are hot; else 0. */
 int ps_hub_tile_flags(const ps_hub_block* hb, const ps_workset* workset, uint8_t* flags,
                       ps_stream_t stream);
-/* Device workspace bytes of ps_hub_spmm_launch (op PS_OP_SPMM) at width N:
- * one feature slice (up to 128) of B's hot rows transposed, and flags. 0 for
- * PS_OP_SDDMM, which needs none. */
+/* Device workspace bytes at width N of ps_hub_spmm_launch (op PS_OP_SPMM: one
+ * feature slice, up to 128, of B's hot rows in fragment order, and flags) or
+ * of ps_hub_sddmm_launch (PS_OP_SDDMM: lhs[hub_rows] and rhs[hot_cols] in
+ * fragment order, rows padded to 64 and 256). */
 size_t ps_hub_workspace_bytes(const ps_hub_block* hb, int op, int N);
 /* C[hub_rows[i], :] += sum over stored block slots (i, h) of value * B[hot_cols[h], :],
  * B (matrix_cols x N) and C (matrix_rows x N) row-major, added with float
@@ -352,11 +360,14 @@ int ps_hub_sddmm_plan(const ps_hub_block* hb, int workset_count, const ps_workse
  * out[s][p] = sp_data[p] * dot(lhs[row, :], rhs[col, :]), the dots taken from
  * dense tiles of X[hub_rows] * Y[hot_cols]^T computed in registers (never
  * stored); with out_csr, out_csr[out_pos[s][p]] instead. tile_count is the
- * plan's list length. No workspace. */
+ * plan's list length; workspace (16-byte aligned) holds the gathered operands
+ * (ps_hub_workspace_bytes(hb, PS_OP_SDDMM, N) bytes). Calls overlapping on
+ * one workspace race. */
 int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
                         const void* plan, uint32_t tile_count, int N, const float* lhs,
                         const float* rhs, float* const* out, const int* const* out_pos,
-                        float* out_csr, ps_stream_t stream);
+                        float* out_csr, void* workspace, size_t workspace_bytes,
+                        ps_stream_t stream);
 
 /* ---------------------------------------------------------- primitives */
 /* Device-wide exclusive prefix sum of n uint32 values (out may alias in).

@@ -169,6 +169,7 @@ HIP_API = [
      [ctypes.POINTER(HubBlock), ctypes.c_int, c_void_p, c_void_p, c_void_p, ctypes.c_size_t,
       c_void_p]),
     ("ps_hub_dense_ld", ctypes.c_size_t, [ctypes.c_int]),
+    ("ps_hub_dense_floats", ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
     ("ps_hub_sddmm_plan_bytes", ctypes.c_size_t, [ctypes.POINTER(HubBlock), ctypes.c_uint32]),
     ("ps_hub_sddmm_plan", ctypes.c_int,
      [ctypes.POINTER(HubBlock), ctypes.c_int, ctypes.POINTER(Workset), c_void_p,
@@ -176,7 +177,7 @@ HIP_API = [
     ("ps_hub_sddmm_launch", ctypes.c_int,
      [ctypes.POINTER(HubBlock), ctypes.c_int, ctypes.POINTER(Workset), c_void_p,
       ctypes.c_uint32, ctypes.c_int, c_void_p, c_void_p, ctypes.POINTER(c_void_p),
-      ctypes.POINTER(c_void_p), c_void_p, c_void_p]),
+      ctypes.POINTER(c_void_p), c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
     ("ps_spmm_launch_ordered", ctypes.c_int,
      [ctypes.c_int, ctypes.POINTER(Workset), c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
       ctypes.c_int, c_void_p, c_void_p, ctypes.c_int, c_void_p, ctypes.c_uint32, c_void_p]),

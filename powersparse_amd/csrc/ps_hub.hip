@@ -8,19 +8,21 @@
 // arithmetic from MFMA tiles with each B / Y row read once per tile.
 //
 //   SpMM:  C[hub_rows[i], :] += sum_h dense[i][h] * B[hot_cols[h], :]
-//          (dense holds the block's stored values, zeros elsewhere). A
-//          pre-pass copies B's hot rows transposed (feature-major, so that
-//          both MFMA operands run along the hot columns) with non-finite
-//          elements replaced by 0; the MFMA kernel splits the hot columns
-//          into chunks, and each workgroup adds its partial rows into C with
-//          float atomics (whole 128-byte row stretches per instruction). A
-//          fix-up adds a * b for every stored block entry whose b is not
-//          finite, so Inf and NaN reach exactly the rows that store that
-//          column, as in the reference's per-nonzero products.
+//          (dense holds the block's stored values, zeros elsewhere, in
+//          fragment order). A pre-pass gathers B's hot rows into the B
+//          operand's fragment order (one feature slice of up to 128 at a
+//          time) with non-finite elements replaced by 0; the MFMA kernel
+//          splits the hot columns into chunks, and each workgroup adds its
+//          partial rows into C with float atomics (whole 128-byte row
+//          stretches per instruction). A fix-up adds a * b for every stored
+//          block entry whose b is not finite, so Inf and NaN reach exactly
+//          the rows that store that column, as in the reference's
+//          per-nonzero products.
 //   SDDMM: the listed tiles (64 consecutive nonzeros of a block group lying
 //          in the block) are planned at build time as per-entry records
 //          grouped by the dense tile (64 hub rows x 256 hot columns) they
-//          fall in. The MFMA kernel computes each dense tile of
+//          fall in. Pre-passes gather X[hub_rows] and Y[hot_cols] into
+//          fragment order; the MFMA kernel computes each dense tile of
 //          D = X[hub_rows] * Y[hot_cols]^T in registers, stages it in LDS and
 //          writes sp_data[p] * D[i][h] to every planned output of the tile:
 //          D never reaches memory.
@@ -29,8 +31,10 @@
 // and B[k][l % 32] for k = l / 32; the 32 x 32 result leaves D[8 j + 4 (l / 32)
 // + i][l % 32] in register 4 j + i of lane l. A k-range of 8 is covered by 4
 // MFMAs in which lane l supplies k = 4 (l / 32) + step: every lane then loads
-// 4 consecutive k of one A row and one B row with a single 128-bit load (both
-// operands are stored with k contiguous), and A and B agree on every k.
+// 4 consecutive k of its A row and B column with a single 128-bit load, and
+// A and B agree on every k. Operands are stored in that order (fragment
+// order, frag_offset below), so a wave's operand load is one contiguous 1 KB
+// read.
 //
 // Repeated entries: a (hub row, hot column) slot stored more than once stays
 // on the sparse SpMM path for all its entries (dense slot 0, no stored bit),
@@ -48,10 +52,24 @@ constexpr int kThreads = 256;
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 inline size_t round256(size_t b) { return (b + 255) & ~size_t(255); }
-// Dense rows are padded with zeros to a multiple of 16 hot columns, so the
-// MFMA kernels' K loops run in steps of 16 without bounds checks.
+// Dense rows are padded with zeros to a multiple of kDenseAlign hot columns,
+// so the SpMM kernel's K loop runs in whole rings of 8-column steps without
+// bounds checks.
+constexpr int kDenseAlign = 64;
 __host__ __device__ inline size_t dense_ld(int cols) {
-  return (size_t(cols) + 15) & ~size_t(15);
+  return (size_t(cols) + kDenseAlign - 1) & ~size_t(kDenseAlign - 1);
+}
+// MFMA fragment order. The kernels' operands are stored so that one 8-column
+// step of a 32-row block is 256 consecutive floats, in the order the 64 lanes
+// load them (lane l: row l % 32, columns 4 (l / 32) .. + 3 of the step), so
+// every operand load is one contiguous 1 KB read. Element (i, h) of a matrix
+// with rows padded to kFragRows and ld columns (a multiple of 8):
+constexpr int kFragRows = 64;
+__host__ __device__ inline size_t frag_offset(size_t i, size_t h, size_t ld) {
+  return ((i / 32) * (ld / 8) + h / 8) * 256 + ((h % 8) / 4) * 128 + (i % 32) * 4 + h % 4;
+}
+__host__ __device__ inline size_t frag_rows(int rows) {
+  return (size_t(rows) + kFragRows - 1) & ~size_t(kFragRows - 1);
 }
 // Bit pattern a repeated slot carries in `dense` between the mark and clear
 // passes of the build (a NaN; the matrix's values are finite).
@@ -133,15 +151,15 @@ __global__ __launch_bounds__(kThreads) void dense_mark_kernel(ps_hub_block hb,
                                                                float* __restrict__ dense,
                                                                uint32_t* __restrict__ stored) {
   const size_t words = (size_t(hb.cols) + 31) / 32, ld = dense_ld(hb.cols);
+  uint32_t* d = reinterpret_cast<uint32_t*>(dense);
   for (int i = blockIdx.x; i < hb.rows; i += gridDim.x) {
     const int r = hb.hub_rows[i];
     uint32_t* srow = stored + size_t(i) * words;
-    uint32_t* drow = reinterpret_cast<uint32_t*>(dense + size_t(i) * ld);
     for (int p = row_ptr[r] + threadIdx.x; p < row_ptr[r + 1]; p += kThreads) {
       const int h = hb.hot_rank[col_ind[p]];
       if (h < 0) continue;
       const uint32_t bit = 1u << (h % 32);
-      if (atomicOr(srow + h / 32, bit) & bit) drow[h] = kRepeated;
+      if (atomicOr(srow + h / 32, bit) & bit) d[frag_offset(i, h, ld)] = kRepeated;
     }
   }
 }
@@ -155,10 +173,11 @@ __global__ __launch_bounds__(kThreads) void dense_fill_kernel(ps_hub_block hb,
   const size_t ld = dense_ld(hb.cols);
   for (int i = blockIdx.x; i < hb.rows; i += gridDim.x) {
     const int r = hb.hub_rows[i];
-    float* drow = dense + size_t(i) * ld;
     for (int p = row_ptr[r] + threadIdx.x; p < row_ptr[r + 1]; p += kThreads) {
       const int h = hb.hot_rank[col_ind[p]];
-      if (h >= 0 && __float_as_uint(drow[h]) != kRepeated) drow[h] = sp_data[p];
+      if (h < 0) continue;
+      float* slot = dense + frag_offset(i, h, ld);
+      if (__float_as_uint(*slot) != kRepeated) *slot = sp_data[p];
     }
   }
 }
@@ -173,11 +192,12 @@ __global__ __launch_bounds__(kThreads) void dense_clear_kernel(ps_hub_block hb,
   for (int i = blockIdx.x; i < hb.rows; i += gridDim.x) {
     const int r = hb.hub_rows[i];
     uint32_t* srow = stored + size_t(i) * words;
-    float* drow = dense + size_t(i) * ld;
     for (int p = row_ptr[r] + threadIdx.x; p < row_ptr[r + 1]; p += kThreads) {
       const int h = hb.hot_rank[col_ind[p]];
-      if (h < 0 || __float_as_uint(drow[h]) != kRepeated) continue;
-      drow[h] = 0.f;  // every entry of the slot writes the same
+      if (h < 0) continue;
+      float* slot = dense + frag_offset(i, h, ld);
+      if (__float_as_uint(*slot) != kRepeated) continue;
+      *slot = 0.f;  // every entry of the slot writes the same
       atomicAnd(srow + h / 32, ~(1u << (h % 32)));
     }
   }
@@ -270,58 +290,59 @@ __global__ __launch_bounds__(kThreads) void mark_atomic_kernel(const int* __rest
 
 // ------------------------------------------------------------- SpMM
 
-__global__ void clear_flag_kernel(int* flag) { *flag = 0; }
-
-// Bt[n][h] = B[hot_cols[h]][f0 + n] for the features [f0, f0 + width) (Bt
-// rows of ld floats; zero for h >= H), non-finite elements replaced by 0;
-// row_flag[h] |= whether the row held a non-finite element there, *any_flag
-// set to 1 if any did. A workgroup moves 64 hot columns x 64 features at a
-// time through LDS (reads along B rows, writes along Bt rows).
-__global__ __launch_bounds__(kThreads) void transpose_hot_kernel(
+// Bt = the slice's B operand in fragment order: element (n, h) = B[hot_cols[h]][f0
+// + n] for the features n < width (a multiple of 32) and hot columns h < ld
+// (0 for h >= H), non-finite elements replaced by 0; row_flag[h] |= whether
+// B's row hot_cols[h] held a non-finite element there, *any_flag set to 1 if
+// any did. Each thread writes one float4 of a 256-float run: lane l of run
+// (32-feature block nb, step ks) holds features nb * 32 + l % 32 at hot
+// columns 8 ks + 4 (l / 32) + c; each of its 4 reads is a 128-byte stretch of
+// a B row shared by 32 lanes.
+__global__ __launch_bounds__(kThreads) void gather_hot_kernel(
     const float* __restrict__ B, const int* __restrict__ hot_cols, int H, int N, int ld, int f0,
     int width, float* __restrict__ Bt, int* __restrict__ row_flag, int* __restrict__ any_flag) {
-  __shared__ float t[64][65];
-  __shared__ int bad[64];
-  const int h0 = blockIdx.x * 64;
-  if (threadIdx.x < 64) bad[threadIdx.x] = 0;
-  for (int n0 = 0; n0 < width; n0 += 64) {
-    const int wn = width - n0 < 64 ? width - n0 : 64;
-    __syncthreads();
-    for (int e = threadIdx.x; e < 64 * 64; e += kThreads) {
-      const int hh = e / 64, nn = e % 64;
-      float v = 0.f;
-      if (h0 + hh < H && nn < wn) {
-        v = B[size_t(hot_cols[h0 + hh]) * size_t(N) + size_t(f0 + n0 + nn)];
-        if (!isfinite(v)) {
-          v = 0.f;
-          bad[hh] = 1;
+  const size_t runs = size_t(width / 32) * size_t(ld / 8);
+  for (size_t q = size_t(blockIdx.x) * kThreads + threadIdx.x; q < runs * 64;
+       q += size_t(gridDim.x) * kThreads) {
+    const size_t run = q / 64;
+    const int l = int(q % 64);
+    const int nb = int(run / size_t(ld / 8)), ks = int(run % size_t(ld / 8));
+    const int n = nb * 32 + l % 32;
+    const int h0 = ks * 8 + 4 * (l / 32);
+    float v[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int h = h0 + c;
+      v[c] = 0.f;
+      if (h < H) {
+        const float x = B[size_t(hot_cols[h]) * size_t(N) + size_t(f0 + n)];
+        if (isfinite(x)) {
+          v[c] = x;
+        } else {
+          row_flag[h] = 1;  // cleared by clear_flags_kernel before the first slice
+          *any_flag = 1;
         }
       }
-      t[hh][nn] = v;
     }
-    __syncthreads();
-    for (int e = threadIdx.x; e < 64 * 64; e += kThreads) {
-      const int nn = e / 64, hh = e % 64;
-      if (nn < wn && h0 + hh < ld) Bt[size_t(n0 + nn) * size_t(ld) + size_t(h0 + hh)] = t[hh][nn];
-    }
+    *reinterpret_cast<float4*>(Bt + run * 256 + size_t(l) * 4) = make_float4(v[0], v[1], v[2], v[3]);
   }
-  __syncthreads();
-  if (threadIdx.x < 64 && h0 + int(threadIdx.x) < H) {
-    const int b = bad[threadIdx.x];
-    if (f0 == 0) row_flag[h0 + threadIdx.x] = b;
-    else if (b) row_flag[h0 + threadIdx.x] = 1;
-    if (b) *any_flag = 1;
-  }
+}
+
+// row_flag[h] = 0 for h < H, *any_flag = 0.
+__global__ __launch_bounds__(kThreads) void clear_flags_kernel(int* __restrict__ row_flag, int H,
+                                                                int* __restrict__ any_flag) {
+  for (int h = blockIdx.x * kThreads + threadIdx.x; h < H; h += gridDim.x * kThreads) row_flag[h] = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *any_flag = 0;
 }
 
 struct HubSpmmArgs {
   const float* dense;
-  const float* Bt;  // kSpSlice (or fewer) feature rows of ld floats
+  const float* Bt;  // the slice's B operand in fragment order (ld columns)
   float* C;
   const int* hub_rows;
   int R, N, ld;
   int f0;        // first feature of this slice
-  int kc;        // hot columns per chunk (multiple of 16)
+  int kc;        // hot columns per chunk (multiple of kDenseAlign)
   int panels;    // row panels of kSpRows rows
   uint32_t chunk_log2;
 };
@@ -330,10 +351,13 @@ struct HubSpmmArgs {
 // slice's 32 CB features, over one chunk of hot columns; the partial rows are
 // added into C with atomics. A (dense) streams from memory once; B (Bt) is
 // the same for the 4 waves of a workgroup and for every row panel of a chunk
-// (neighbouring workgroups take the chunk's panels on one XCD). ST stages of
-// operand loads stay in flight.
-template <int CB, int ST>
+// (neighbouring workgroups take the chunk's panels on one XCD). The operands
+// of 8-column steps go through a ring of RING stages loaded RING - 1 steps
+// ahead; chunks are whole rings (kc and ld are multiples of kDenseAlign), and
+// loads past the chunk's end (never used) read its last step again.
+template <int CB, int RING>
 __global__ __launch_bounds__(kThreads, 2) void hub_spmm_kernel(HubSpmmArgs a) {
+  static_assert(kDenseAlign % (8 * RING) == 0, "chunks must hold whole rings of steps");
   const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, a.chunk_log2);
   const int panel = int(blk % uint32_t(a.panels)), chunk = int(blk / uint32_t(a.panels));
   const int lane = lane_id(), g = lane >> 5, l32 = lane & 31;
@@ -341,49 +365,137 @@ __global__ __launch_bounds__(kThreads, 2) void hub_spmm_kernel(HubSpmmArgs a) {
   const int k0 = chunk * a.kc;
   const int k1 = k0 + a.kc < a.ld ? k0 + a.kc : a.ld;
   if (m0 >= a.R || k0 >= k1) return;
-  // rows past R load row R - 1; their results are never written
+  // operand runs of step 0 (rows past R are zero padding; their results are
+  // never written): step k / 8 is 256 floats further on
+  const size_t steps = size_t(a.ld / 8);
   const float* arow[2];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int m = m0 + rb * 32 + l32;
-    arow[rb] = a.dense + size_t(m < a.R ? m : a.R - 1) * size_t(a.ld) + 4 * g;
-  }
+  for (int rb = 0; rb < 2; ++rb) arow[rb] = a.dense + size_t(m0 / 32 + rb) * steps * 256 + lane * 4;
   const float* brow[CB];
 #pragma unroll
-  for (int cb = 0; cb < CB; ++cb) brow[cb] = a.Bt + size_t(cb * 32 + l32) * size_t(a.ld) + 4 * g;
+  for (int cb = 0; cb < CB; ++cb) brow[cb] = a.Bt + size_t(cb) * steps * 256 + lane * 4;
 
   v16f acc[2][CB];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = v16f{};
-  float4 A[ST][2], Bf[ST][CB];
+  float4 A[RING][2], Bf[RING][CB];
+  const int klast = k1 - 8;
 #pragma unroll
-  for (int s = 0; s < ST; ++s)
-    if (k0 + 8 * s < k1) {
+  for (int s = 0; s < RING - 1; ++s) {
+    const int k = k0 + 8 * s < klast ? k0 + 8 * s : klast;
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) A[s][rb] = load4(arow[rb] + k0 + 8 * s);
+    for (int rb = 0; rb < 2; ++rb) A[s][rb] = load4(arow[rb] + size_t(k) * 32);
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) Bf[s][cb] = load4(brow[cb] + k0 + 8 * s);
-    }
-  for (int h = k0; h < k1; h += 8 * ST) {
+    for (int cb = 0; cb < CB; ++cb) Bf[s][cb] = load4(brow[cb] + size_t(k) * 32);
+    // stages issued in ring order, as the loop issues them
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int h = k0; h < k1; h += 8 * RING) {
 #pragma unroll
-    for (int s = 0; s < ST; ++s) {
-      if (h + 8 * s < k1) {
-        mfma_step<2, CB>(acc, A[s], Bf[s]);
-        const int nh = h + 8 * (s + ST);
-        if (nh < k1) {
+    for (int s = 0; s < RING; ++s) {
+      mfma_step<2, CB>(acc, A[s], Bf[s]);
+      const int ahead = (s + RING - 1) % RING;
+      const int nk = h + 8 * (s + RING - 1);
+      const int k = nk < klast ? nk : klast;
 #pragma unroll
-          for (int rb = 0; rb < 2; ++rb) A[s][rb] = load4(arow[rb] + nh);
+      for (int rb = 0; rb < 2; ++rb) A[ahead][rb] = load4(arow[rb] + size_t(k) * 32);
 #pragma unroll
-          for (int cb = 0; cb < CB; ++cb) Bf[s][cb] = load4(brow[cb] + nh);
-        }
-      }
+      for (int cb = 0; cb < CB; ++cb) Bf[ahead][cb] = load4(brow[cb] + size_t(k) * 32);
+      // keep the loads at this step (the scheduler would sink them towards
+      // their use and shorten the prefetch distance)
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   // C[hub_rows[m]][f0 + 32 cb + l32] += acc: register r of a block holds row
   // 8 (r / 4) + 4 g + r % 4, so each atomic instruction adds two 32-float
   // row stretches.
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int mb = m0 + rb * 32;
+    const int hr = a.hub_rows[mb + l32 < a.R ? mb + l32 : a.R - 1];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int lr = 8 * (r / 4) + 4 * g + (r % 4);
+      const int dst = __shfl(hr, lr);
+      if (mb + lr < a.R) {
+        float* crow = a.C + size_t(dst) * size_t(a.N) + size_t(a.f0 + l32);
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) unsafeAtomicAdd(crow + cb * 32, acc[rb][cb][r]);
+      }
+    }
+  }
+}
+
+// The same product for slices of 64 or more features: the 4 waves share the
+// slice's B fragments, so each wave loads one 32-feature block of every step
+// (G steps ahead, into registers) and the workgroup passes them through a
+// double-buffered LDS stage, one barrier per step; A fragments stream per wave
+// through a ring of RA steps as above. Waves whose 64 rows lie past R compute
+// on row block 0 and write nothing (every wave takes part in the barriers).
+template <int CB, int RA>
+__global__ __launch_bounds__(kThreads, 2) void hub_spmm_lds_kernel(HubSpmmArgs a) {
+  constexpr int G = 4;                               // B steps in flight per wave
+  constexpr int U = RA > G ? RA : G;                 // steps per loop iteration
+  static_assert(U % RA == 0 && U % G == 0 && U % 2 == 0, "ring sizes must divide the unroll");
+  static_assert(kDenseAlign % (8 * U) == 0, "chunks must hold whole iterations");
+  __shared__ float4 bs[2][CB][kWave];
+  const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, a.chunk_log2);
+  const int panel = int(blk % uint32_t(a.panels)), chunk = int(blk / uint32_t(a.panels));
+  const int wave = threadIdx.x / kWave, lane = lane_id(), g = lane >> 5, l32 = lane & 31;
+  const int m0 = panel * kSpRows + wave * 64;
+  const int k0 = chunk * a.kc;
+  const int k1 = k0 + a.kc < a.ld ? k0 + a.kc : a.ld;
+  if (panel * kSpRows >= a.R || k0 >= k1) return;  // uniform over the workgroup
+  const bool active = m0 < a.R;
+  const size_t steps = size_t(a.ld / 8);
+  const float* arow[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+    arow[rb] = a.dense + size_t((active ? m0 / 32 : 0) + rb) * steps * 256 + lane * 4;
+  const bool loader = wave < CB;  // loads B block `wave` of every step
+  const float* bsrc = a.Bt + size_t(loader ? wave : 0) * steps * 256 + lane * 4;
+  const int klast = k1 - 8;
+  auto kclamp = [klast](int k) { return k < klast ? k : klast; };
+
+  v16f acc[2][CB];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = v16f{};
+  float4 A[RA][2], breg[G];
+  // B(0) into LDS slot 0, B(1 .. G) into the register ring (step t in slot t % G)
+  if (loader) {
+    bs[0][wave][lane] = load4(bsrc + size_t(k0) * 32);
+#pragma unroll
+    for (int j = 1; j <= G; ++j) breg[j % G] = load4(bsrc + size_t(kclamp(k0 + 8 * j)) * 32);
+  }
+#pragma unroll
+  for (int j = 0; j < RA - 1; ++j)
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) A[j][rb] = load4(arow[rb] + size_t(kclamp(k0 + 8 * j)) * 32);
+  __syncthreads();
+  for (int h = k0; h < k1; h += 8 * U) {
+#pragma unroll
+    for (int s = 0; s < U; ++s) {
+      const int k = h + 8 * s;  // this step's first hot column
+      float4 bf[CB];
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) bf[cb] = bs[s % 2][cb][lane];
+      if (loader) {
+        bs[(s + 1) % 2][wave][lane] = breg[(s + 1) % G];  // B(t + 1), read after the barrier
+        breg[(s + 1) % G] = load4(bsrc + size_t(kclamp(k + 8 * (G + 1))) * 32);
+      }
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+        A[(s + RA - 1) % RA][rb] = load4(arow[rb] + size_t(kclamp(k + 8 * (RA - 1))) * 32);
+      float4 as[2] = {A[s % RA][0], A[s % RA][1]};
+      mfma_step<2, CB>(acc, as, bf);
+      __syncthreads();
+    }
+  }
+  if (!active) return;
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     const int mb = m0 + rb * 32;
@@ -415,7 +527,7 @@ __global__ __launch_bounds__(kThreads) void fixup_kernel(ps_hub_block hb, const 
     const int r = hb.hub_rows[i];
     for (int h = threadIdx.x; h < hb.cols; h += kThreads) {
       if (!row_flag[h] || !((hb.stored[size_t(i) * words + h / 32] >> (h % 32)) & 1u)) continue;
-      const float a = hb.dense[size_t(i) * ld + h];
+      const float a = hb.dense[frag_offset(i, h, ld)];
       const float* brow = B + size_t(hb.hot_cols[h]) * size_t(N);
       for (int j = 0; j < N; ++j) {
         const float v = brow[j];
@@ -504,131 +616,185 @@ __global__ __launch_bounds__(kThreads) void plan_fill_kernel(Worksets a,
   }
 }
 
+// dst = rows idx[i] of the row-major src (K floats per row, K a multiple of
+// 32) in fragment order with ld = K, for i < padded (a multiple of 32); zero
+// rows for i >= count. Each thread moves one float4.
+__global__ __launch_bounds__(kThreads) void gather_rows_kernel(const float* __restrict__ src,
+                                                                const int* __restrict__ idx,
+                                                                int count, int padded, int K,
+                                                                float* __restrict__ dst) {
+  const size_t steps = size_t(K / 8);
+  const size_t n = size_t(padded / 32) * steps * 64;
+  for (size_t q = size_t(blockIdx.x) * kThreads + threadIdx.x; q < n;
+       q += size_t(gridDim.x) * kThreads) {
+    const size_t run = q / 64;
+    const int l = int(q % 64);
+    const int i = int(run / steps) * 32 + l % 32;
+    const int k = int(run % steps) * 8 + 4 * (l / 32);
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < count) v = load4(src + size_t(idx[i]) * size_t(K) + size_t(k));
+    *reinterpret_cast<float4*>(dst + run * 256 + size_t(l) * 4) = v;
+  }
+}
+
 struct HubSddmmArgs {
-  const float* X;
-  const float* Y;
+  const float* Xf;  // X[hub_rows], fragment order, rows padded to kSdRows
+  const float* Yf;  // Y[hot_cols], fragment order, rows padded to kSdCols
   int K;
-  const int* hub_rows;
-  const int* hot_cols;
-  int R, H;
   const uint32_t* tile_begin;
   const uint64_t* entries;
   const float* values;
   int tiles_r, tiles_c;
   int range;  // column tiles per workgroup
   uint32_t chunk_log2;
-  int S;
   float* out[PS_MAX_WORKSETS];
   const int* out_pos[PS_MAX_WORKSETS];
   float* out_csr;
 };
 
-__device__ __forceinline__ float* out_of(const HubSddmmArgs& a, int s) {
-  float* p = a.out[0];
-#pragma unroll
-  for (int q = 1; q < PS_MAX_WORKSETS; ++q) {
-    if (q >= a.S) break;
-    if (s == q) p = a.out[q];
-  }
-  return p;
-}
-__device__ __forceinline__ const int* pos_of(const HubSddmmArgs& a, int s) {
-  const int* p = a.out_pos[0];
-#pragma unroll
-  for (int q = 1; q < PS_MAX_WORKSETS; ++q) {
-    if (q >= a.S) break;
-    if (s == q) p = a.out_pos[q];
-  }
-  return p;
-}
-
 // One workgroup: the dense tiles of one row panel (kSdRows hub rows) over a
-// range of column tiles. Wave w computes rows 0..63 x columns 64 w .. 64 w + 63
-// of each tile (2 x 2 MFMA blocks) over the K features, passes of 8 KB8; with
-// kResident (one pass) its X fragments stay in registers across the column
-// tiles, and Y fragments stream one step ahead. The tile then goes through LDS
-// and the workgroup writes out[s][p] = value * D[r][c] for the tile's planned
-// entries (sorted by output position, so the stores run along the outputs).
-// Rows past R and columns past H compute on clamped rows; no entry names them.
+// range of column tiles. The 4 waves split a tile 2 x 2: wave w computes rows
+// 32 (w & 1) .. + 31 x columns 128 (w >> 1) .. + 127 (4 MFMA blocks), over
+// the K features in units of 8 KB8 (one unit per tile when kResident: the
+// wave's X fragments then stay in registers across the column tiles; else
+// K / 32 units, X reloaded per unit). Operands come in fragment order (each
+// load one contiguous 1 KB run). Y fragments stream through a ring of 4 steps
+// loaded 3 steps ahead, across unit and tile boundaries, so the next tile's
+// first loads are in flight during this tile's output phase. A finished tile
+// goes through LDS and the workgroup writes out[s][p] = value * D[r][c] for
+// the tile's planned entries (sorted by output position), 16 per thread in
+// flight. Padding rows and columns compute zeros; no entry names them.
+constexpr int kSdRing = 4;
+constexpr int kSdBatch = 16;
 template <int KB8, bool kResident>
 __global__ __launch_bounds__(kThreads, 2) void hub_sddmm_kernel(HubSddmmArgs a) {
+  static_assert(KB8 % kSdRing == 0, "units must hold whole rings of Y steps");
   __shared__ float dt[kSdRows * kSdLd];
+  __shared__ float* s_out[PS_MAX_WORKSETS];
+  __shared__ const int* s_pos[PS_MAX_WORKSETS];
   const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, a.chunk_log2);
   const int rp = int(blk % uint32_t(a.tiles_r)), cr = int(blk / uint32_t(a.tiles_r));
   const int cq0 = cr * a.range;
   const int cq1 = cq0 + a.range < a.tiles_c ? cq0 + a.range : a.tiles_c;
   if (cq0 >= cq1) return;  // uniform over the workgroup
-  const int wave = threadIdx.x / kWave, lane = lane_id(), g = lane >> 5, l32 = lane & 31;
-  const int passes = kResident ? 1 : a.K / (8 * KB8);
-
-  const float* xrow[2];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int m = rp * kSdRows + rb * 32 + l32;
-    xrow[rb] = a.X + size_t(a.hub_rows[m < a.R ? m : a.R - 1]) * size_t(a.K) + 4 * g;
+  if (threadIdx.x < PS_MAX_WORKSETS) {
+    s_out[threadIdx.x] = a.out[threadIdx.x];
+    s_pos[threadIdx.x] = a.out_pos[threadIdx.x];
   }
-  float4 xa[KB8][2];
+  const int wave = threadIdx.x / kWave, lane = lane_id(), g = lane >> 5, l32 = lane & 31;
+  const int wr = (wave & 1) * 32, wc = (wave >> 1) * 128;
+  const int units = kResident ? 1 : a.K / (8 * KB8);  // units per tile
+  const size_t steps = size_t(a.K / 8);               // 8-feature steps per row block
+
+  const float* xrun = a.Xf + size_t((rp * kSdRows + wr) / 32) * steps * 256 + lane * 4;
+  float4 xa[KB8];
   if (kResident) {
 #pragma unroll
-    for (int kb = 0; kb < KB8; ++kb)
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) xa[kb][rb] = load4(xrow[rb] + 8 * kb);
+    for (int kb = 0; kb < KB8; ++kb) xa[kb] = load4(xrun + kb * 256);
   }
+  // step 0 of the wave's column block cb in column tile q (the last tile of
+  // the range stands in for the one past it)
+  auto y_run = [&](int q, int cb) {
+    q = q < cq1 ? q : cq1 - 1;
+    return a.Yf + size_t((q * kSdCols + wc) / 32 + cb) * steps * 256 + lane * 4;
+  };
+  float4 yb[kSdRing][4];
+  // prologue: steps 0 .. kSdRing - 2 of the first unit
+#pragma unroll
+  for (int j = 0; j < kSdRing - 1; ++j)
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) yb[j][cb] = load4(y_run(cq0, cb) + j * 256);
 
-  for (int cq = cq0; cq < cq1; ++cq) {
-    const float* yrow[2];
+  v16f acc[1][4];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-      const int c = cq * kSdCols + wave * 64 + cb * 32 + l32;
-      yrow[cb] = a.Y + size_t(a.hot_cols[c < a.H ? c : a.H - 1]) * size_t(a.K) + 4 * g;
+  for (int cb = 0; cb < 4; ++cb) acc[0][cb] = v16f{};
+  int cq = cq0, unit = 0;
+  while (true) {
+    const int f8 = unit * KB8;  // first step of this unit
+    const bool tile_end = kResident || unit + 1 == units;
+    const int t = rp * a.tiles_c + cq;
+    uint32_t e0 = 0, e1 = 0;
+    if (tile_end) {
+      e0 = a.tile_begin[t];
+      e1 = a.tile_begin[t + 1];
     }
-    v16f acc[2][2];
+    if (!kResident) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) acc[rb][cb] = v16f{};
-    for (int ps = 0; ps < passes; ++ps) {
-      const int f = ps * 8 * KB8;
-      if (!kResident) {
-#pragma unroll
-        for (int kb = 0; kb < KB8; ++kb)
-#pragma unroll
-          for (int rb = 0; rb < 2; ++rb) xa[kb][rb] = load4(xrow[rb] + f + 8 * kb);
-      }
-      float4 yb[2][2];
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb) yb[0][cb] = load4(yrow[cb] + f);
-#pragma unroll
-      for (int kb = 0; kb < KB8; ++kb) {
-        if (kb + 1 < KB8) {
-#pragma unroll
-          for (int cb = 0; cb < 2; ++cb) yb[(kb + 1) & 1][cb] = load4(yrow[cb] + f + 8 * (kb + 1));
-        }
-        mfma_step<2, 2>(acc, xa[kb], yb[kb & 1]);
-      }
+      for (int kb = 0; kb < KB8; ++kb) xa[kb] = load4(xrun + (f8 + kb) * 256);
     }
+    // the runs the loads ahead read: this tile's, or the next tile's
+    const float* ycur[4];
+    const float* ynext[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      ycur[cb] = y_run(cq, cb);
+      ynext[cb] = tile_end ? y_run(cq + 1, cb) : ycur[cb] + (f8 + KB8) * 256;
+    }
+#pragma unroll
+    for (int kb = 0; kb < KB8; ++kb) {
+      float4 xs[1] = {xa[kb]};
+      float4 ys[4] = {yb[kb % kSdRing][0], yb[kb % kSdRing][1], yb[kb % kSdRing][2],
+                      yb[kb % kSdRing][3]};
+      mfma_step<1, 4>(acc, xs, ys);
+      // the step loaded now: of this unit, of the next unit of this tile, or
+      // of the next tile's first unit
+      const int ahead = kb + kSdRing - 1;
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+        yb[ahead % kSdRing][cb] = ahead < KB8 ? load4(ycur[cb] + (f8 + ahead) * 256)
+                                              : load4(ynext[cb] + (ahead - KB8) * 256);
+      // keep the loads at this step (the scheduler would sink them towards
+      // their use and shorten the prefetch distance)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!tile_end) {
+      ++unit;
+      continue;
+    }
+    // the tile is done: D through LDS, then the planned entries
     __syncthreads();  // the previous tile's entries are done with dt
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-      for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          dt[(rb * 32 + 8 * (r / 4) + 4 * g + (r % 4)) * kSdLd + wave * 64 + cb * 32 + l32] =
-              acc[rb][cb][r];
+      for (int r = 0; r < 16; ++r)
+        dt[(wr + 8 * (r / 4) + 4 * g + (r % 4)) * kSdLd + wc + cb * 32 + l32] = acc[0][cb][r];
     __syncthreads();
-    const int t = rp * a.tiles_c + cq;
-    const uint32_t e1 = a.tile_begin[t + 1];
-    for (uint32_t e = a.tile_begin[t] + threadIdx.x; e < e1; e += kThreads) {
-      const uint64_t code = a.entries[e];
-      const float v = a.values[e];
-      const uint32_t local = uint32_t(code >> (kPosBits + kWsBits));
-      const float d = dt[(local >> 8) * kSdLd + (local & 255u)];
-      const uint32_t p = uint32_t(code);
-      const int s = int((code >> kPosBits) & ((1u << kWsBits) - 1u));
-      if (a.out_csr) a.out_csr[pos_of(a, s)[p]] = v * d;
-      else out_of(a, s)[p] = v * d;
+    for (uint32_t base = e0; base < e1; base += kSdBatch * kThreads) {
+      uint64_t code[kSdBatch];
+      float val[kSdBatch];
+#pragma unroll
+      for (int j = 0; j < kSdBatch; ++j) {
+        const uint32_t e = base + uint32_t(j * kThreads) + threadIdx.x;
+        code[j] = e < e1 ? __builtin_nontemporal_load(a.entries + e) : 0;
+        val[j] = e < e1 ? __builtin_nontemporal_load(a.values + e) : 0.f;
+      }
+      int dst[kSdBatch];
+      if (a.out_csr) {
+#pragma unroll
+        for (int j = 0; j < kSdBatch; ++j) {
+          const uint32_t e = base + uint32_t(j * kThreads) + threadIdx.x;
+          const int s = int((code[j] >> kPosBits) & ((1u << kWsBits) - 1u));
+          dst[j] = e < e1 ? s_pos[s][uint32_t(code[j])] : 0;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kSdBatch; ++j) {
+        const uint32_t e = base + uint32_t(j * kThreads) + threadIdx.x;
+        if (e >= e1) continue;
+        const uint32_t local = uint32_t(code[j] >> (kPosBits + kWsBits));
+        const float d = val[j] * dt[(local >> 8) * kSdLd + (local & 255u)];
+        if (a.out_csr) {
+          __builtin_nontemporal_store(d, a.out_csr + dst[j]);
+        } else {
+          const int s = int((code[j] >> kPosBits) & ((1u << kWsBits) - 1u));
+          __builtin_nontemporal_store(d, s_out[s] + uint32_t(code[j]));
+        }
+      }
     }
+    if (++cq == cq1) break;
+    unit = 0;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) acc[0][cb] = v16f{};
   }
 }
 
@@ -666,13 +832,14 @@ int spmm_chunk(int rows, int ld) {
   if (chunks > ld / 256) chunks = ld / 256;
   if (chunks < 1) chunks = 1;
   const int kc = (ld + chunks - 1) / chunks;
-  return (kc + 15) & ~15;
+  return (kc + kDenseAlign - 1) & ~(kDenseAlign - 1);
 }
 
 template <int CB>
 void spmm_launch_cb(const HubSpmmArgs& a, unsigned grid, hipStream_t st) {
-  if (CB >= 2) hub_spmm_kernel<CB, 2><<<grid, kThreads, 0, st>>>(a);
-  else hub_spmm_kernel<CB, 4><<<grid, kThreads, 0, st>>>(a);
+  // one 32-feature block: no B sharing worth staging, a deep operand ring
+  if (CB == 1) hub_spmm_kernel<1, 8><<<grid, kThreads, 0, st>>>(a);
+  else hub_spmm_lds_kernel<CB, 4><<<grid, kThreads, 0, st>>>(a);
 }
 
 }  // namespace
@@ -697,6 +864,10 @@ size_t ps_hub_stored_words(const ps_hub_block* hb) {
 
 size_t ps_hub_dense_ld(int cols) { return cols > 0 ? ps::dense_ld(cols) : 0; }
 
+size_t ps_hub_dense_floats(int rows, int cols) {
+  return rows > 0 && cols > 0 ? ps::frag_rows(rows) * ps::dense_ld(cols) : 0;
+}
+
 int ps_hub_dense_build(const ps_hub_block* hb, const int* row_ptr, const int* col_ind,
                        const float* sp_data, float* dense, uint32_t* stored, ps_stream_t stream) {
   const int rc = ps::check_block(hb);
@@ -704,7 +875,7 @@ int ps_hub_dense_build(const ps_hub_block* hb, const int* row_ptr, const int* co
   PS_CHECK_ARG(row_ptr && col_ind && sp_data && dense && stored, "ps_hub_dense_build: null argument");
   PS_CHECK_ARG(ps::aligned16(dense), "ps_hub_dense_build: dense must be 16-byte aligned");
   hipStream_t st = ps::to_hip(stream);
-  PS_HIP(hipMemsetAsync(dense, 0, sizeof(float) * size_t(hb->rows) * ps::dense_ld(hb->cols), st));
+  PS_HIP(hipMemsetAsync(dense, 0, sizeof(float) * ps_hub_dense_floats(hb->rows, hb->cols), st));
   PS_HIP(hipMemsetAsync(stored, 0, sizeof(uint32_t) * ps_hub_stored_words(hb), st));
   const unsigned grid = ps::grid_for(size_t(hb->rows), 1);
   ps::dense_mark_kernel<<<grid, ps::kThreads, 0, st>>>(*hb, row_ptr, col_ind, dense, stored);
@@ -776,8 +947,15 @@ int ps_hub_tile_flags(const ps_hub_block* hb, const ps_workset* workset, uint8_t
 }
 
 size_t ps_hub_workspace_bytes(const ps_hub_block* hb, int op, int N) {
-  if (!hb || N <= 0 || op != PS_OP_SPMM) return 0;
-  // one feature slice of B's hot rows, transposed; row flags; the any-flag
+  if (!hb || N <= 0 || hb->rows <= 0 || hb->cols <= 0) return 0;
+  if (op == PS_OP_SDDMM) {
+    // X[hub_rows] and Y[hot_cols] in fragment order, padded to whole tiles
+    const size_t xrows = size_t(ps::sddmm_tiles_r(hb)) * ps::kSdRows;
+    const size_t yrows = size_t(ps::sddmm_tiles_c(hb)) * ps::kSdCols;
+    return ps::round256(xrows * size_t(N) * 4) + ps::round256(yrows * size_t(N) * 4);
+  }
+  if (op != PS_OP_SPMM) return 0;
+  // one feature slice of B's hot rows in fragment order; row flags; the any-flag
   const size_t slice = size_t(N < ps::kSpSlice ? N : ps::kSpSlice);
   return ps::round256(slice * ps::dense_ld(hb->cols) * 4) + ps::round256(size_t(hb->cols) * 4) + 256;
 }
@@ -802,7 +980,8 @@ int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, 
   int* any_flag = reinterpret_cast<int*>(reinterpret_cast<char*>(row_flag) +
                                          ps::round256(size_t(hb->cols) * 4));
   hipStream_t st = ps::to_hip(stream);
-  ps::clear_flag_kernel<<<1, 1, 0, st>>>(any_flag);
+  ps::clear_flags_kernel<<<ps::grid_for(size_t(hb->cols), ps::kThreads), ps::kThreads, 0, st>>>(
+      row_flag, hb->cols, any_flag);
   PS_LAUNCHED();
   ps::HubSpmmArgs a{};
   a.dense = hb->dense;
@@ -821,8 +1000,9 @@ int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, 
   a.chunk_log2 = uint32_t(ps::task_chunk_log2(PS_TASK_CHUNK_AUTO, grid, 64));
   for (int f0 = 0; f0 < N; f0 += ps::kSpSlice) {
     const int width = N - f0 < ps::kSpSlice ? N - f0 : ps::kSpSlice;
-    ps::transpose_hot_kernel<<<unsigned((ld + 63) / 64), ps::kThreads, 0, st>>>(
-        B, hb->hot_cols, hb->cols, N, ld, f0, width, Bt, row_flag, any_flag);
+    ps::gather_hot_kernel<<<ps::grid_for(size_t(width / 32) * size_t(ld / 8) * 64, ps::kThreads),
+                            ps::kThreads, 0, st>>>(B, hb->hot_cols, hb->cols, N, ld, f0, width, Bt,
+                                                   row_flag, any_flag);
     PS_LAUNCHED();
     a.f0 = f0;
     switch (width / 32) {
@@ -929,7 +1109,8 @@ int ps_hub_sddmm_plan(const ps_hub_block* hb, int workset_count, const ps_workse
 int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
                         const void* plan, uint32_t tile_count, int N, const float* lhs,
                         const float* rhs, float* const* out, const int* const* out_pos,
-                        float* out_csr, ps_stream_t stream) {
+                        float* out_csr, void* workspace, size_t workspace_bytes,
+                        ps_stream_t stream) {
   int rc = ps::check_block(hb);
   if (rc != PS_OK) return rc;
   PS_CHECK_ARG(workset_count >= 1 && workset_count <= PS_MAX_WORKSETS && worksets,
@@ -944,6 +1125,9 @@ int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_work
   PS_CHECK_ARG(int64_t(hb->matrix_rows) * N <= INT32_MAX && int64_t(hb->matrix_cols) * N <= INT32_MAX,
                "Dense dimensions exceed the 32-bit kernel indexing range");
   if (tile_count == 0) return PS_OK;
+  PS_CHECK_ARG(workspace && ps::aligned16(workspace) &&
+                   workspace_bytes >= ps_hub_workspace_bytes(hb, PS_OP_SDDMM, N),
+               "ps_hub_sddmm_launch: workspace too small");
   ps::HubSddmmArgs a{};
   for (int s = 1; s < workset_count; ++s) {
     a.out[s] = out ? out[s] : nullptr;
@@ -952,15 +1136,8 @@ int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_work
                      (out_csr ? a.out_pos[s] != nullptr : a.out[s] != nullptr),
                  "ps_hub_sddmm_launch: missing outputs of a block workset");
   }
-  a.S = workset_count;
   a.out_csr = out_csr;
-  a.X = lhs;
-  a.Y = rhs;
   a.K = N;
-  a.hub_rows = hb->hub_rows;
-  a.hot_cols = hb->hot_cols;
-  a.R = hb->rows;
-  a.H = hb->cols;
   a.tiles_r = int(ps::sddmm_tiles_r(hb));
   a.tiles_c = int(ps::sddmm_tiles_c(hb));
   const size_t T = size_t(a.tiles_r) * size_t(a.tiles_c);
@@ -979,6 +1156,19 @@ int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_work
   // runs of one column range's row panels on one XCD share its Y rows in L2
   a.chunk_log2 = uint32_t(ps::task_chunk_log2(PS_TASK_CHUNK_AUTO, grid, 32));
   hipStream_t st = ps::to_hip(stream);
+  // X[hub_rows] and Y[hot_cols] in fragment order
+  const int xrows = a.tiles_r * ps::kSdRows, yrows = a.tiles_c * ps::kSdCols;
+  float* xf = static_cast<float*>(workspace);
+  float* yf = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                       ps::round256(size_t(xrows) * size_t(N) * 4));
+  ps::gather_rows_kernel<<<ps::grid_for(size_t(xrows) * size_t(N) / 4, ps::kThreads), ps::kThreads,
+                           0, st>>>(lhs, hb->hub_rows, hb->rows, xrows, N, xf);
+  PS_LAUNCHED();
+  ps::gather_rows_kernel<<<ps::grid_for(size_t(yrows) * size_t(N) / 4, ps::kThreads), ps::kThreads,
+                           0, st>>>(rhs, hb->hot_cols, hb->cols, yrows, N, yf);
+  PS_LAUNCHED();
+  a.Xf = xf;
+  a.Yf = yf;
   switch (N) {
     case 32: ps::hub_sddmm_kernel<4, true><<<unsigned(grid), ps::kThreads, 0, st>>>(a); break;
     case 64: ps::hub_sddmm_kernel<8, true><<<unsigned(grid), ps::kThreads, 0, st>>>(a); break;

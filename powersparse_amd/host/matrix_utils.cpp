@@ -661,10 +661,9 @@ struct HubTier {
 
 struct PowerSparseMatrixGPU::HubState {
   std::vector<std::unique_ptr<HubTier>> tiers;
-  // the SpMM workspace (allocated with the block, sized for the widest
-  // feature slice, so calls allocate nothing): one call at a time, in GPU
-  // order (`done` is recorded after each call's hub kernels, the next call
-  // waits for it). SDDMM needs no workspace.
+  // the operator workspace (allocated with the block for every width, so
+  // calls allocate nothing): one call at a time, in GPU order (`done` is
+  // recorded after each call's hub kernels, the next call waits for it)
   std::mutex mu;
   DeviceArray<char> ws;
   ps_event_t done = nullptr;
@@ -672,9 +671,11 @@ struct PowerSparseMatrixGPU::HubState {
   ~HubState() {
     if (done) ps_event_destroy(done);
   }
-  size_t SpmmWorkspace(int N) const {
+  size_t Workspace(int op, int N) const {
     size_t need = 0;
-    for (const auto& t : tiers) need = std::max(need, ps_hub_workspace_bytes(&t->desc, PS_OP_SPMM, N));
+    for (const auto& t : tiers)
+      if (op == PS_OP_SPMM || t->plan_tiles)
+        need = std::max(need, ps_hub_workspace_bytes(&t->desc, op, N));
     return need;
   }
 };
@@ -808,7 +809,7 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
     d.hub_index = t->hub_index.data();
     d.hot_cols = t->hot_cols.data();
     d.hot_rank = t->hot_rank.data();
-    t->dense.Allocate(size_t(R) * ps_hub_dense_ld(int(H)));
+    t->dense.Allocate(ps_hub_dense_floats(int(R), int(H)));
     t->stored.Allocate(ps_hub_stored_words(&d));
     d.dense = t->dense.data();
     d.stored = t->stored.data();
@@ -935,8 +936,9 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
       ThrowOnError(rc);
     }
   }
-  // SpMM workspace for every width (feature slices of at most 128)
-  hub->ws.Allocate(hub->SpmmWorkspace(128));
+  // the workspace for every width: SpMM runs feature slices of at most 128,
+  // SDDMM widths go up to 512
+  hub->ws.Allocate(std::max(hub->Workspace(PS_OP_SPMM, 128), hub->Workspace(PS_OP_SDDMM, 512)));
   ThrowOnError(ps_event_create(&hub->done));
   ps_free(_run_order[k]);
   _run_order[k] = order;
@@ -949,8 +951,8 @@ bool PowerSparseMatrixGPU::BuildHub(const int* row_ptr, Prepared& in,
 void PowerSparseMatrixGPU::HubSpmm(int N, const float* B, float* C, ps_stream_t stream) const {
   HubState& h = *_hub;
   std::lock_guard<std::mutex> lock(h.mu);
-  if (h.ws.size() < h.SpmmWorkspace(N))  // allocated for every width with the block
-    throw std::logic_error("Hub block SpMM workspace smaller than the block needs");
+  if (h.ws.size() < h.Workspace(PS_OP_SPMM, N))  // allocated for every width with the block
+    throw std::logic_error("Hub block workspace smaller than the block needs");
   if (h.recorded) ThrowOnError(ps_stream_wait_event(stream, h.done));
   for (const auto& t : h.tiers)
     ThrowOnError(ps_hub_spmm_launch(&t->desc, N, B, C, h.ws.data(), h.ws.size(), stream));
@@ -960,12 +962,20 @@ void PowerSparseMatrixGPU::HubSpmm(int N, const float* B, float* C, ps_stream_t 
 
 void PowerSparseMatrixGPU::HubSddmm(int N, const float* lhs, const float* rhs, float* const* out,
                                     float* csr_out, ps_stream_t stream) const {
+  HubState& h = *_hub;
   const std::vector<ps_workset> ws = PublicWorksets();
-  for (const auto& t : _hub->tiers)
+  std::lock_guard<std::mutex> lock(h.mu);
+  if (h.ws.size() < h.Workspace(PS_OP_SDDMM, N))  // allocated for every width with the block
+    throw std::logic_error("Hub block workspace smaller than the block needs");
+  if (h.recorded) ThrowOnError(ps_stream_wait_event(stream, h.done));
+  for (const auto& t : h.tiers)
     if (t->plan_tiles)
       ThrowOnError(ps_hub_sddmm_launch(&t->desc, _group_type_num, ws.data(), t->plan.data(),
                                        t->plan_tiles, N, lhs, rhs, out,
-                                       csr_out ? _workset_csr_pos : nullptr, csr_out, stream));
+                                       csr_out ? _workset_csr_pos : nullptr, csr_out, h.ws.data(),
+                                       h.ws.size(), stream));
+  ThrowOnError(ps_event_record(h.done, stream));
+  h.recorded = true;
 }
 
 std::vector<ps_workset> PowerSparseMatrixGPU::PublicWorksets() const {

@@ -96,8 +96,9 @@ constexpr int kTunedSpmmGroupTypes = 3;
 // nonzeros); a (row, column) slot stored more than once stays on the sparse
 // SpMM path. Cost: 4 bytes per block element (dense), 12 bytes per planned
 // SDDMM nonzero, the tuned partition's own preprocessing (it no longer
-// shares the public one's), and an SpMM workspace allocated with the block
-// (128 floats per hot column of the widest tier).
+// shares the public one's), and an operator workspace allocated with the
+// block (SDDMM at N = 512: 2 KiB per hub row and per hot column of the
+// widest tier, padded to whole tiles).
 enum class HubBlock { kAuto = 0, kOff = 1 };
 constexpr int kHubMaxTiers = 3;
 constexpr double kHubDenseCost = 0.12, kHubMinGain = 0.05, kHubMinTierGain = 0.02;
@@ -236,9 +237,9 @@ class PowerSparseMatrixGPU {
   int HubCols(int tier = 0) const;
   // The hub block's part of an operator call, enqueued on `stream` after the
   // sparse part (SpMM: C += block * B; SDDMM: the block groups' outputs, into
-  // out[s] or, with csr_out, into csr_out at the CSR positions). SpMM calls on
-  // one matrix share its workspace and run one after another on the GPU;
-  // neither allocates.
+  // out[s] or, with csr_out, into csr_out at the CSR positions). Calls on one
+  // matrix share its workspace and run one after another on the GPU; neither
+  // allocates.
   void HubSpmm(int N, const float* B, float* C, ps_stream_t stream) const;
   void HubSddmm(int N, const float* lhs, const float* rhs, float* const* out, float* csr_out,
                 ps_stream_t stream) const;

@@ -322,8 +322,10 @@ def test_hub_entry_points_through_the_abi():
     for k in ("hub_rows", "hub_index", "hot_cols", "hot_rank"):
         setattr(hb, k, bufs[k].ptr)
     ld = hip.ps_hub_dense_ld(H)
-    assert ld % 16 == 0 and H <= ld < H + 16
-    dense = ps.DeviceBuffer(R * ld * 4)
+    assert ld % 64 == 0 and H <= ld < H + 64
+    R64 = -(-R // 64) * 64
+    assert hip.ps_hub_dense_floats(R, H) == R64 * ld
+    dense = ps.DeviceBuffer(R64 * ld * 4)
     stored = ps.DeviceBuffer(max(hip.ps_hub_stored_words(ctypes.byref(hb)), 1) * 4)
     hb.dense, hb.stored = dense.ptr, stored.ptr
     _hip_call(hip.ps_hub_dense_build(ctypes.byref(hb), bufs["row_ptr"].ptr, bufs["col_ind"].ptr,
@@ -335,11 +337,14 @@ def test_hub_entry_points_through_the_abi():
     _, inv, times = np.unique(slot, return_inverse=True, return_counts=True)
     once = times[inv] == 1
     say(f"block entries {int(inblock.sum())}, of them in repeated slots {int((inblock & ~once).sum())}")
-    # the dense rows: stored-once values, zeros elsewhere (padding included)
-    want_dense = np.zeros((R, ld), np.float32)
+    # the dense block: stored-once values, zeros elsewhere (padding included),
+    # in fragment order: (row block of 32, step of 8 columns, half of the step,
+    # row within the block, column within the half)
+    want_dense = np.zeros((R64, ld), np.float32)
     sel = inblock & once
     want_dense[hub_index[rowof[sel]], hot_rank[g.col_ind[sel]]] = g.values[sel]
-    np.testing.assert_array_equal(dense.download(np.float32, R * ld).reshape(R, ld), want_dense)
+    frag = want_dense.reshape(R64 // 32, 32, ld // 8, 2, 4).transpose(0, 2, 3, 1, 4)
+    np.testing.assert_array_equal(dense.download(np.float32, R64 * ld), frag.ravel())
     inblock = sel
 
     # SpMM: C = 0 + block * B on the hub rows, zero elsewhere
@@ -379,7 +384,6 @@ def test_hub_entry_points_through_the_abi():
     listed = np.array(bad[:2] + tiles + bad[2:], np.uint32)
     dt = ps.DeviceBuffer(host=listed)
     wa = _workset_array(up.worksets)
-    assert hip.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SDDMM, N) == 0
     plan_bytes = hip.ps_hub_sddmm_plan_bytes(ctypes.byref(hb), listed.size)
     plan = ps.DeviceBuffer(plan_bytes)
     _hip_call(hip.ps_hub_sddmm_plan(ctypes.byref(hb), w.S, wa, dt.ptr, listed.size, plan.ptr,
@@ -393,8 +397,10 @@ def test_hub_entry_points_through_the_abi():
     outs = [ps.DeviceBuffer(host=np.full(max(w.col[s].size, 1), sentinel, np.float32))
             for s in range(w.S)]
     dX, dY = ps.DeviceBuffer(host=X), ps.DeviceBuffer(host=Y)
+    wsd = ps.DeviceBuffer(hip.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SDDMM, N))
     _hip_call(hip.ps_hub_sddmm_launch(ctypes.byref(hb), w.S, wa, plan.ptr, listed.size, N,
-                                      dX.ptr, dY.ptr, _out_array(outs, w.S), None, None, None))
+                                      dX.ptr, dY.ptr, _out_array(outs, w.S), None, None,
+                                      wsd.ptr, wsd.nbytes, None))
     ps.synchronize()
     for s in range(w.S):
         out = outs[s].download(np.float32, max(w.col[s].size, 1))[:w.col[s].size]

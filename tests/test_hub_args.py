@@ -28,9 +28,14 @@ def last_error():
     return _native.hip().ps_last_error().decode()
 
 
-def test_dense_ld_rounds_to_16():
+def test_dense_ld_rounds_to_64():
     lib = _native.hip()
-    assert [lib.ps_hub_dense_ld(c) for c in (0, -3, 1, 15, 16, 17, 70)] == [0, 0, 16, 16, 16, 32, 80]
+    assert [lib.ps_hub_dense_ld(c) for c in (0, -3, 1, 63, 64, 65, 70, 200)] == \
+        [0, 0, 64, 64, 64, 128, 128, 256]
+    # rows padded to 64 as well
+    assert [lib.ps_hub_dense_floats(r, c) for r, c in ((0, 5), (5, 0), (1, 1), (64, 64),
+                                                       (65, 70), (130, 200))] == \
+        [0, 0, 64 * 64, 64 * 64, 128 * 128, 192 * 256]
 
 
 def test_workspace_and_stored_words():
@@ -38,13 +43,16 @@ def test_workspace_and_stored_words():
     hb = block(rows=5, cols=70)
     assert lib.ps_hub_stored_words(ctypes.byref(hb)) == 5 * 3
     assert lib.ps_hub_stored_words(None) == 0
-    ld = 80  # 70 hot columns padded to a multiple of 16
+    ld = 128  # 70 hot columns padded to a multiple of 64
     for N, slice_ in ((32, 32), (128, 128), (256, 128)):
         spmm = r256(slice_ * ld * 4) + r256(70 * 4) + 256
         assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SPMM, N) == spmm
-    # the fused SDDMM kernel keeps its dense tiles in LDS: no workspace
-    assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SDDMM, 32) == 0
+    # SDDMM: X[hub_rows] padded to 64 rows and Y[hot_cols] to 256, N floats each
+    for N in (32, 128, 512):
+        sddmm = r256(64 * N * 4) + r256(256 * N * 4)
+        assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SDDMM, N) == sddmm
     assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SPMM, 0) == 0
+    assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), 7, 32) == 0
 
 
 def test_plan_bytes_follow_the_tile_grid():
@@ -84,12 +92,12 @@ def test_spmm_launch_rejects_null_descriptor_and_misaligned_operands():
         _native.PS_ERR_INVALID and "16-byte aligned" in last_error()
 
 
-def sddmm(hb, N=32, plan=FAKE, count=1, out=True, worksets=2):
+def sddmm(hb, N=32, plan=FAKE, count=1, out=True, worksets=2, ws=1 << 40):
     lib = _native.hip()
     w = (_native.Workset * max(worksets, 1))()
     outs = (ctypes.c_void_p * max(worksets, 1))(*([FAKE] * max(worksets, 1)))
     return lib.ps_hub_sddmm_launch(ctypes.byref(hb), worksets, w, plan, count, N, FAKE,
-                                   FAKE, outs if out else None, None, None, None)
+                                   FAKE, outs if out else None, None, None, FAKE, ws, None)
 
 
 @pytest.mark.parametrize("kw,msg", [
@@ -98,6 +106,7 @@ def sddmm(hb, N=32, plan=FAKE, count=1, out=True, worksets=2):
     (dict(plan=None), "missing plan"),
     (dict(out=False), "missing outputs"),
     (dict(worksets=0), "invalid worksets"),
+    (dict(ws=1024), "workspace too small"),
 ])
 def test_sddmm_launch_rejects(kw, msg):
     rc = sddmm(block(), **kw)
