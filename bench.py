@@ -20,12 +20,13 @@ sparse launch, plus the dense hub block's kernels when the matrix keeps one,
 `config.hub_block` = its rows x columns); `cpu_baseline` is the OpenMP
 double-precision restatement of the reference's check path (the oracle) timed
 on this host over a bounded row sample of the same graph and operators.
-`roofline.traffic` is the bytes per launch the operator's sparse kernel's L2
-exchanges with the memory fabric (Infinity Cache and HBM; calibrated
-FETCH_SIZE + WRITE_SIZE; the hub block's GEMM and sampling kernels are not
-counted), taken from the committed rocprofv3 summary of the same workload
-when that summary was made from the current kernel sources (else null);
-`traffic_GBps` is that byte count over this run's call time;
+`roofline.traffic` is the bytes one operator call's kernels (the sparse
+launch and the hub block's kernels) exchange between the L2 and the memory
+fabric (Infinity Cache and HBM; calibrated FETCH_SIZE + WRITE_SIZE), taken
+from the committed rocprofv3 summary of the same workload when that summary
+was made from the current kernel sources (else null; `kernel_traffic` is the
+sparse launch's share); `traffic_GBps` is the call's bytes over this run's
+call time;
 `profile_call_kernel_us` is the summed duration of one call's kernels in
 that summary's traced bench run (`profile_call_kernels` of them: the sparse
 launch and the hub block's kernels), to compare with `call_us`.
@@ -82,8 +83,10 @@ def measured_counters(config, op, n):
     if summary.get("sources_digest") != sources_digest():
         return None, {}, rel, "profile summary made from other kernel sources: not used"
     key = f"{op}_N{n}"
-    traffic = summary.get("traffic", {}).get(key, {}).get("traffic_bytes")
+    entry = summary.get("traffic", {}).get(key, {})
+    traffic = entry.get("traffic_bytes")
     counters = dict(summary.get("counters", {}).get(key, {}))
+    counters["kernel_traffic"] = entry.get("kernel_traffic_bytes")
     # the traced bench run's kernels of one call, summed (the call time this
     # run measures with events should agree)
     call = summary.get("operators", {}).get(key, {})
@@ -290,12 +293,14 @@ def main():
         "roofline": {"bound": "hbm", "kernel": kernel, "op": f"{dom['op']} N={dom['N']}",
                      "achieved": dom["alg_GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": dom["roofline_frac"], "traffic": traffic,
-                     # bytes the L2 exchanged with the memory fabric per launch
-                     # (Infinity Cache hits and HBM together), over this run's
-                     # launch time
-                     "traffic_scope": "L2 to memory fabric (Infinity Cache and HBM), "
-                                      "calibrated FETCH_SIZE + WRITE_SIZE, of the "
-                                      "operator's sparse kernel",
+                     # bytes the L2 exchanged with the memory fabric per
+                     # operator call (Infinity Cache hits and HBM together),
+                     # over this run's call time
+                     "traffic_scope": "per operator call: L2 to memory fabric (Infinity "
+                                      "Cache and HBM), calibrated FETCH_SIZE + WRITE_SIZE, "
+                                      "summed over the call's kernels (sparse launch and "
+                                      "hub block)",
+                     "kernel_traffic": counters.get("kernel_traffic"),
                      "traffic_GBps": traffic / (dom["ms"] * 1e-3) / 1e9 if traffic else None,
                      "l2_hit_pct": counters.get("l2_hit_pct"),
                      "valu_busy_pct": counters.get("valu_busy_pct"),

@@ -204,13 +204,6 @@ def fill_random(buf, count, seed, lo, hi, normal=False, stream=None):
                                                  float(hi), int(bool(normal)), _ptr(stream)))
 
 
-def copy_f32(dst, src, count, stream=None):
-    """Plain streaming device copy of `count` floats (bandwidth reference; from
-    the measurement-probe library)."""
-    _hip_call(_native.probes().ps_copy_f32_async(_ptr(dst), _ptr(src), int(count),
-                                                  _ptr(stream)))
-
-
 # ---------------------------------------------------------------- host CSR
 
 class HostCsr:

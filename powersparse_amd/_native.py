@@ -2,8 +2,9 @@
 
 lib/libpowersparse_hip.so     HIP kernels + C ABI        (include/powersparse_hip.h)
 lib/libpowersparse.so         C++17 host API, C facade   (include/powersparse.h)
-lib/libpowersparse_probes.so  measurement probes         (include/powersparse_probes.h),
-                              loaded only by the measurement tooling (probes())
+lib/libpowersparse_perf.so    the measurement tooling's calibration copy (not
+                              product code), loaded only by powersparse_amd.perf
+                              (perf_lib())
 
 Loading fails loudly when the libraries are missing: there is no CPU fallback.
 """
@@ -14,7 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(_HERE, "lib")
 HIP_LIB_PATH = os.path.join(LIB_DIR, "libpowersparse_hip.so")
 HOST_LIB_PATH = os.path.join(LIB_DIR, "libpowersparse.so")
-PROBES_LIB_PATH = os.path.join(LIB_DIR, "libpowersparse_probes.so")
+PERF_LIB_PATH = os.path.join(LIB_DIR, "libpowersparse_perf.so")
 
 PS_OK = 0
 PS_ERR_INVALID = 1
@@ -245,14 +246,8 @@ HIP_API = [
       c_void_p, c_void_p, c_void_p, c_void_p]),
 ]
 
-PROBES_API = [
-    ("ps_copy_f32_async", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
-    ("ps_probe_xcc_ids_async", ctypes.c_int, [c_void_p, ctypes.c_int, c_void_p]),
-    ("ps_probe_row_update_async", ctypes.c_int,
-     [c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_int, ctypes.c_uint64, c_void_p]),
-    ("ps_probe_gather_async", ctypes.c_int,
-     [c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_longlong, ctypes.c_uint64, c_void_p,
-      c_void_p]),
+PERF_API = [
+    ("ps_perf_copy_f32_async", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
 ]
 
 HOST_API = [
@@ -318,7 +313,7 @@ HOST_API = [
 
 _hip = None
 _host = None
-_probes = None
+_perf = None
 
 
 def _bind(lib, api):
@@ -354,15 +349,15 @@ def host():
     return libs()[1]
 
 
-def probes():
-    """Loads (once) and returns the measurement-probe library."""
-    global _probes
-    if _probes is None:
+def perf_lib():
+    """Loads (once) and returns the measurement tooling's calibration-copy library."""
+    global _perf
+    if _perf is None:
         libs()
-        if not os.path.exists(PROBES_LIB_PATH):
-            raise ImportError(f"powersparse_amd: probe library {PROBES_LIB_PATH} is missing; "
-                              "build it with `make -C powersparse_amd`")
-        lib = ctypes.CDLL(PROBES_LIB_PATH)
-        _bind(lib, PROBES_API)
-        _probes = lib
-    return _probes
+        if not os.path.exists(PERF_LIB_PATH):
+            raise ImportError(f"powersparse_amd: {PERF_LIB_PATH} is missing; "
+                              "build it with `make -C powersparse_amd perf`")
+        lib = ctypes.CDLL(PERF_LIB_PATH)
+        _bind(lib, PERF_API)
+        _perf = lib
+    return _perf

@@ -349,93 +349,18 @@ struct HubSpmmArgs {
 
 // One workgroup: kSpRows hub rows (64 per wave: 2 MFMA row blocks) x the
 // slice's 32 CB features, over one chunk of hot columns; the partial rows are
-// added into C with atomics. A (dense) streams from memory once; B (Bt) is
-// the same for the 4 waves of a workgroup and for every row panel of a chunk
-// (neighbouring workgroups take the chunk's panels on one XCD). The operands
-// of 8-column steps go through a ring of RING stages loaded RING - 1 steps
-// ahead; chunks are whole rings (kc and ld are multiples of kDenseAlign), and
-// loads past the chunk's end (never used) read its last step again.
-template <int CB, int RING>
-__global__ __launch_bounds__(kThreads, 2) void hub_spmm_kernel(HubSpmmArgs a) {
-  static_assert(kDenseAlign % (8 * RING) == 0, "chunks must hold whole rings of steps");
-  const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, a.chunk_log2);
-  const int panel = int(blk % uint32_t(a.panels)), chunk = int(blk / uint32_t(a.panels));
-  const int lane = lane_id(), g = lane >> 5, l32 = lane & 31;
-  const int m0 = panel * kSpRows + (threadIdx.x / kWave) * 64;
-  const int k0 = chunk * a.kc;
-  const int k1 = k0 + a.kc < a.ld ? k0 + a.kc : a.ld;
-  if (m0 >= a.R || k0 >= k1) return;
-  // operand runs of step 0 (rows past R are zero padding; their results are
-  // never written): step k / 8 is 256 floats further on
-  const size_t steps = size_t(a.ld / 8);
-  const float* arow[2];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) arow[rb] = a.dense + size_t(m0 / 32 + rb) * steps * 256 + lane * 4;
-  const float* brow[CB];
-#pragma unroll
-  for (int cb = 0; cb < CB; ++cb) brow[cb] = a.Bt + size_t(cb) * steps * 256 + lane * 4;
-
-  v16f acc[2][CB];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = v16f{};
-  float4 A[RING][2], Bf[RING][CB];
-  const int klast = k1 - 8;
-#pragma unroll
-  for (int s = 0; s < RING - 1; ++s) {
-    const int k = k0 + 8 * s < klast ? k0 + 8 * s : klast;
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) A[s][rb] = load4(arow[rb] + size_t(k) * 32);
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb) Bf[s][cb] = load4(brow[cb] + size_t(k) * 32);
-    // stages issued in ring order, as the loop issues them
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  for (int h = k0; h < k1; h += 8 * RING) {
-#pragma unroll
-    for (int s = 0; s < RING; ++s) {
-      mfma_step<2, CB>(acc, A[s], Bf[s]);
-      const int ahead = (s + RING - 1) % RING;
-      const int nk = h + 8 * (s + RING - 1);
-      const int k = nk < klast ? nk : klast;
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) A[ahead][rb] = load4(arow[rb] + size_t(k) * 32);
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) Bf[ahead][cb] = load4(brow[cb] + size_t(k) * 32);
-      // keep the loads at this step (the scheduler would sink them towards
-      // their use and shorten the prefetch distance)
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-  // C[hub_rows[m]][f0 + 32 cb + l32] += acc: register r of a block holds row
-  // 8 (r / 4) + 4 g + r % 4, so each atomic instruction adds two 32-float
-  // row stretches.
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int mb = m0 + rb * 32;
-    const int hr = a.hub_rows[mb + l32 < a.R ? mb + l32 : a.R - 1];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int lr = 8 * (r / 4) + 4 * g + (r % 4);
-      const int dst = __shfl(hr, lr);
-      if (mb + lr < a.R) {
-        float* crow = a.C + size_t(dst) * size_t(a.N) + size_t(a.f0 + l32);
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) unsafeAtomicAdd(crow + cb * 32, acc[rb][cb][r]);
-      }
-    }
-  }
-}
-
-// The same product for slices of 64 or more features: the 4 waves share the
-// slice's B fragments, so each wave loads one 32-feature block of every step
-// (G steps ahead, into registers) and the workgroup passes them through a
-// double-buffered LDS stage, one barrier per step; A fragments stream per wave
-// through a ring of RA steps as above. Waves whose 64 rows lie past R compute
-// on row block 0 and write nothing (every wave takes part in the barriers).
+// added into C with atomics. A (dense) streams from memory once, through a
+// per-wave ring of RA 8-column steps loaded RA - 1 steps ahead. The 4 waves
+// share the slice's B fragments: wave w < CB loads 32-feature block w of
+// every step (G steps ahead, into registers) and the workgroup passes them
+// through a double-buffered LDS stage, one barrier per step; neighbouring
+// workgroups take a chunk's row panels on one XCD, so B is read from memory
+// about once per chunk. Chunks are whole loop iterations (kc and ld are
+// multiples of kDenseAlign); loads past the chunk's end (never used) read its
+// last step again. Waves whose 64 rows lie past R compute on row block 0 and
+// write nothing (every wave takes part in the barriers).
 template <int CB, int RA>
-__global__ __launch_bounds__(kThreads, 2) void hub_spmm_lds_kernel(HubSpmmArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void hub_spmm_kernel(HubSpmmArgs a) {
   constexpr int G = 4;                               // B steps in flight per wave
   constexpr int U = RA > G ? RA : G;                 // steps per loop iteration
   static_assert(U % RA == 0 && U % G == 0 && U % 2 == 0, "ring sizes must divide the unroll");
@@ -824,11 +749,13 @@ int worksets_of(int workset_count, const ps_workset* worksets, Worksets* a) {
 uint32_t sddmm_tiles_r(const ps_hub_block* hb) { return uint32_t((hb->rows + kSdRows - 1) / kSdRows); }
 uint32_t sddmm_tiles_c(const ps_hub_block* hb) { return uint32_t((hb->cols + kSdCols - 1) / kSdCols); }
 
-// Hot columns per SpMM chunk: about 1024 workgroups per feature slice (4 per
-// CU), at least 256 columns per chunk, a multiple of 16.
+// Hot columns per SpMM chunk: about 768 workgroups per feature slice (3 per
+// CU; measured on C3 against 512, 1024 and 2048: fewer chunks add fewer
+// partial rows into C), at least 256 columns per chunk, a multiple of
+// kDenseAlign.
 int spmm_chunk(int rows, int ld) {
   const int panels = (rows + kSpRows - 1) / kSpRows;
-  int chunks = (1024 + panels - 1) / panels;
+  int chunks = (768 + panels - 1) / panels;
   if (chunks > ld / 256) chunks = ld / 256;
   if (chunks < 1) chunks = 1;
   const int kc = (ld + chunks - 1) / chunks;
@@ -837,9 +764,8 @@ int spmm_chunk(int rows, int ld) {
 
 template <int CB>
 void spmm_launch_cb(const HubSpmmArgs& a, unsigned grid, hipStream_t st) {
-  // one 32-feature block: no B sharing worth staging, a deep operand ring
-  if (CB == 1) hub_spmm_kernel<1, 8><<<grid, kThreads, 0, st>>>(a);
-  else hub_spmm_lds_kernel<CB, 4><<<grid, kThreads, 0, st>>>(a);
+  // a deeper A ring for a single feature block (fewer MFMAs per A load)
+  hub_spmm_kernel<CB, (CB == 1 ? 8 : 4)><<<grid, kThreads, 0, st>>>(a);
 }
 
 }  // namespace

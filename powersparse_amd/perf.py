@@ -2,16 +2,10 @@
 
   python -m powersparse_amd.perf workload [--config C1] [--steps 3]
       Runs, once each after one warm-up: a plain 1 GiB streaming copy
-      (ps_copy_f32_async, the counter calibration: it reads and writes exactly
-      1 GiB) and the bench operators of the configuration. Meant to run under
-      `rocprofv3 --pmc FETCH_SIZE` and `rocprofv3 --pmc WRITE_SIZE`.
-
-  python -m powersparse_amd.perf ceiling
-      Streaming-copy bandwidth, the throughput of uniformly random row
-      gathers (128- and 512-byte rows) against table size (the hardware
-      ceiling of the operators' per-nonzero B / Y row gathers), and the rate of
-      128-byte row updates at random rows by plain stores and by float atomics
-      in three lane layouts (the cost of the SpMM kernel's C-row writes).
+      (ps_perf_copy_f32_async from lib/libpowersparse_perf.so, `make -C
+      powersparse_amd perf`; the counter calibration: it reads and writes
+      exactly 1 GiB) and the bench operators of the configuration. Meant to run
+      under `rocprofv3 --pmc FETCH_SIZE` and `rocprofv3 --pmc WRITE_SIZE`.
 
   python -m powersparse_amd.perf csr [--config C1] [--n 128]
       Times the SDDMM output orders on one matrix built with csr_positions:
@@ -22,13 +16,15 @@
   python -m powersparse_amd.perf summarize --trace KT.db [--fetch F.db --write W.db]
         [--l2 L.db] [--valu V.db] [--config C1] [--json OUT.json]
       Reads rocprofv3 SQLite result databases: per kernel the dispatch count and
-      mean duration (kernel trace), and per operator kernel the HBM traffic per
-      dispatch = FETCH_SIZE + WRITE_SIZE (KiB), each scaled by the factor that
-      makes the calibration copy read and write exactly its size; with --l2 (a
-      `--pmc TCC_HIT_sum TCC_MISS_sum` pass) the L2 hit rate, with --valu (a `--pmc VALUBusy
+      mean duration (kernel trace); per operator call (the sparse launch and the
+      dense hub block's kernels after it) and per sparse launch alone, the
+      traffic between the L2 and the memory fabric = FETCH_SIZE + WRITE_SIZE
+      (KiB), each scaled by the factor that makes the calibration copy read and
+      write exactly its size; with --l2 (a `--pmc TCC_HIT_sum TCC_MISS_sum`
+      pass) the L2 hit rate of the whole call, with --valu (a `--pmc VALUBusy
       VALUUtilization` pass) the share of time the VALUs issue and the share of
-      active lanes per VALU instruction, each averaged over the operator's
-      dispatches.
+      active lanes per VALU instruction of the sparse launch; means over the
+      operator's calls.
 """
 import argparse
 import collections
@@ -97,9 +93,19 @@ def short_name(name):
 
 def kernel_op(name):
     """(op, lanes-template) of an operator kernel name, else None."""
-    # spmm_kernel<lanes, buf>, sddmm_kernel<KQ, buf, store mode>
-    m = re.search(r"(spmm|sddmm)_kernel<(\d+), (true|false)(, \d+)?>", short_name(name))
+    # spmm_kernel<lanes, buf>, sddmm_kernel<KQ, buf, store mode>; the hub
+    # block's kernels (hub_spmm_kernel<..>, hub_sddmm_kernel<..>) are not
+    m = re.search(r"(?:^|::)(spmm|sddmm)_kernel<(\d+), (true|false)(, \d+)?>", short_name(name))
     return (m.group(1), int(m.group(2))) if m else None
+
+
+def copy_f32(dst, src, count, stream=None):
+    """The calibration copy: a plain streaming device copy of `count` floats."""
+    import powersparse_amd as ps
+    from powersparse_amd import _native
+
+    ps._hip_call(_native.perf_lib().ps_perf_copy_f32_async(
+        ps._ptr(dst), ps._ptr(src), int(count), ps._ptr(stream)))
 
 
 def workload(args):
@@ -112,7 +118,7 @@ def workload(args):
     dst = ps.DeviceBuffer(CALIB_BYTES)
     ps.fill_random(src, CALIB_BYTES // 4, 7, 0.0, 1.0)
     for _ in range(2):
-        ps.copy_f32(dst, src, CALIB_BYTES // 4)
+        copy_f32(dst, src, CALIB_BYTES // 4)
     ps.synchronize()
     csr = ps.synth(args.config, seed=1)
     m = ps.PowerSparseMatrixGPU.from_csr(csr)
@@ -138,56 +144,6 @@ def workload(args):
                 ps.SDDMMAsync(m, n, X, Y, outs)
         ps.synchronize()
     print(f"workload {args.config}: nnz={csr.nnz} done", flush=True)
-
-
-def ceiling(args):
-    """Streaming-copy bandwidth, random row-gather throughput vs table size, and
-    random row-update rates by store and atomic lane layout."""
-    import powersparse_amd as ps
-    from powersparse_amd import _native
-
-    ps.set_device(0)
-    st = ps.Stream()
-    t0, t1 = ps.Event(), ps.Event()
-
-    def timed(fn, reps=4):
-        fn()
-        best = None
-        for _ in range(reps):
-            t0.record(st)
-            fn()
-            t1.record(st)
-            t1.synchronize()
-            ms = t0.elapsed_ms(t1)
-            best = ms if best is None else min(best, ms)
-        return best
-
-    big = 2048 << 20
-    table = ps.DeviceBuffer(big)
-    ps.fill_random(table, big // 4, 3, 0.0, 1.0, stream=st)
-    dst = ps.DeviceBuffer(1 << 30)
-    out = ps.DeviceBuffer(4)
-    ms = timed(lambda: ps.copy_f32(dst, table, (1 << 30) // 4, st))
-    lines = ["| probe | working set | time (ms) | GB/s |", "|---|---|---|---|",
-             f"| streaming copy (read + write) | 1 GiB | {ms:.3f} | {2 * (1 << 30) / ms / 1e6:.0f} |"]
-    n = 1 << 24
-    for row_floats in (32, 128):
-        for mb in (2, 4, 8, 32, 128, 256, 512, 2048):
-            rows = (mb << 20) // (4 * row_floats)
-            ms = timed(lambda: ps._hip_call(_native.probes().ps_probe_gather_async(
-                table.ptr, rows, row_floats, n, 9, out.ptr, st.ptr)))
-            lines.append(f"| random {4 * row_floats}-byte row gathers | {mb} MB table | "
-                         f"{ms:.3f} | {n * 4 * row_floats / ms / 1e6:.0f} |")
-    lines += ["", "| 128-byte row updates at random rows of a 128 MB C | time for 4 M (ms) | "
-                  "M rows/s |", "|---|---|---|"]
-    modes = ("plain 128-bit stores", "float atomics, lanes 16 B apart (4 per lane)",
-             "float atomics, 8 lanes x 4 consecutive bytes", "float atomics, 32 lanes per row")
-    nu = 1 << 22
-    for mode, name in enumerate(modes):
-        ms = timed(lambda: ps._hip_call(_native.probes().ps_probe_row_update_async(
-            dst.ptr, 1 << 20, nu, mode, 5, st.ptr)))
-        lines.append(f"| {name} | {ms:.3f} | {nu / ms / 1e3:.0f} |")
-    print("\n".join(lines))
 
 
 def csr_order(args):
@@ -232,6 +188,16 @@ def csr_order(args):
         print(f"| {name} | {ms:.3f} |")
 
 
+# The dense hub block's kernels of an operator call (they follow the sparse
+# launch on its stream).
+HUB_KERNEL = re.compile(r"(?:^|::)(hub_spmm_kernel|hub_sddmm_kernel|gather_hot_kernel|"
+                        r"gather_rows_kernel|clear_flags_kernel|fixup_kernel)\b")
+
+
+def is_hub_kernel(name):
+    return HUB_KERNEL.search(short_name(name)) is not None
+
+
 def read_counters(db, counter):
     """[(kernel, grid, value)] of every dispatch, in dispatch order."""
     con = sqlite3.connect(db)
@@ -248,13 +214,18 @@ def counter_means(db, counter, ops):
 
 
 def l2_hit_means(db, ops):
-    """{op_N: mean L2 hit rate in percent, 100 * TCC_HIT / (TCC_HIT + TCC_MISS)
-    per dispatch} (rocprofv3 defines no L2CacheHit metric for gfx950)."""
+    """{op_N: L2 hit rate in percent of one operator call, 100 * TCC_HIT /
+    (TCC_HIT + TCC_MISS) summed over the call's kernels (the sparse launch and
+    the hub block's kernels), mean over the calls} (rocprofv3 defines no
+    L2CacheHit metric for gfx950)."""
     hits, misses = read_counters(db, "TCC_HIT_sum"), read_counters(db, "TCC_MISS_sum")
-    rates = [(k, g, 100.0 * h / (h + m) if h + m > 0 else 0.0)
-             for (k, g, h), (_, _, m) in zip(hits, misses)]
-    runs = operator_runs(rates)
-    return {f"{op}_N{n}": sum(v) / len(v) for (op, n), (_, v) in zip(ops, runs)}
+    hr = call_runs(hits)
+    mr = call_runs(misses)
+    out = {}
+    for (op, n), (_, hv, _), (_, mv, _) in zip(ops, hr, mr):
+        rates = [100.0 * h / (h + m) if h + m > 0 else 0.0 for h, m in zip(hv, mv)]
+        out[f"{op}_N{n}"] = sum(rates) / len(rates)
+    return out
 
 
 def read_trace(db):
@@ -294,6 +265,28 @@ def operator_calls(dispatches, ops):
             out[f"{op}_N{n}"] = (len(mine), max(len(c) for c in mine),
                                  sum(sum(c) for c in mine) / len(mine))
     return out
+
+
+def call_runs(dispatches):
+    """Groups dispatches into operator calls (an operator kernel's dispatch and
+    the hub block's kernels after it; other kernels belong to no call) and the
+    calls into runs of equal (operator kernel, grid), in order: [((kernel,
+    grid), [summed value per call], kernels per call)], one run per operator
+    of the workload."""
+    calls = []
+    for k, g, v in dispatches:
+        if kernel_op(k) is not None:
+            calls.append(((k, g), [v]))
+        elif calls and is_hub_kernel(k):
+            calls[-1][1].append(v)
+    runs = []
+    for key, vals in calls:
+        if runs and runs[-1][0] == key:
+            runs[-1][1].append(sum(vals))
+            runs[-1][2] = max(runs[-1][2], len(vals))
+        else:
+            runs.append([key, [sum(vals)], len(vals)])
+    return [tuple(r) for r in runs]
 
 
 def operator_runs(dispatches):
@@ -346,24 +339,34 @@ def summarize(args):
         kf, kw = calibration(fetch), calibration(write)
         lines += ["", f"Calibration (1 GiB ps::copy_f32_kernel): FETCH x{kf:.4f}, "
                       f"WRITE x{kw:.4f}", "",
-                  "| operator | kernel | grid | FETCH (MB) | WRITE (MB) | traffic per launch (MB) |",
-                  "|---|---|---|---|---|---|"]
+                  "Per operator call (the sparse launch and the hub block's kernels), and of "
+                  "the sparse launch alone:", "",
+                  "| operator | kernels per call | FETCH (MB) | WRITE (MB) | traffic per call (MB) "
+                  "| sparse kernel | its traffic per launch (MB) |",
+                  "|---|---|---|---|---|---|---|"]
         result["calibration"] = {"fetch": kf, "write": kw}
         result["traffic"] = {}
         fr, wr = operator_runs(fetch), operator_runs(write)
-        for (op, n), ((k, g), fv), (_, wv) in zip(CONFIG_OPS[args.config], fr, wr):
-            fb = sum(fv) / len(fv) * 1024.0 * kf
-            wb = sum(wv) / len(wv) * 1024.0 * kw
-            result["traffic"][f"{op}_N{n}"] = {"kernel": k, "grid": g, "fetch_bytes": fb,
-                                                "write_bytes": wb, "traffic_bytes": fb + wb}
-            lines.append(f"| {op} N={n} | `{k}` | {g} | {fb / 1e6:.1f} | {wb / 1e6:.1f} | "
-                         f"{(fb + wb) / 1e6:.1f} |")
+        fc, wc = call_runs(fetch), call_runs(write)
+        for (op, n), ((k, g), fv), (_, wv), (_, fcv, kpc), (_, wcv, _) in zip(
+                CONFIG_OPS[args.config], fr, wr, fc, wc):
+            fb = sum(fcv) / len(fcv) * 1024.0 * kf
+            wb = sum(wcv) / len(wcv) * 1024.0 * kw
+            kfb = sum(fv) / len(fv) * 1024.0 * kf
+            kwb = sum(wv) / len(wv) * 1024.0 * kw
+            result["traffic"][f"{op}_N{n}"] = {
+                "kernel": k, "grid": g, "kernels_per_call": kpc, "fetch_bytes": fb,
+                "write_bytes": wb, "traffic_bytes": fb + wb, "kernel_fetch_bytes": kfb,
+                "kernel_write_bytes": kwb, "kernel_traffic_bytes": kfb + kwb}
+            lines.append(f"| {op} N={n} | {kpc} | {fb / 1e6:.1f} | {wb / 1e6:.1f} | "
+                         f"{(fb + wb) / 1e6:.1f} | `{k}` | {(kfb + kwb) / 1e6:.1f} |")
     if args.l2 or args.valu:
         ops = CONFIG_OPS[args.config]
         l2 = l2_hit_means(args.l2, ops) if args.l2 else {}
         busy = counter_means(args.valu, "VALUBusy", ops) if args.valu else {}
         util = counter_means(args.valu, "VALUUtilization", ops) if args.valu else {}
-        lines += ["", "| operator | L2 hit rate (%) | VALU busy (%) | VALU lanes active (%) |",
+        lines += ["", "L2 hit rate per operator call; VALU figures of the sparse launch:", "",
+                  "| operator | L2 hit rate (%) | VALU busy (%) | VALU lanes active (%) |",
                   "|---|---|---|---|"]
         result["counters"] = {}
         for op, n in ops:
@@ -385,7 +388,6 @@ def main(argv=None):
     w = sub.add_parser("workload")
     w.add_argument("--config", default="C1", choices=sorted(CONFIG_OPS))
     w.add_argument("--steps", type=int, default=3)
-    sub.add_parser("ceiling")
     c = sub.add_parser("csr")
     c.add_argument("--config", default="C1", choices=sorted(CONFIG_OPS))
     c.add_argument("--n", type=int, default=128)
@@ -400,8 +402,6 @@ def main(argv=None):
     args = ap.parse_args(argv)
     if args.cmd == "workload":
         workload(args)
-    elif args.cmd == "ceiling":
-        ceiling(args)
     elif args.cmd == "csr":
         csr_order(args)
     else:

@@ -54,42 +54,3 @@ def test_radix_sort_pairs_stable(bits, n, lo, hi, keymax):
     order = np.argsort(sel, kind="stable")
     np.testing.assert_array_equal(got_v, vals[order])
     np.testing.assert_array_equal(got_k, keys[order])
-
-
-@pytest.mark.parametrize("mode", [0, 1, 2, 3])
-def test_row_update_probe(mode):
-    """ps_probe_row_update_async touches whole 128-byte rows: every atomic mode
-    adds 1 to each of the 32 floats of n rows (the sum is 32 n, exact in FP32
-    at this size), the store mode writes 1, 2, 3, 4 into every updated row."""
-    setup()
-    rows, n = 4096, 10001
-    say(f"row update probe mode={mode}")
-    c = ps.DeviceBuffer(rows * 32 * 4)
-    c.zero()
-    ps._hip_call(_native.probes().ps_probe_row_update_async(c.ptr, rows, n, mode, 3, None))
-    got = c.download(np.float32, rows * 32).reshape(rows, 32)
-    if mode == 0:
-        touched = got.any(axis=1)
-        assert 0 < touched.sum() <= n
-        np.testing.assert_array_equal(got[touched], np.tile([1, 2, 3, 4], 8)[None, :]
-                                      .repeat(touched.sum(), 0).astype(np.float32))
-    else:
-        assert got.sum(dtype=np.float64) == 32.0 * n
-        # each touched row holds the same count in all 32 floats
-        np.testing.assert_array_equal(got, got[:, :1].repeat(32, 1))
-
-
-def test_workgroups_dealt_round_robin_over_xcds():
-    """The task_chunk mapping assumes the hardware deals a launch's workgroups
-    round-robin over the XCDs: workgroup b on XCD (x0 + b) mod (number of
-    XCDs), where x0 (the XCD after the previous dispatch's last workgroup) is
-    0 only in a fresh process."""
-    setup()
-    n = 4096
-    say("xcc ids of 4096 workgroups")
-    out = ps.DeviceBuffer(n * 4)
-    ps._hip_call(_native.probes().ps_probe_xcc_ids_async(out.ptr, n, None))
-    ids = out.download(np.int32, n)
-    xcds = int(ids.max()) + 1
-    assert xcds == 8 or ps.device_props(0)["cu_count"] != 256
-    np.testing.assert_array_equal(ids, (ids[0] + np.arange(n)) % xcds)

@@ -23,11 +23,9 @@ def declared(header):
 
 
 @pytest.mark.parametrize("header,libpath", [
-    ("powersparse_hip.h", _native.HIP_LIB_PATH), ("powersparse.h", _native.HOST_LIB_PATH),
-    ("powersparse_probes.h", _native.PROBES_LIB_PATH)])
+    ("powersparse_hip.h", _native.HIP_LIB_PATH), ("powersparse.h", _native.HOST_LIB_PATH)])
 def test_every_declared_symbol_is_exported(header, libpath):
     _native.libs()
-    _native.probes()
     names = declared(header)
     assert len(names) >= 4
     out = subprocess.run(["nm", "-D", "--defined-only", libpath], capture_output=True, text=True,
@@ -35,8 +33,22 @@ def test_every_declared_symbol_is_exported(header, libpath):
     exported = set(line.split()[-1] for line in out.splitlines() if line.strip())
     missing = [n for n in names if n not in exported]
     assert not missing, missing
-    bound = {n for n, _, _ in (_native.HIP_API + _native.HOST_API + _native.PROBES_API)}
+    bound = {n for n, _, _ in (_native.HIP_API + _native.HOST_API)}
     assert not [n for n in names if n not in bound]
+
+
+def test_measurement_copy_library_is_separate():
+    """The measurement tooling's calibration copy lives in its own library
+    (lib/libpowersparse_perf.so), outside the product libraries."""
+    _native.perf_lib()
+    for lib in (_native.HIP_LIB_PATH, _native.HOST_LIB_PATH):
+        out = subprocess.run(["nm", "-D", "--defined-only", lib], capture_output=True,
+                             text=True, check=True).stdout
+        assert "ps_perf_copy_f32_async" not in out and "probe" not in out
+    out = subprocess.run(["nm", "-D", "--defined-only", _native.PERF_LIB_PATH],
+                         capture_output=True, text=True, check=True).stdout
+    assert [n for n, _, _ in _native.PERF_API] == ["ps_perf_copy_f32_async"]
+    assert "ps_perf_copy_f32_async" in out
 
 
 def test_sigbit_matches_oracle_with_ties():

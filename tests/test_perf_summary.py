@@ -22,6 +22,9 @@ SDDMM128 = "void ps::(anonymous namespace)::sddmm_kernel<4, true, 0>(ps::SddmmAr
 SDDMM32 = "void ps::(anonymous namespace)::sddmm_kernel<1, true, 0>(ps::SddmmArgs)"
 COPY = "void ps::copy_f32_kernel(float*, float const*, unsigned long)"
 PRE = "void ps::rank_small_kernel(int const*, int, int const*)"
+FILL = "void ps::(anonymous namespace)::fill_random_kernel(float*, unsigned long)"
+HUB = "void ps::(anonymous namespace)::hub_sddmm_kernel<16, true>(ps::HubSddmmArgs)"
+GATHER = "ps::(anonymous namespace)::gather_rows_kernel(float const*, int const*, int)"
 
 
 def counter_db(path, counter, dispatches):
@@ -39,12 +42,18 @@ def counter_db(path, counter, dispatches):
 def workload(values):
     """The perf workload's dispatch order: a warm-up and a timed copy, a
     preprocessing kernel, then each C1 operator 1 + 3 times (values[i] for
-    operator i; the copy gets values['copy'])."""
+    operator i; the copy gets values['copy']), its operands filled by a kernel
+    first; SDDMM N=128 calls are followed by two hub block kernels (a gather
+    and the product, values['hub'] each, when given)."""
     out = [(COPY, 1 << 20, values["copy"])] * 2 + [(PRE, 4096, 7.0)]
     # SpMM N=32 and N=128 share a kernel and differ in grid (32-column slices)
     launches = [(SPMM32, 1000), (SPMM128, 4000), (SDDMM128, 3000), (SDDMM32, 3000)]
     for (kernel, grid), v in zip(launches, values["ops"]):
-        out += [(kernel, grid, v)] * 4
+        out.append((FILL, 512, 1e6))  # not part of any call
+        call = [(kernel, grid, v)]
+        if kernel == SDDMM128 and "hub" in values:
+            call += [(GATHER, 64, values["hub"]), (HUB, 128, values["hub"])]
+        out += call * 4
     return out
 
 
@@ -61,16 +70,19 @@ def dbs(tmp_path):
     con.close()
     # FETCH reads the 1 GiB copy as 2 GiB (factor 0.5), WRITE as 1 GiB (factor 1)
     fetch = counter_db(tmp_path / "f.db", "FETCH_SIZE",
-                       workload({"copy": 2 * (1 << 30) / KIB, "ops": [1000, 2000, 3000, 4000]}))
+                       workload({"copy": 2 * (1 << 30) / KIB, "ops": [1000, 2000, 3000, 4000],
+                                 "hub": 100}))
     write = counter_db(tmp_path / "w.db", "WRITE_SIZE",
                        workload({"copy": (1 << 30) / KIB, "ops": [10, 20, 30, 40]}))
-    # hit rates 45, 30, 25, 40 % from TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)
+    # hit rates 45, 30, 25 (with the hub kernels: (250 + 2 * 375) / 2000 = 50),
+    # 40 % from TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum), over each call
     l2 = counter_db(tmp_path / "l2.db", "TCC_HIT_sum",
-                    workload({"copy": 1.0, "ops": [450.0, 300.0, 250.0, 40.0]}))
+                    workload({"copy": 1.0, "ops": [450.0, 300.0, 250.0, 40.0], "hub": 375.0}))
     con = sqlite3.connect(l2)
     con.executemany("insert into counters_collection values (?, ?, ?, ?, ?)",
                     [(100 + i, k, g, "TCC_MISS_sum", v) for i, (k, g, v) in enumerate(
-                        workload({"copy": 1.0, "ops": [550.0, 700.0, 750.0, 60.0]}))])
+                        workload({"copy": 1.0, "ops": [550.0, 700.0, 750.0, 60.0],
+                                  "hub": 125.0}))])
     con.commit()
     con.close()
     valu = tmp_path / "v.db"
@@ -93,13 +105,18 @@ def test_summary_traffic_and_counters(dbs, tmp_path, capsys):
     assert summary["calibration"] == {"fetch": 0.5, "write": 1.0}
     t = summary["traffic"]
     assert list(t) == ["spmm_N32", "spmm_N128", "sddmm_N128", "sddmm_N32"]
-    # bytes = KiB * 1024 * calibration factor
+    # bytes = KiB * 1024 * calibration factor; a call's bytes include the hub
+    # kernels after the sparse launch, the operand fills belong to no call
     assert t["spmm_N32"]["fetch_bytes"] == 1000 * KIB * 0.5
     assert t["sddmm_N32"]["write_bytes"] == 40 * KIB
-    assert t["sddmm_N128"]["traffic_bytes"] == 3000 * KIB * 0.5 + 30 * KIB
+    assert t["sddmm_N128"]["traffic_bytes"] == (3000 + 2 * 100) * KIB * 0.5 + 30 * KIB
+    assert t["sddmm_N128"]["kernel_traffic_bytes"] == 3000 * KIB * 0.5 + 30 * KIB
+    assert t["sddmm_N128"]["kernels_per_call"] == 3 and t["spmm_N128"]["kernels_per_call"] == 1
+    assert t["spmm_N128"]["traffic_bytes"] == t["spmm_N128"]["kernel_traffic_bytes"]
     c = summary["counters"]
     assert c["spmm_N128"] == {"l2_hit_pct": 30.0, "valu_busy_pct": 12.0,
                               "valu_utilization_pct": 91.0}
+    assert c["sddmm_N128"]["l2_hit_pct"] == 50.0
     assert c["sddmm_N32"]["l2_hit_pct"] == 40.0
     # kernel table: busiest first (dispatches x mean duration)
     table = summary["kernels"]
@@ -117,7 +134,7 @@ def test_bench_reads_counters(dbs, tmp_path, monkeypatch):
                "--json", str(profiles / "traffic_C1.json")])
     monkeypatch.setattr(bench, "ROOT", str(tmp_path))
     traffic, counters, src, note = bench.measured_counters("C1", "sddmm", 128)
-    assert traffic == 3000 * KIB * 0.5 + 30 * KIB
+    assert traffic == (3000 + 2 * 100) * KIB * 0.5 + 30 * KIB  # the whole call
     assert counters["valu_busy_pct"] == 13.0 and src == os.path.join("profiles", "traffic_C1.json")
     assert "same kernel sources" in note
     assert bench.measured_counters("C4", "spmm", 64) == (None, {}, None, "no profile summary")
@@ -140,13 +157,16 @@ def test_operator_calls_take_the_hub_kernels_that_follow():
     """A call is the operator kernel's dispatch plus the dispatches after it up
     to the next operator kernel; calls take the workload's operators in turn;
     dispatches before the first operator kernel belong to no call."""
-    GEMM = "Cijk_Ailk_Bljk_S_B"
-    SAMPLE = "void ps::(anonymous namespace)::sample_kernel(ps::SampleArgs, float const*)"
+    HUB_SPMM = "void ps::(anonymous namespace)::hub_spmm_kernel<4, 4>(ps::HubSpmmArgs)"
+    HUB_SDDMM = "void ps::(anonymous namespace)::hub_sddmm_kernel<16, true>(ps::HubSddmmArgs)"
+    GATHER = "ps::(anonymous namespace)::gather_rows_kernel(float const*, int const*, int)"
+    assert perf.kernel_op(HUB_SPMM) is None and perf.kernel_op(HUB_SDDMM) is None
+    assert perf.kernel_op(SDDMM128) == ("sddmm", 4) and perf.kernel_op(SPMM32) == ("spmm", 8)
     seq = [(PRE, 4096, 50.0)]
     for _ in range(3):  # three steps of C3: SpMM 32, SpMM 128, SDDMM 128
-        seq += [(SPMM32, 1000, 1300.0), (GEMM, 64, 140.0), (GEMM, 64, 60.0),
-                (SPMM128, 4000, 5100.0), (GEMM, 64, 340.0),
-                (SDDMM128, 3000, 5500.0), (GEMM, 64, 430.0), (SAMPLE, 512, 340.0)]
+        seq += [(SPMM32, 1000, 1300.0), (HUB_SPMM, 64, 140.0), (HUB_SPMM, 64, 60.0),
+                (SPMM128, 4000, 5100.0), (HUB_SPMM, 64, 340.0),
+                (SDDMM128, 3000, 5500.0), (GATHER, 64, 430.0), (HUB_SDDMM, 512, 340.0)]
     got = perf.operator_calls(seq, [("spmm", 32), ("spmm", 128), ("sddmm", 128)])
     assert got == {"spmm_N32": (3, 3, 1500.0), "spmm_N128": (3, 2, 5440.0),
                    "sddmm_N128": (3, 3, 6270.0)}
