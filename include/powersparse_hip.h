@@ -69,6 +69,16 @@ int ps_device_synchronize(void);
  * benchmark_utils.h:13-37). ps_free(NULL) is a no-op. */
 int ps_malloc(void** ptr, size_t bytes);
 int ps_free(void* ptr);
+/* Debugging aid, no reference counterpart. With the environment variable
+ * PS_DEVICE_GUARD set to a byte count when the library is first used, every
+ * device block the library allocates (ps_malloc, and the temporaries of the
+ * entry points below) is surrounded by that many bytes (rounded up to a
+ * multiple of 256) of a known pattern, which ps_free checks on the host
+ * before it frees the block (the device is synchronised first). Returns the
+ * number of guard bytes found changed so far, freed blocks and live ones
+ * (each run is also reported on stderr); -1 when guards are off, -2 when the
+ * device cannot be synchronised. */
+long long ps_guard_violations(void);
 /* Free and total device memory of the current device, in bytes (hipMemGetInfo).
  * No reference counterpart: callers and tests use it to check that a matrix
  * releases every device allocation it made. */

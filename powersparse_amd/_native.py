@@ -92,6 +92,7 @@ class HubBlock(ctypes.Structure):
 # (name, restype, argtypes) of every exported entry point. Tests check that
 # each symbol declared in include/*.h is exported.
 HIP_API = [
+    ("ps_guard_violations", ctypes.c_longlong, []),
     ("ps_last_error", ctypes.c_char_p, []),
     ("ps_set_device", ctypes.c_int, [ctypes.c_int]),
     ("ps_get_device", ctypes.c_int, [c_int_p]),

@@ -23,6 +23,15 @@ inline int fail(int code, const std::string& msg) {
 
 inline hipStream_t to_hip(ps_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Device temporaries of the entry points go through ps_malloc / ps_free, so
+// they get the allocation guards (PS_DEVICE_GUARD) like every other block.
+template <typename T>
+inline hipError_t dev_malloc(T** p, size_t bytes) {
+  return ps_malloc(reinterpret_cast<void**>(p), bytes) == PS_OK ? hipSuccess
+                                                                : hipErrorOutOfMemory;
+}
+inline void dev_free(void* p) { (void)ps_free(p); }
+
 // The kernels move dense rows and staged nonzeros with 128-bit accesses.
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

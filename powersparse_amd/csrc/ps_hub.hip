@@ -985,7 +985,7 @@ int ps_hub_sddmm_plan(const ps_hub_block* hb, int workset_count, const ps_workse
   const size_t bytes = 2 * ps::round256(size_t(tile_count) * 4) + 4 * ps::round256(size_t(n) * 4) +
                        ps::round256(size_t(n) * 2) + ps::round256(rw);
   char* base = nullptr;
-  PS_HIP(hipMalloc(&base, bytes));
+  PS_HIP(ps::dev_malloc(&base, bytes));
   char* q = base;
   auto take = [&q](size_t b) {
     char* r = q;
@@ -1026,7 +1026,7 @@ int ps_hub_sddmm_plan(const ps_hub_block* hb, int workset_count, const ps_workse
     e = hipGetLastError();
   }
   if (e == hipSuccess) e = hipStreamSynchronize(st);
-  (void)hipFree(base);
+  ps::dev_free(base);
   if (r != PS_OK) return r;
   PS_HIP(e);
   return PS_OK;

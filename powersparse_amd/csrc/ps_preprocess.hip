@@ -1152,14 +1152,14 @@ int bits_for(uint64_t v) {  // bits needed to hold values 0..v
 }
 
 // One device allocation cut into 256-byte aligned arrays, freed when the
-// object leaves scope (hipFree waits for the device, so queued work that still
-// reads the arrays completes first).
+// object leaves scope (the free waits for the device, so queued work that
+// still reads the arrays completes first).
 class Scratch {
  public:
   static size_t bytes(size_t n, size_t elem) { return (n * elem + 255) & ~size_t(255); }
-  explicit Scratch(size_t total) : err_(hipMalloc(&base_, total ? total : 1)) {}
+  explicit Scratch(size_t total) : err_(dev_malloc(&base_, total ? total : 1)) {}
   ~Scratch() {
-    if (base_) (void)hipFree(base_);
+    if (base_) dev_free(base_);
   }
   Scratch(const Scratch&) = delete;
   Scratch& operator=(const Scratch&) = delete;
@@ -1204,7 +1204,7 @@ int ps_pre_degree_sums(const int* row_ptr, int rows, unsigned long long* sums_ho
   PS_CHECK_ARG(row_ptr && rows > 0 && sums_host, "ps_pre_degree_sums: bad argument");
   hipStream_t st = ps::to_hip(stream);
   unsigned long long* d_sums = nullptr;
-  PS_HIP(hipMalloc(&d_sums, 32 * sizeof(unsigned long long)));
+  PS_HIP(ps::dev_malloc(&d_sums, 32 * sizeof(unsigned long long)));
   hipError_t e = hipMemsetAsync(d_sums, 0, 32 * sizeof(unsigned long long), st);
   if (e == hipSuccess) {
     const unsigned grid = ps::grid_for(size_t(rows)) < 4096 ? ps::grid_for(size_t(rows)) : 4096;
@@ -1215,7 +1215,7 @@ int ps_pre_degree_sums(const int* row_ptr, int rows, unsigned long long* sums_ho
     e = hipMemcpyAsync(sums_host, d_sums, 32 * sizeof(unsigned long long),
                        hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
-  (void)hipFree(d_sums);
+  ps::dev_free(d_sums);
   PS_HIP(e);
   return PS_OK;
 }
@@ -1418,7 +1418,7 @@ int ps_pre_signature_span(const uint32_t* sig, int groups, int words, uint32_t* 
     init[2 * w + 1] = ~0u;
   }
   uint32_t* d = nullptr;
-  PS_HIP(hipMalloc(&d, init.size() * sizeof(uint32_t)));
+  PS_HIP(ps::dev_malloc(&d, init.size() * sizeof(uint32_t)));
   hipError_t e = hipMemcpyAsync(d, init.data(), init.size() * sizeof(uint32_t),
                                 hipMemcpyHostToDevice, st);
   if (e == hipSuccess) {
@@ -1430,7 +1430,7 @@ int ps_pre_signature_span(const uint32_t* sig, int groups, int words, uint32_t* 
   if (e == hipSuccess)
     e = hipMemcpyAsync(init.data(), d, init.size() * sizeof(uint32_t), hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
-  (void)hipFree(d);
+  ps::dev_free(d);
   PS_HIP(e);
   for (int w = 0; w < words; ++w) {
     or_host[w] = init[2 * w];
@@ -1495,11 +1495,11 @@ int ps_pre_gather_workset(int group_size, const uint32_t* perm, int groups,
   uint64_t *keys = nullptr, *keys_alt = nullptr;
   uint32_t *vals = nullptr, *vals_alt = nullptr;
   void* ws = nullptr;
-  hipError_t e = hipMalloc(&keys, total * sizeof(uint64_t));
-  if (e == hipSuccess) e = hipMalloc(&keys_alt, total * sizeof(uint64_t));
-  if (e == hipSuccess) e = hipMalloc(&vals, total * sizeof(uint32_t));
-  if (e == hipSuccess) e = hipMalloc(&vals_alt, total * sizeof(uint32_t));
-  if (e == hipSuccess) e = hipMalloc(&ws, ps_radix_workspace_bytes(total));
+  hipError_t e = ps::dev_malloc(&keys, total * sizeof(uint64_t));
+  if (e == hipSuccess) e = ps::dev_malloc(&keys_alt, total * sizeof(uint64_t));
+  if (e == hipSuccess) e = ps::dev_malloc(&vals, total * sizeof(uint32_t));
+  if (e == hipSuccess) e = ps::dev_malloc(&vals_alt, total * sizeof(uint32_t));
+  if (e == hipSuccess) e = ps::dev_malloc(&ws, ps_radix_workspace_bytes(total));
   int rc = PS_OK;
   if (e == hipSuccess) {
     ps::large_group_keys_kernel<<<ps::grid_for(total), ps::kThreads, 0, st>>>(
@@ -1518,11 +1518,11 @@ int ps_pre_gather_workset(int group_size, const uint32_t* perm, int groups,
     e = hipGetLastError();
   }
   if (e == hipSuccess && rc == PS_OK) e = hipStreamSynchronize(st);
-  (void)hipFree(keys);
-  (void)hipFree(keys_alt);
-  (void)hipFree(vals);
-  (void)hipFree(vals_alt);
-  (void)hipFree(ws);
+  ps::dev_free(keys);
+  ps::dev_free(keys_alt);
+  ps::dev_free(vals);
+  ps::dev_free(vals_alt);
+  ps::dev_free(ws);
   if (rc != PS_OK) return rc;
   PS_HIP(e);
   return PS_OK;

@@ -151,7 +151,7 @@ int build_order(int op, int N, int workset_count, const ps_workset* worksets,
   auto round = [](size_t b) { return (b + 255) & ~size_t(255); };
   const size_t bytes = 3 * round(n * 4) + round(radix_ws) + 256;
   char* base = nullptr;
-  PS_HIP(hipMalloc(&base, bytes));
+  PS_HIP(ps::dev_malloc(&base, bytes));
   uint32_t* keys = reinterpret_cast<uint32_t*>(base);
   uint32_t* keys_alt = reinterpret_cast<uint32_t*>(base + round(n * 4));
   uint32_t* vals = reinterpret_cast<uint32_t*>(base + 2 * round(n * 4));
@@ -176,7 +176,7 @@ int build_order(int op, int N, int workset_count, const ps_workset* worksets,
   if (e == hipSuccess && r == PS_OK)
     e = hipMemcpyAsync(&host_skipped, skipped, sizeof(host_skipped), hipMemcpyDeviceToHost, st);
   if (e == hipSuccess) e = hipStreamSynchronize(st);
-  (void)hipFree(base);
+  ps::dev_free(base);
   if (r != PS_OK) return r;
   PS_HIP(e);
   if (kept) *kept = a.total - host_skipped;

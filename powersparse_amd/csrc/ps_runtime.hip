@@ -1,7 +1,12 @@
 // Device, memory, stream and event entry points of the C ABI, plus the
 // counter-based random fill used for synthetic dense operands.
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <unordered_map>
+#include <vector>
 
 #include "ps_common.hpp"
 
@@ -9,7 +14,65 @@ namespace ps {
 
 namespace {
 thread_local std::string g_last_error;
+
+// Device allocation guards (debugging aid, off unless PS_DEVICE_GUARD names a
+// byte count): every ps_malloc block gets that many bytes of a known pattern
+// before and after it (the count rounded up to a multiple of 256, so blocks
+// keep their alignment). ps_free and ps_guard_violations read the guards back
+// on the host; a changed byte means some device code wrote outside the block.
+constexpr unsigned char kGuardByte = 0xA5;
+struct Guarded {
+  char* base;    // what hipMalloc returned
+  size_t bytes;  // the caller's size
+};
+struct GuardState {
+  size_t guard = 0;
+  std::mutex mu;
+  std::unordered_map<void*, Guarded> live;
+  size_t violations = 0;
+};
+GuardState& guards() {
+  static GuardState* g = [] {
+    auto* s = new GuardState;  // never destroyed: frees may come from any exit path
+    if (const char* v = std::getenv("PS_DEVICE_GUARD")) {
+      const long long n = std::atoll(v);
+      if (n > 0) s->guard = (size_t(n) + 255) & ~size_t(255);
+    }
+    return s;
+  }();
+  return *g;
 }
+// Checks both guards of one block (device synchronised by the caller); the
+// number of changed bytes, each run of them reported on stderr.
+size_t check_guards(size_t guard, void* user, const Guarded& a) {
+  std::vector<unsigned char> h(guard);
+  size_t bad = 0;
+  const char* where[2] = {"before", "after"};
+  const char* src[2] = {a.base, a.base + guard + a.bytes};
+  for (int k = 0; k < 2; ++k) {
+    if (hipMemcpy(h.data(), src[k], guard, hipMemcpyDeviceToHost) != hipSuccess) {
+      std::fprintf(stderr, "ps guard: cannot read the guard %s block %p\n", where[k], user);
+      ++bad;
+      continue;
+    }
+    size_t first = guard, last = 0, n = 0;
+    for (size_t i = 0; i < guard; ++i)
+      if (h[i] != kGuardByte) {
+        first = i < first ? i : first;
+        last = i;
+        ++n;
+      }
+    if (n) {
+      std::fprintf(stderr,
+                   "ps guard: %zu byte(s) written %s the %zu-byte block at %p (guard offsets "
+                   "%zu..%zu of %zu)\n",
+                   n, where[k], a.bytes, user, first, last, guard);
+      bad += n;
+    }
+  }
+  return bad;
+}
+}  // namespace
 
 void set_error(const std::string& msg) { g_last_error = msg; }
 void clear_error() { g_last_error.clear(); }
@@ -113,13 +176,56 @@ int ps_malloc(void** ptr, size_t bytes) {
   PS_CHECK_ARG(ptr, "ps_malloc: null output");
   *ptr = nullptr;
   if (bytes == 0) return PS_OK;
-  PS_HIP(hipMalloc(ptr, bytes));
+  ps::GuardState& g = ps::guards();
+  if (g.guard == 0) {
+    PS_HIP(hipMalloc(ptr, bytes));
+    return PS_OK;
+  }
+  char* base = nullptr;
+  PS_HIP(hipMalloc(reinterpret_cast<void**>(&base), bytes + 2 * g.guard));
+  hipError_t e = hipMemset(base, ps::kGuardByte, g.guard);
+  if (e == hipSuccess) e = hipMemset(base + g.guard + bytes, ps::kGuardByte, g.guard);
+  if (e != hipSuccess) {
+    (void)hipFree(base);
+    PS_HIP(e);
+  }
+  *ptr = base + g.guard;
+  std::lock_guard<std::mutex> lock(g.mu);
+  g.live[*ptr] = ps::Guarded{base, bytes};
   return PS_OK;
 }
 
 int ps_free(void* ptr) {
-  if (ptr) PS_HIP(hipFree(ptr));
+  if (!ptr) return PS_OK;
+  ps::GuardState& g = ps::guards();
+  if (g.guard) {
+    std::unique_lock<std::mutex> lock(g.mu);
+    auto it = g.live.find(ptr);
+    if (it != g.live.end()) {
+      const ps::Guarded a = it->second;
+      g.live.erase(it);
+      lock.unlock();
+      PS_HIP(hipDeviceSynchronize());
+      const size_t bad = ps::check_guards(g.guard, ptr, a);
+      lock.lock();
+      g.violations += bad;
+      lock.unlock();
+      PS_HIP(hipFree(a.base));
+      return PS_OK;
+    }
+  }
+  PS_HIP(hipFree(ptr));
   return PS_OK;
+}
+
+long long ps_guard_violations(void) {
+  ps::GuardState& g = ps::guards();
+  if (g.guard == 0) return -1;
+  if (hipDeviceSynchronize() != hipSuccess) return -2;
+  std::lock_guard<std::mutex> lock(g.mu);
+  size_t bad = g.violations;
+  for (const auto& kv : g.live) bad += ps::check_guards(g.guard, kv.first, kv.second);
+  return (long long)bad;
 }
 
 int ps_mem_get_info(size_t* free_bytes, size_t* total_bytes) {
