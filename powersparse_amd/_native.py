@@ -2,6 +2,8 @@
 
 lib/libpowersparse_hip.so     HIP kernels + C ABI        (include/powersparse_hip.h)
 lib/libpowersparse.so         C++17 host API, C facade   (include/powersparse.h)
+lib/libpowersparse_bench.so   the CSV benchmark harness (include/powersparse_bench.h),
+                              loaded on demand (bench())
 lib/libpowersparse_perf.so    the measurement tooling's calibration copy (not
                               product code), loaded only by powersparse_amd.perf
                               (perf_lib())
@@ -16,6 +18,7 @@ LIB_DIR = os.path.join(_HERE, "lib")
 HIP_LIB_PATH = os.path.join(LIB_DIR, "libpowersparse_hip.so")
 HOST_LIB_PATH = os.path.join(LIB_DIR, "libpowersparse.so")
 PERF_LIB_PATH = os.path.join(LIB_DIR, "libpowersparse_perf.so")
+BENCH_LIB_PATH = os.path.join(LIB_DIR, "libpowersparse_bench.so")
 
 PS_OK = 0
 PS_ERR_INVALID = 1
@@ -247,6 +250,10 @@ HIP_API = [
       c_void_p, c_void_p, c_void_p, c_void_p]),
 ]
 
+BENCH_API = [
+    ("psx_bench_main", ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_char_p)]),
+]
+
 PERF_API = [
     ("ps_perf_copy_f32_async", ctypes.c_int, [c_void_p, c_void_p, ctypes.c_size_t, c_void_p]),
 ]
@@ -315,6 +322,7 @@ HOST_API = [
 _hip = None
 _host = None
 _perf = None
+_bench = None
 
 
 def _bind(lib, api):
@@ -348,6 +356,20 @@ def hip():
 
 def host():
     return libs()[1]
+
+
+def bench():
+    """Loads (once) and returns the CSV benchmark harness library."""
+    global _bench
+    if _bench is None:
+        libs()
+        if not os.path.exists(BENCH_LIB_PATH):
+            raise ImportError(f"powersparse_amd: {BENCH_LIB_PATH} is missing; "
+                              "build it with `make -C powersparse_amd`")
+        lib = ctypes.CDLL(BENCH_LIB_PATH)
+        _bind(lib, BENCH_API)
+        _bench = lib
+    return _bench
 
 
 def perf_lib():

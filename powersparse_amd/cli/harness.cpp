@@ -1,4 +1,6 @@
-// powersparse_spmm / powersparse_sddmm: the CSV benchmark command line.
+// The CSV benchmark harness behind powersparse_spmm / powersparse_sddmm
+// (cli/main.cpp), as a library entry point (psx_bench_main,
+// include/powersparse_bench.h) so that callers can also run it in process:
 //
 //   powersparse_{spmm,sddmm} MATRIX N DEVICE CHECK REPEATS
 //   powersparse_{spmm,sddmm} --header
@@ -42,11 +44,8 @@
 #include "PowerSparse_SpMM.h"
 #include "device_buffer.h"
 #include "matrix_market.h"
+#include "powersparse_bench.h"
 #include "synth.h"
-
-#ifndef POWERSPARSE_BENCH_SDDMM
-#define POWERSPARSE_BENCH_SDDMM 0
-#endif
 
 namespace {
 
@@ -55,8 +54,6 @@ using PowerSparse::HostCsr;
 using PowerSparse::PowerSparseMatrixGPU;
 using PowerSparse::ThrowOnError;
 
-constexpr bool kIsSddmm = POWERSPARSE_BENCH_SDDMM != 0;
-constexpr const char* kOpName = kIsSddmm ? "SDDMM" : "SpMM";
 constexpr int kWarmupCalls = 30;
 constexpr unsigned kInputSeed = 1;
 constexpr const char* kCsvHeader =
@@ -388,7 +385,8 @@ double TimeCalls(Workload& w, int calls) {
   return double(ms) / calls;
 }
 
-int Bench(const Spec& spec) {
+int Bench(const Spec& spec, bool sddmm) {
+  const char* const kOpName = sddmm ? "SDDMM" : "SpMM";
   const DeviceInfo dev = OpenDevice(spec.device);
   std::cerr << kOpName << ": " << spec.matrix << ", N=" << spec.n << ", GPU=" << dev.name << " ("
             << dev.arch << ")\n";
@@ -405,7 +403,7 @@ int Bench(const Spec& spec) {
 
   std::mt19937 rng(kInputSeed);
   std::unique_ptr<Workload> work;
-  if (kIsSddmm) work = std::make_unique<SddmmWorkload>(matrix, spec.n, rng);
+  if (sddmm) work = std::make_unique<SddmmWorkload>(matrix, spec.n, rng);
   else work = std::make_unique<SpmmWorkload>(matrix, spec.n, rng);
 
   auto clear = [&] {
@@ -442,14 +440,20 @@ int Bench(const Spec& spec) {
 
 }  // namespace
 
-int main(int argc, char** argv) {
+int psx_bench_main(int op, int argc, char** argv) {
+  const bool sddmm = op == PSX_BENCH_SDDMM;
+  const char* const kOpName = sddmm ? "SDDMM" : "SpMM";
   try {
+    if (op != PSX_BENCH_SPMM && op != PSX_BENCH_SDDMM) {
+      std::cerr << "Error: unknown benchmark operator " << op << '\n';
+      return 1;
+    }
     if (argc == 2 && std::strcmp(argv[1], "--header") == 0) {
-      std::cout << kCsvHeader << '\n';
+      std::cout << kCsvHeader << std::endl;
       return 0;
     }
     if (argc != 6) {
-      PrintUsage(argv[0]);
+      PrintUsage(argc > 0 ? argv[0] : (sddmm ? "powersparse_sddmm" : "powersparse_spmm"));
       return 2;
     }
     const int n = WholeInt(argv[2], "N");
@@ -458,7 +462,7 @@ int main(int argc, char** argv) {
                 << " was not selected in main; please use N=32, 64 or 128.\n";
       return 2;
     }
-    return Bench(ParseSpec(argv));
+    return Bench(ParseSpec(argv), sddmm);
   } catch (const std::exception& e) {
     std::cerr << "Error: " << e.what() << '\n';
     return 1;

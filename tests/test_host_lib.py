@@ -22,18 +22,20 @@ def declared(header):
     return sorted(set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b((?:ps|psx)_\w+)\s*\(", text, re.M)))
 
 
-@pytest.mark.parametrize("header,libpath", [
-    ("powersparse_hip.h", _native.HIP_LIB_PATH), ("powersparse.h", _native.HOST_LIB_PATH)])
-def test_every_declared_symbol_is_exported(header, libpath):
+@pytest.mark.parametrize("header,libpath,minimum", [
+    ("powersparse_hip.h", _native.HIP_LIB_PATH, 4), ("powersparse.h", _native.HOST_LIB_PATH, 4),
+    ("powersparse_bench.h", _native.BENCH_LIB_PATH, 1)])
+def test_every_declared_symbol_is_exported(header, libpath, minimum):
     _native.libs()
+    _native.bench()
     names = declared(header)
-    assert len(names) >= 4
+    assert len(names) >= minimum
     out = subprocess.run(["nm", "-D", "--defined-only", libpath], capture_output=True, text=True,
                          check=True).stdout
     exported = set(line.split()[-1] for line in out.splitlines() if line.strip())
     missing = [n for n in names if n not in exported]
     assert not missing, missing
-    bound = {n for n, _, _ in (_native.HIP_API + _native.HOST_API)}
+    bound = {n for n, _, _ in (_native.HIP_API + _native.HOST_API + _native.BENCH_API)}
     assert not [n for n in names if n not in bound]
 
 
