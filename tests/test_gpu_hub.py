@@ -207,6 +207,59 @@ def test_hub_block_nonfinite_b():
     off.close()
 
 
+def test_hub_block_repeated_slots_keep_per_entry_products():
+    """A (hub row, hot column) slot stored twice stays out of the block: SpMM
+    adds a1 * b + a2 * b as the reference does, not (a1 + a2) * b. With a1 =
+    a2 = 3e38 and b = 1e-10 the sum of the values overflows to Inf while the
+    per-entry products stay finite; with non-exact values (0.1, 0.7) the rows
+    match the oracle within the FP32 tolerance, and a second build of the same
+    matrix gives the same rows (up to the order of the sparse kernels' atomic
+    additions)."""
+    setup()
+    g = gd.load("hubs")
+    th = thresholds(csr_of(g), 1)
+    d_min, c_min = th[0]
+    deg = np.diff(g.row_ptr.astype(np.int64))
+    cnt = np.bincount(g.col_ind, minlength=g.cols)
+    hub_rows = np.flatnonzero(deg >= d_min)
+    hot = np.flatnonzero(cnt >= c_min)
+    rows = [list(g.col_ind[g.row_ptr[r]:g.row_ptr[r + 1]]) for r in range(g.rows)]
+    vals = [list(g.values[g.row_ptr[r]:g.row_ptr[r + 1]]) for r in range(g.rows)]
+    r1, r2 = int(hub_rows[0]), int(hub_rows[-1])
+    c1 = int(next(c for c in hot if c not in rows[r1]))
+    c2 = int(next(c for c in hot if c not in rows[r2] and c != c1))
+    rows[r1] += [c1, c1]
+    vals[r1] += [3e38, 3e38]
+    rows[r2] += [c2, c2]
+    vals[r2] += [0.1, 0.7]
+    rp = np.concatenate([[0], np.cumsum([len(x) for x in rows])]).astype(np.int32)
+    ci = np.concatenate([np.asarray(x, np.int32) for x in rows])
+    sv = np.concatenate([np.asarray(x, np.float32) for x in vals])
+    csr = ps.HostCsr(g.rows, g.cols, rp, ci, sv)
+    N = 64
+    rng = np.random.default_rng(9)
+    B = rng.uniform(-1, 1, (g.cols, N)).astype(np.float32)
+    B[c1, :] = 1e-10
+    results = []
+    for build in range(2):
+        m = ps.PowerSparseMatrixGPU.from_csr(csr, cu_count=1, hub_thresholds=[(d_min, c_min)])
+        assert m.hub_block, "the block was not built"
+        dB, dC = ps.DeviceBuffer(host=B), ps.DeviceBuffer.zeros(g.rows * N * 4)
+        S = m.GroupTypeNum()
+        ps.SpMM(m, N, dB, dC, S, [ps.Stream() for _ in range(S)] if S > 1 else None)
+        ps.synchronize()
+        results.append(dC.download(np.float32).reshape(g.rows, N))
+        m.close()
+    C = results[0]
+    assert np.isfinite(C).all(), "a repeated slot's values were summed before the product"
+    E, M = oracle.spmm(rp, ci, sv, N, B, with_mag=True)
+    say("  ", tolerance.check(C, E, M, "SpMM with repeated block slots"))
+    # the sparse kernels' atomics add in no fixed order; rows r1 and r2 hold
+    # the repeated slots, compare them and the overflow row exactly across builds
+    np.testing.assert_array_equal(np.isfinite(results[1]), np.isfinite(C))
+    np.testing.assert_allclose(results[1][[r1, r2]], C[[r1, r2]], rtol=1e-5, atol=1e-5)
+
+
 @pytest.mark.parametrize("cfg,scale", [("C3", 40), ("C1", 20)])
 def test_hub_block_on_power_law_graphs(cfg, scale):
     """Scaled power-law graphs with an explicit block against the oracle's
