@@ -346,7 +346,7 @@ int ps_hub_tile_flags(const ps_hub_block* hb, const ps_workset* workset, uint8_t
 /* Device workspace bytes at width N of ps_hub_spmm_launch (op PS_OP_SPMM: one
  * feature slice, up to 128, of B's hot rows in fragment order, and flags) or
  * of ps_hub_sddmm_launch (PS_OP_SDDMM: lhs[hub_rows] and rhs[hot_cols] in
- * fragment order, rows padded to 64 and 256). */
+ * fragment order, rows padded to 64 and 128). */
 size_t ps_hub_workspace_bytes(const ps_hub_block* hb, int op, int N);
 /* C[hub_rows[i], :] += sum over stored block slots (i, h) of value * B[hot_cols[h], :],
  * B (matrix_cols x N) and C (matrix_rows x N) row-major, added with float
@@ -360,7 +360,7 @@ int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, 
  * inside the block); codes that name no such tile, and entries outside the
  * block, are left out of the plan. The plan (ps_hub_sddmm_plan_bytes bytes of
  * device memory) groups the listed nonzeros by the dense tile (64 hub rows x
- * 256 hot columns) they fall in, each with its output position and sp_data;
+ * 128 hot columns) they fall in, each with its output position and sp_data;
  * ps_hub_sddmm_plan allocates temporaries and synchronises the stream. */
 size_t ps_hub_sddmm_plan_bytes(const ps_hub_block* hb, uint32_t tile_count);
 int ps_hub_sddmm_plan(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,

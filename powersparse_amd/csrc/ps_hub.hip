@@ -20,7 +20,7 @@
 //          per-nonzero products.
 //   SDDMM: the listed tiles (64 consecutive nonzeros of a block group lying
 //          in the block) are planned at build time as per-entry records
-//          grouped by the dense tile (64 hub rows x 256 hot columns) they
+//          grouped by the dense tile (64 hub rows x 128 hot columns) they
 //          fall in. Pre-passes gather X[hub_rows] and Y[hot_cols] into
 //          fragment order; the MFMA kernel computes each dense tile of
 //          D = X[hub_rows] * Y[hot_cols]^T in registers, stages it in LDS and
@@ -79,13 +79,15 @@ constexpr uint32_t kRepeated = 0xFFFFFFFFu;
 // (the workspace's transposed copy holds one slice at a time).
 constexpr int kSpRows = 256;
 constexpr int kSpSlice = 128;
-// SDDMM: dense tile of a workgroup (4 waves, each 64 rows x 64 columns), and
+// SDDMM: dense tile of a workgroup (4 waves, each 64 rows x 32 columns), and
 // the padded LDS row (a row 4 apart starts 32 banks over: the two half-waves
 // of an MFMA result register write disjoint banks).
 constexpr int kSdRows = 64;
-constexpr int kSdCols = 256;
+constexpr int kSdCols = 128;
 constexpr int kSdLd = kSdCols + 8;
-constexpr int kSdCoordBits = 14;  // 6 row bits + 8 column bits of an entry's tile coordinate
+// an entry's place in the LDS copy of its dense tile: row * kSdLd + column
+constexpr int kSdCoordBits = 15;
+static_assert(kSdRows * kSdLd <= (1 << kSdCoordBits), "tile coordinate field too narrow");
 constexpr int kPosBits = 32;
 constexpr int kWsBits = 5;        // PS_MAX_WORKSETS = 32
 static_assert(PS_MAX_WORKSETS <= (1 << kWsBits), "workset index field too narrow");
@@ -486,7 +488,8 @@ __device__ __forceinline__ bool tile_valid(const Worksets& a, uint32_t code) {
 // Entry e = 64 t + j of the (code-sorted) list: keys[e] = its dense tile
 // (kSdRows hub rows x kSdCols hot columns, row-panel major), or `T` (one past
 // the last tile) when the code names no tile or the entry lies outside the
-// block; coords[e] = its row and column inside the tile; vals[e] = e.
+// block; coords[e] = its place in the tile's LDS copy (row * kSdLd + column);
+// vals[e] = e.
 __global__ __launch_bounds__(kThreads) void plan_keys_kernel(ps_hub_block hb, Worksets a,
                                                               const uint32_t* __restrict__ codes,
                                                               uint32_t count, uint32_t tiles_c,
@@ -506,7 +509,7 @@ __global__ __launch_bounds__(kThreads) void plan_keys_kernel(ps_hub_block hb, Wo
       const int h = hb.hot_rank[w.col_ind[p]];
       if (i >= 0 && h >= 0) {
         key = uint32_t(i / kSdRows) * tiles_c + uint32_t(h / kSdCols);
-        coords[e] = uint16_t(((i % kSdRows) << 8) | (h % kSdCols));
+        coords[e] = uint16_t((i % kSdRows) * kSdLd + h % kSdCols);
       }
     }
     keys[e] = key;
@@ -570,156 +573,310 @@ struct HubSddmmArgs {
   const uint64_t* entries;
   const float* values;
   int tiles_r, tiles_c;
-  int range;  // column tiles per workgroup
   uint32_t chunk_log2;
   float* out[PS_MAX_WORKSETS];
   const int* out_pos[PS_MAX_WORKSETS];
   float* out_csr;
 };
 
-// One workgroup: the dense tiles of one row panel (kSdRows hub rows) over a
-// range of column tiles. The 4 waves split a tile 2 x 2: wave w computes rows
-// 32 (w & 1) .. + 31 x columns 128 (w >> 1) .. + 127 (4 MFMA blocks), over
-// the K features in units of 8 KB8 (one unit per tile when kResident: the
-// wave's X fragments then stay in registers across the column tiles; else
-// K / 32 units, X reloaded per unit). Operands come in fragment order (each
-// load one contiguous 1 KB run). Y fragments stream through a ring of 4 steps
-// loaded 3 steps ahead, across unit and tile boundaries, so the next tile's
-// first loads are in flight during this tile's output phase. A finished tile
-// goes through LDS and the workgroup writes out[s][p] = value * D[r][c] for
-// the tile's planned entries (sorted by output position), 16 per thread in
-// flight. Padding rows and columns compute zeros; no entry names them.
+// Two workgroups per CU (each holds two D buffers, 68 KB of LDS), each over
+// an even share of the dense tiles in row-panel-major order (a row panel is
+// kSdRows hub rows, a tile that panel x kSdCols hot columns). The 4 waves sit
+// side by side: wave w computes all 64 rows x columns 32 w .. + 31 (two MFMA
+// blocks), over the K features in units of 8 KB8 (one unit per tile when
+// kResident: the wave's X fragments then stay in registers across a row
+// panel's tiles; else K / 32 units, X reloaded per unit). Operands come in
+// fragment order (each load one contiguous 1 KB run); no two waves load the
+// same Y. Y fragments stream through a ring of 4 steps loaded 3 steps ahead,
+// across unit and tile boundaries. A finished tile's D goes to one of the two
+// LDS buffers; while the matrix cores compute the next tile, the workgroup
+// writes out[s][p] = value * D[r][c] for the finished tile's planned entries
+// (sorted by output position), split into one chunk per 8-feature step: a
+// step stores the chunk loaded kSdOutAhead steps before and loads the chunk
+// kSdOutAhead steps after, so the plan reads and the output stores run under
+// the MFMAs. The last tile's outputs are written after the loop. Padding rows
+// and columns compute zeros; no entry names them.
+// A wave's share of a tile: kSdRb 32-row x kSdNb 32-column MFMA blocks
+constexpr int kSdWaveRows = 64;
+constexpr int kSdRb = kSdWaveRows / 32;
+constexpr int kSdNb = kSdRows * kSdCols / (4 * kSdWaveRows) / 32;
+constexpr int kSdDtBytes = 2 * kSdRows * kSdLd * 4;
+// workgroups per CU that the two D buffers leave room for in 160 KB of LDS
+constexpr int kSdWgPerCu = (160 * 1024 - 1024) / kSdDtBytes;
+static_assert(kSdWgPerCu >= 1, "D buffers exceed the LDS");
 constexpr int kSdRing = 4;
-constexpr int kSdBatch = 16;
-template <int KB8, bool kResident>
-__global__ __launch_bounds__(kThreads, 2) void hub_sddmm_kernel(HubSddmmArgs a) {
+constexpr int kSdBatch = 16;   // outputs per thread in flight in the final pass
+constexpr int kSdOutAhead = 3;  // steps between a chunk's loads and its stores
+constexpr int kSdOutSets = kSdOutAhead + 1;
+// Pipelined outputs per thread per step: a tile's steps together cover a full
+// tile (kSdRows * kSdCols entries); entries past that (only repeated nonzeros
+// make them) are written after the last tile from direct dot products.
+constexpr int sddmm_out_per(int KB8, bool resident) {
+  return resident ? (kSdRows * kSdCols / kThreads + KB8 - 1) / KB8 : 4;
+}
+using global_float = __attribute__((address_space(1))) float;
+// read-only for the kernel's lifetime: uniform reads become scalar loads (a
+// vector load there would make the wave wait for every load and store ahead)
+using const_u32 = const __attribute__((address_space(4))) uint32_t;
+template <int KB8, bool kResident, bool kCsr>
+__global__ __launch_bounds__(kThreads, kSdWgPerCu) void hub_sddmm_kernel(HubSddmmArgs a) {
   static_assert(KB8 % kSdRing == 0, "units must hold whole rings of Y steps");
-  __shared__ float dt[kSdRows * kSdLd];
+  static_assert(KB8 % kSdOutSets == 0, "units must hold whole cycles of output sets");
+  constexpr int OP = sddmm_out_per(KB8, kResident);
+  // slot counts of the three forms of a tile's steps (a tile's outputs take
+  // the smallest that holds them: a slot costs its loads whether used or not)
+  constexpr int OP1 = OP / 4 > 0 ? OP / 4 : 1, OP2 = OP / 2 > 0 ? OP / 2 : 1;
+  static_assert(kResident || 20 * OP * kThreads >= kSdRows * kSdCols,
+                "non-resident tiles (K >= 160) must cover a full tile in their steps");
+  __shared__ float dt[2][kSdRows * kSdLd];
   __shared__ float* s_out[PS_MAX_WORKSETS];
   __shared__ const int* s_pos[PS_MAX_WORKSETS];
   const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, a.chunk_log2);
-  const int rp = int(blk % uint32_t(a.tiles_r)), cr = int(blk / uint32_t(a.tiles_r));
-  const int cq0 = cr * a.range;
-  const int cq1 = cq0 + a.range < a.tiles_c ? cq0 + a.range : a.tiles_c;
-  if (cq0 >= cq1) return;  // uniform over the workgroup
+  const uint64_t T = uint64_t(a.tiles_r) * uint64_t(a.tiles_c);
+  const uint32_t t0 = uint32_t(T * blk / gridDim.x), t1 = uint32_t(T * (blk + 1) / gridDim.x);
+  if (t0 >= t1) return;  // uniform over the workgroup
+  const uint32_t tc = uint32_t(a.tiles_c);
   if (threadIdx.x < PS_MAX_WORKSETS) {
     s_out[threadIdx.x] = a.out[threadIdx.x];
     s_pos[threadIdx.x] = a.out_pos[threadIdx.x];
   }
-  const int wave = threadIdx.x / kWave, lane = lane_id(), g = lane >> 5, l32 = lane & 31;
-  const int wr = (wave & 1) * 32, wc = (wave >> 1) * 128;
+  __syncthreads();
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = lane_id(), g = lane >> 5, l32 = lane & 31;
+  constexpr int kWaveCols = kSdNb * 32;
+  constexpr int kRowWaves = kSdRows / kSdWaveRows;  // waves down a tile
+  const int wr = (wave % kRowWaves) * kSdWaveRows, wc = (wave / kRowWaves) * kWaveCols;
   const int units = kResident ? 1 : a.K / (8 * KB8);  // units per tile
-  const size_t steps = size_t(a.K / 8);               // 8-feature steps per row block
+  const int TS = units * KB8;                          // 8-feature steps per tile
+  const size_t steps = size_t(a.K / 8);                // 8-feature steps per row block
 
-  const float* xrun = a.Xf + size_t((rp * kSdRows + wr) / 32) * steps * 256 + lane * 4;
-  float4 xa[KB8];
-  if (kResident) {
-#pragma unroll
-    for (int kb = 0; kb < KB8; ++kb) xa[kb] = load4(xrun + kb * 256);
-  }
-  // step 0 of the wave's column block cb in column tile q (the last tile of
-  // the range stands in for the one past it)
-  auto y_run = [&](int q, int cb) {
-    q = q < cq1 ? q : cq1 - 1;
+  // out[s][p] (or out_csr[out_pos[s][p]]) = value * D[r][c] of one planned entry
+  auto emit = [&](uint64_t code, float v, const float* d) {
+    const float r = v * d[uint32_t(code >> (kPosBits + kWsBits))];
+    const int s = int((code >> kPosBits) & ((1u << kWsBits) - 1u));
+    if (kCsr) __builtin_nontemporal_store(r, a.out_csr + s_pos[s][uint32_t(code)]);
+    else __builtin_nontemporal_store(r, s_out[s] + uint32_t(code));
+  };
+  // The same in the pipelined form for a lane that may lie past its chunk
+  // (`live` false: its clamped entry names a place inside the tile, and it
+  // stores nothing); with nothing pending (`pend` false) the loaded entry may
+  // be no entry, so code 0 stands in.
+  auto emit_pipe = [&](uint64_t code, float v, const float* d, bool live, bool pend) {
+    if (!pend) code = 0;
+    const float r = v * d[uint32_t(code >> (kPosBits + kWsBits))];
+    const int s = int((code >> kPosBits) & ((1u << kWsBits) - 1u));
+    if (kCsr) {
+      if (live) __builtin_nontemporal_store(r, a.out_csr + s_pos[s][uint32_t(code)]);
+    } else {
+      // (the empty asm keeps the table read out of the branch: only the store
+      // depends on `live`)
+      uint64_t base = reinterpret_cast<uint64_t>(s_out[s]);
+      asm volatile("" : "+v"(base));
+      if (live) __builtin_nontemporal_store(r, (global_float*)base + uint32_t(code));
+    }
+  };
+
+  // step 0 of the wave's X rows in tile t's row panel
+  auto x_run = [&](uint32_t t) {
+    return a.Xf + size_t((int(t / tc) * kSdRows + wr) / 32) * steps * 256 + lane * 4;
+  };
+  float4 xa[KB8][kSdRb];
+  // step 0 of the wave's column block cb in tile t (the workgroup's last tile
+  // stands in for the one past it)
+  auto y_run = [&](uint32_t t, int cb) {
+    const int q = int((t < t1 ? t : t1 - 1) % tc);
     return a.Yf + size_t((q * kSdCols + wc) / 32 + cb) * steps * 256 + lane * 4;
   };
-  float4 yb[kSdRing][4];
+  float4 yb[kSdRing][kSdNb];
   // prologue: steps 0 .. kSdRing - 2 of the first unit
 #pragma unroll
   for (int j = 0; j < kSdRing - 1; ++j)
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) yb[j][cb] = load4(y_run(cq0, cb) + j * 256);
+    for (int cb = 0; cb < kSdNb; ++cb) yb[j][cb] = load4(y_run(t0, cb) + j * 256);
 
-  v16f acc[1][4];
+  v16f acc[kSdRb][kSdNb];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) acc[0][cb] = v16f{};
-  int cq = cq0, unit = 0;
-  while (true) {
-    const int f8 = unit * KB8;  // first step of this unit
-    const bool tile_end = kResident || unit + 1 == units;
-    const int t = rp * a.tiles_c + cq;
-    uint32_t e0 = 0, e1 = 0;
-    if (tile_end) {
-      e0 = a.tile_begin[t];
-      e1 = a.tile_begin[t + 1];
+  for (int rb = 0; rb < kSdRb; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < kSdNb; ++cb) acc[rb][cb] = v16f{};
+  // The finished tile whose outputs are written under the next tile's MFMAs.
+  // Its entries [pe0, pe1) go out in TS chunks of clen = ceil((pe1 - pe0) /
+  // TS) entries; chunk gs = [pe0 + gs clen, pe0 + (gs + 1) clen) cut at pe1.
+  // Before the first tile there is none: every chunk is empty.
+  // A tile's first cap entries go through the pipeline, the rest (only
+  // repeated nonzeros make a tile hold more) at the end.
+  const uint32_t cap = uint32_t(TS * OP * kThreads);
+  uint32_t pe0 = 0, pe1 = 0;
+  const float* pd = dt[0];
+  const const_u32* tb = (const const_u32*)a.tile_begin;
+  // the share's tiles, one row panel at a time (no conditional load inside a
+  // panel's loop: the wait for one would drain every load and store ahead)
+  for (uint32_t t = t0; t < t1;) {
+    const uint32_t panel_end = (t / tc + 1) * tc < t1 ? (t / tc + 1) * tc : t1;
+    if (kResident) {
+#pragma unroll
+      for (int kb = 0; kb < KB8; ++kb)
+#pragma unroll
+        for (int rb = 0; rb < kSdRb; ++rb) xa[kb][rb] = load4(x_run(t) + (rb * steps + kb) * 256);
     }
-    if (!kResident) {
+  for (; t < panel_end; ++t) {
+    const uint32_t ne0 = tb[t], ne1 = tb[t + 1];
+    const uint32_t clen = (pe1 - pe0 + uint32_t(TS) - 1) / uint32_t(TS);
+    // the tile's steps with OPv output slots per thread and step
+    auto tile_steps = [&](auto op_count) {
+    constexpr int OPv = decltype(op_count)::value;
+    uint64_t oc[kSdOutSets][OPv];
+    float ov[kSdOutSets][OPv];
+    // lanes past the chunk take its last entry (entry 0 when nothing is
+    // pending and no entry precedes: a plan holds at least one tile's room)
+    auto load_chunk = [&](int gs, int set) {
+      const uint32_t cs = pe0 + uint32_t(gs) * clen;
+      const uint32_t ce = cs + clen < pe1 ? cs + clen : pe1;
+      const uint32_t lim = ce > 0 ? ce - 1 : 0;
 #pragma unroll
-      for (int kb = 0; kb < KB8; ++kb) xa[kb] = load4(xrun + (f8 + kb) * 256);
+      for (int j = 0; j < OPv; ++j) {
+        uint32_t e = cs + uint32_t(j * kThreads + tid);
+        e = e < lim ? e : lim;
+        oc[set][j] = __builtin_nontemporal_load(a.entries + e);
+        ov[set][j] = __builtin_nontemporal_load(a.values + e);
+      }
+    };
+    auto store_chunk = [&](int gs, int set) {
+      const uint32_t cs = pe0 + uint32_t(gs) * clen;
+      const uint32_t ce = cs + clen < pe1 ? cs + clen : pe1;
+#pragma unroll
+      for (int j = 0; j < OPv; ++j)
+        emit_pipe(oc[set][j], ov[set][j], pd, cs + uint32_t(j * kThreads + tid) < ce, pe1 > pe0);
+    };
+#pragma unroll
+    for (int j = 0; j < kSdOutAhead; ++j) load_chunk(j, j);
+    for (int unit = 0; unit < units; ++unit) {
+      const int f8 = unit * KB8;  // first step of this unit
+      const bool tile_end = kResident || unit + 1 == units;
+      if (!kResident) {
+        const float* xrun = x_run(t);
+#pragma unroll
+        for (int kb = 0; kb < KB8; ++kb)
+#pragma unroll
+          for (int rb = 0; rb < kSdRb; ++rb) xa[kb][rb] = load4(xrun + (rb * steps + f8 + kb) * 256);
+      }
+      // the runs the loads ahead read: this tile's, or the next tile's
+      const float* ycur[kSdNb];
+      const float* ynext[kSdNb];
+#pragma unroll
+      for (int cb = 0; cb < kSdNb; ++cb) {
+        ycur[cb] = y_run(t, cb);
+        ynext[cb] = tile_end ? y_run(t + 1, cb) : ycur[cb] + (f8 + KB8) * 256;
+      }
+#pragma unroll
+      for (int kb = 0; kb < KB8; ++kb) {
+        float4 xs[kSdRb];
+#pragma unroll
+        for (int rb = 0; rb < kSdRb; ++rb) xs[rb] = xa[kb][rb];
+        float4 ys[kSdNb];
+#pragma unroll
+        for (int cb = 0; cb < kSdNb; ++cb) ys[cb] = yb[kb % kSdRing][cb];
+        mfma_step<kSdRb, kSdNb>(acc, xs, ys);
+        // the Y step loaded now: of this unit, of the next unit of this tile,
+        // or of the next tile's first unit
+        const int ahead = kb + kSdRing - 1;
+#pragma unroll
+        for (int cb = 0; cb < kSdNb; ++cb)
+          yb[ahead % kSdRing][cb] = ahead < KB8 ? load4(ycur[cb] + (f8 + ahead) * 256)
+                                                : load4(ynext[cb] + (ahead - KB8) * 256);
+        // the previous tile's outputs: this step's chunk out, a later one in
+        // (chunks past the tile's last step are not loaded where that is known)
+        const int gs = f8 + kb;
+        store_chunk(gs, kb % kSdOutSets);
+        if (!kResident || kb + kSdOutAhead < KB8)
+          load_chunk(gs + kSdOutAhead, (kb + kSdOutAhead) % kSdOutSets);
+        // interleave the step's other instructions with its MFMAs (one wave
+        // per SIMD: the matrix core idles while the wave issues anything else
+        // in a run of its own), and keep them in this step (the scheduler
+        // would sink the loads towards their use and shorten the prefetch)
+#pragma unroll
+        for (int i = 0; i < 4 * kSdRb * kSdNb; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+          __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);  // VMEM write
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    // the runs the loads ahead read: this tile's, or the next tile's
-    const float* ycur[4];
-    const float* ynext[4];
+    };
+    const uint32_t n = pe1 - pe0;
+    if (n <= uint32_t(TS * OP1 * kThreads)) tile_steps(std::integral_constant<int, OP1>{});
+    else if (n <= uint32_t(TS * OP2 * kThreads)) tile_steps(std::integral_constant<int, OP2>{});
+    else tile_steps(std::integral_constant<int, OP>{});
+    // the tile's D into the buffer the pending tile does not use; after the
+    // barrier every wave has finished the pending tile's outputs and sees D
+    float* dn = pd == dt[0] ? dt[1] : dt[0];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      ycur[cb] = y_run(cq, cb);
-      ynext[cb] = tile_end ? y_run(cq + 1, cb) : ycur[cb] + (f8 + KB8) * 256;
-    }
+    for (int rb = 0; rb < kSdRb; ++rb)
 #pragma unroll
-    for (int kb = 0; kb < KB8; ++kb) {
-      float4 xs[1] = {xa[kb]};
-      float4 ys[4] = {yb[kb % kSdRing][0], yb[kb % kSdRing][1], yb[kb % kSdRing][2],
-                      yb[kb % kSdRing][3]};
-      mfma_step<1, 4>(acc, xs, ys);
-      // the step loaded now: of this unit, of the next unit of this tile, or
-      // of the next tile's first unit
-      const int ahead = kb + kSdRing - 1;
+      for (int cb = 0; cb < kSdNb; ++cb) {
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
-        yb[ahead % kSdRing][cb] = ahead < KB8 ? load4(ycur[cb] + (f8 + ahead) * 256)
-                                              : load4(ynext[cb] + (ahead - KB8) * 256);
-      // keep the loads at this step (the scheduler would sink them towards
-      // their use and shorten the prefetch distance)
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (!tile_end) {
-      ++unit;
-      continue;
-    }
-    // the tile is done: D through LDS, then the planned entries
-    __syncthreads();  // the previous tile's entries are done with dt
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        dt[(wr + 8 * (r / 4) + 4 * g + (r % 4)) * kSdLd + wc + cb * 32 + l32] = acc[0][cb][r];
+        for (int r = 0; r < 16; ++r)
+          dn[(wr + rb * 32 + 8 * (r / 4) + 4 * g + (r % 4)) * kSdLd + wc + cb * 32 + l32] =
+              acc[rb][cb][r];
+        acc[rb][cb] = v16f{};
+      }
     __syncthreads();
-    for (uint32_t base = e0; base < e1; base += kSdBatch * kThreads) {
-      uint64_t code[kSdBatch];
-      float val[kSdBatch];
+    pd = dn;
+    pe0 = ne0;
+    pe1 = ne1 - ne0 < cap ? ne1 : ne0 + cap;
+  }
+  }
+  // the last tile's outputs, kSdBatch per thread in flight
+  for (uint32_t base = pe0; base < pe1; base += kSdBatch * kThreads) {
+    uint64_t code[kSdBatch];
+    float val[kSdBatch];
 #pragma unroll
-      for (int j = 0; j < kSdBatch; ++j) {
-        const uint32_t e = base + uint32_t(j * kThreads) + threadIdx.x;
-        code[j] = e < e1 ? __builtin_nontemporal_load(a.entries + e) : 0;
-        val[j] = e < e1 ? __builtin_nontemporal_load(a.values + e) : 0.f;
-      }
-      int dst[kSdBatch];
-      if (a.out_csr) {
-#pragma unroll
-        for (int j = 0; j < kSdBatch; ++j) {
-          const uint32_t e = base + uint32_t(j * kThreads) + threadIdx.x;
-          const int s = int((code[j] >> kPosBits) & ((1u << kWsBits) - 1u));
-          dst[j] = e < e1 ? s_pos[s][uint32_t(code[j])] : 0;
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < kSdBatch; ++j) {
-        const uint32_t e = base + uint32_t(j * kThreads) + threadIdx.x;
-        if (e >= e1) continue;
-        const uint32_t local = uint32_t(code[j] >> (kPosBits + kWsBits));
-        const float d = val[j] * dt[(local >> 8) * kSdLd + (local & 255u)];
-        if (a.out_csr) {
-          __builtin_nontemporal_store(d, a.out_csr + dst[j]);
-        } else {
-          const int s = int((code[j] >> kPosBits) & ((1u << kWsBits) - 1u));
-          __builtin_nontemporal_store(d, s_out[s] + uint32_t(code[j]));
-        }
-      }
+    for (int j = 0; j < kSdBatch; ++j) {
+      const uint32_t e = base + uint32_t(j * kThreads + tid);
+      code[j] = e < pe1 ? __builtin_nontemporal_load(a.entries + e) : 0;
+      val[j] = e < pe1 ? __builtin_nontemporal_load(a.values + e) : 0.f;
     }
-    if (++cq == cq1) break;
-    unit = 0;
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) acc[0][cb] = v16f{};
+    for (int j = 0; j < kSdBatch; ++j)
+      if (base + uint32_t(j * kThreads + tid) < pe1) emit(code[j], val[j], pd);
+  }
+  // entries past a tile's cap: the dot products taken one entry per thread
+  // from the fragment-order operands
+  for (uint32_t t = t0; t < t1; ++t) {
+    const uint32_t e1 = tb[t + 1];
+    for (uint32_t e = tb[t] + cap + uint32_t(tid); e < e1; e += kThreads) {
+      const uint64_t code = a.entries[e];
+      const uint32_t local = uint32_t(code >> (kPosBits + kWsBits));
+      const size_t i = size_t(t / tc) * kSdRows + local / kSdLd;
+      const size_t h = size_t(t % tc) * kSdCols + local % kSdLd;
+      float dot = 0.f;
+      for (int k = 0; k < a.K; k += 4) {
+        const float4 x = load4(a.Xf + frag_offset(i, size_t(k), size_t(a.K)));
+        const float4 y = load4(a.Yf + frag_offset(h, size_t(k), size_t(a.K)));
+        dot = fmaf(x.x, y.x, dot);
+        dot = fmaf(x.y, y.y, dot);
+        dot = fmaf(x.z, y.z, dot);
+        dot = fmaf(x.w, y.w, dot);
+      }
+      const float r = a.values[e] * dot;
+      const int s = int((code >> kPosBits) & ((1u << kWsBits) - 1u));
+      if (kCsr) a.out_csr[s_pos[s][uint32_t(code)]] = r;
+      else s_out[s][uint32_t(code)] = r;
+    }
+  }
+}
+
+template <bool kCsr>
+void launch_hub_sddmm(const HubSddmmArgs& a, unsigned grid, hipStream_t st) {
+  switch (a.K) {
+    case 32: hub_sddmm_kernel<4, true, kCsr><<<grid, kThreads, 0, st>>>(a); break;
+    case 64: hub_sddmm_kernel<8, true, kCsr><<<grid, kThreads, 0, st>>>(a); break;
+    case 96: hub_sddmm_kernel<12, true, kCsr><<<grid, kThreads, 0, st>>>(a); break;
+    case 128: hub_sddmm_kernel<16, true, kCsr><<<grid, kThreads, 0, st>>>(a); break;
+    default: hub_sddmm_kernel<4, false, kCsr><<<grid, kThreads, 0, st>>>(a); break;
   }
 }
 
@@ -1072,15 +1229,22 @@ int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_work
   a.entries = reinterpret_cast<const uint64_t*>(pb + ps::round256((T + 1) * 4));
   a.values = reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.entries) +
                                             ps::round256(size_t(tile_count) * 64 * 8));
-  // about 1024 workgroups (4 per CU): column ranges per row panel
-  int ranges = (1024 + a.tiles_r - 1) / a.tiles_r;
-  if (ranges > a.tiles_c) ranges = a.tiles_c;
-  a.range = (a.tiles_c + ranges - 1) / ranges;
-  ranges = (a.tiles_c + a.range - 1) / a.range;
-  const uint64_t grid = uint64_t(a.tiles_r) * uint64_t(ranges);
-  PS_CHECK_ARG(grid < (1ull << 31), "ps_hub_sddmm_launch: block too large");
-  // runs of one column range's row panels on one XCD share its Y rows in L2
-  a.chunk_log2 = uint32_t(ps::task_chunk_log2(PS_TASK_CHUNK_AUTO, grid, 32));
+  // as many workgroups as the CUs hold at once (the D buffers in LDS bound
+  // them), each over an even share of the tiles
+  int cus = 0;
+  {
+    int dev = 0;
+    PS_HIP(hipGetDevice(&dev));
+    PS_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  }
+  const uint64_t slots = uint64_t(cus > 0 ? cus : 1) * ps::kSdWgPerCu;
+  const uint64_t grid = T < slots ? T : slots;
+  PS_CHECK_ARG(T < (1ull << 32), "ps_hub_sddmm_launch: block too large");
+  // neighbouring shares (a row panel's X, Y columns of neighbouring tiles) on
+  // one XCD: up to 32 consecutive shares per XCD
+  a.chunk_log2 = 0;
+  while ((2u << a.chunk_log2) <= 32 && (uint64_t(2) << a.chunk_log2) * ps::kXcd <= grid)
+    ++a.chunk_log2;
   hipStream_t st = ps::to_hip(stream);
   // X[hub_rows] and Y[hot_cols] in fragment order
   const int xrows = a.tiles_r * ps::kSdRows, yrows = a.tiles_c * ps::kSdCols;
@@ -1095,13 +1259,8 @@ int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_work
   PS_LAUNCHED();
   a.Xf = xf;
   a.Yf = yf;
-  switch (N) {
-    case 32: ps::hub_sddmm_kernel<4, true><<<unsigned(grid), ps::kThreads, 0, st>>>(a); break;
-    case 64: ps::hub_sddmm_kernel<8, true><<<unsigned(grid), ps::kThreads, 0, st>>>(a); break;
-    case 96: ps::hub_sddmm_kernel<12, true><<<unsigned(grid), ps::kThreads, 0, st>>>(a); break;
-    case 128: ps::hub_sddmm_kernel<16, true><<<unsigned(grid), ps::kThreads, 0, st>>>(a); break;
-    default: ps::hub_sddmm_kernel<4, false><<<unsigned(grid), ps::kThreads, 0, st>>>(a); break;
-  }
+  if (out_csr) ps::launch_hub_sddmm<true>(a, unsigned(grid), st);
+  else ps::launch_hub_sddmm<false>(a, unsigned(grid), st);
   PS_LAUNCHED();
   return PS_OK;
 }

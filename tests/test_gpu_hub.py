@@ -114,6 +114,51 @@ def test_hub_block_exact_on_golden(name, tiers):
     off.close()
 
 
+def test_hub_sddmm_tile_past_the_pipeline_capacity():
+    """SDDMM's dense kernel writes a tile's first 8192 entries (64 x 128, the
+    most a tile holds without repeated nonzeros) while it computes the next
+    tile, and any further entries afterwards from direct dot products. 64 hub
+    rows storing each of 256 hot columns three times (768 nonzeros each) put
+    24576 entries into each of two tiles; on exact inputs (values k/64, operands k/16)
+    the outputs in workset and CSR order equal the block-off build's bit for
+    bit, at widths that run the resident and the streamed kernels."""
+    setup()
+    rng = np.random.default_rng(31)
+    rows, cols, hub, hot = 4096, 8192, 64, 256
+    lists = []
+    for r in range(rows):
+        if r < hub:
+            c = np.repeat(np.arange(hot), 3)
+        else:
+            c = np.sort(rng.choice(np.arange(hot, cols), 8 if r % 2 else 160, replace=False))
+        lists.append(c.astype(np.int32))
+    rp = np.concatenate([[0], np.cumsum([len(c) for c in lists])]).astype(np.int32)
+    ci = np.concatenate(lists)
+    sv = (rng.integers(1, 64, ci.size) / 64).astype(np.float32)
+    csr = ps.HostCsr(rows, cols, rp, ci, sv)
+    kw = dict(cu_count=8, csr_positions=True)
+    on = ps.PowerSparseMatrixGPU.from_csr(csr, hub_thresholds=[(768, 100)], **kw)
+    off = ps.PowerSparseMatrixGPU.from_csr(csr, hub_block="off", **kw)
+    say(f"capacity: hub block {on.hub_block}, S={on.GroupTypeNum()}")
+    assert on.hub_block == [(hub, hot)], "the block was not built"
+
+    class G:
+        pass
+    g = G()
+    g.rows, g.cols, g.nnz = rows, cols, int(ci.size)
+    for N in (32, 128, 160):
+        B, X, Y = (gd.dense(cols, N, gd.SALT_B), gd.dense(rows, N, gd.SALT_X),
+                   gd.dense(cols, N, gd.SALT_Y))
+        a = run_ops(on, g, N, B, X, Y)
+        b = run_ops(off, g, N, B, X, Y)
+        for s in range(on.GroupTypeNum()):
+            np.testing.assert_array_equal(a[1][s], b[1][s], err_msg=f"SDDMM N={N} ws {s}")
+        np.testing.assert_array_equal(a[2], b[2], err_msg=f"SDDMMToCSR N={N}")
+        np.testing.assert_array_equal(a[0], b[0], err_msg=f"SpMM N={N}")
+    on.close()
+    off.close()
+
+
 def tiles_inside(g, p, th):
     """(tiles inside the block, whole groups inside, groups split) of the
     block workset tiles (64 consecutive nonzeros of a group of 64+) for the
@@ -441,8 +486,8 @@ def test_hub_entry_points_through_the_abi():
     plan = ps.DeviceBuffer(plan_bytes)
     _hip_call(hip.ps_hub_sddmm_plan(ctypes.byref(hb), w.S, wa, dt.ptr, listed.size, plan.ptr,
                                     plan_bytes, None))
-    # the plan's tile table: 64 x 256 dense tiles, the listed entries counted once each
-    T = -(-R // 64) * -(-H // 256)
+    # the plan's tile table: 64 x 128 dense tiles, the listed entries counted once each
+    T = -(-R // 64) * -(-H // 128)
     begin = plan.download(np.uint32, T + 1)
     assert begin[0] == 0 and (np.diff(begin.astype(np.int64)) >= 0).all()
     assert begin[T] == 64 * len(tiles), (begin[T], len(tiles))

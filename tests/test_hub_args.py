@@ -47,9 +47,9 @@ def test_workspace_and_stored_words():
     for N, slice_ in ((32, 32), (128, 128), (256, 128)):
         spmm = r256(slice_ * ld * 4) + r256(70 * 4) + 256
         assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SPMM, N) == spmm
-    # SDDMM: X[hub_rows] padded to 64 rows and Y[hot_cols] to 256, N floats each
+    # SDDMM: X[hub_rows] padded to 64 rows and Y[hot_cols] to 128, N floats each
     for N in (32, 128, 512):
-        sddmm = r256(64 * N * 4) + r256(256 * N * 4)
+        sddmm = r256(64 * N * 4) + r256(128 * N * 4)
         assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SDDMM, N) == sddmm
     assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), _native.PS_OP_SPMM, 0) == 0
     assert lib.ps_hub_workspace_bytes(ctypes.byref(hb), 7, 32) == 0
@@ -57,11 +57,11 @@ def test_workspace_and_stored_words():
 
 def test_plan_bytes_follow_the_tile_grid():
     lib = _native.hip()
-    # 130 hub rows -> 3 row panels of 64; 600 hot columns -> 3 column tiles of 256
+    # 130 hub rows -> 3 row panels of 64; 600 hot columns -> 5 column tiles of 128
     hb = block(rows=130, cols=600)
     for tiles in (0, 1, 7):
         n = 64 * tiles
-        want = r256((3 * 3 + 1) * 4) + r256(n * 8) + r256(n * 4)
+        want = r256((3 * 5 + 1) * 4) + r256(n * 8) + r256(n * 4)
         assert lib.ps_hub_sddmm_plan_bytes(ctypes.byref(hb), tiles) == want
     assert lib.ps_hub_sddmm_plan_bytes(None, 4) == 0
 
