@@ -344,97 +344,106 @@ struct HubSpmmArgs {
   const int* hub_rows;
   int R, N, ld;
   int f0;        // first feature of this slice
-  int kc;        // hot columns per chunk (multiple of kDenseAlign)
   int panels;    // row panels of kSpRows rows
-  uint32_t chunk_log2;
 };
 
-// One workgroup: kSpRows hub rows (64 per wave: 2 MFMA row blocks) x the
-// slice's 32 CB features, over one chunk of hot columns; the partial rows are
-// added into C with atomics. A (dense) streams from memory once, through a
-// per-wave ring of RA 8-column steps loaded RA - 1 steps ahead. The 4 waves
-// share the slice's B fragments: wave w < CB loads 32-feature block w of
-// every step (G steps ahead, into registers) and the workgroup passes them
-// through a double-buffered LDS stage, one barrier per step; neighbouring
-// workgroups take a chunk's row panels on one XCD, so B is read from memory
-// about once per chunk. Chunks are whole loop iterations (kc and ld are
-// multiples of kDenseAlign); loads past the chunk's end (never used) read its
-// last step again. Waves whose 64 rows lie past R compute on row block 0 and
-// write nothing (every wave takes part in the barriers).
+// The slice's 32 CB features of the hub rows, split evenly over the grid
+// (one workgroup per slot the CUs hold at once): the row panels' hot columns
+// in loop iterations of 8 U columns, panel-major, each workgroup an equal run
+// of them, taken as segments of at most one panel each. A segment: kSpRows
+// hub rows (64 per wave: 2 MFMA row blocks) over its hot columns; the partial
+// rows are added into C with atomics. A (dense) streams from memory once,
+// through a per-wave ring of RA 8-column steps loaded RA - 1 steps ahead. The
+// 4 waves share the slice's B fragments: wave w < CB loads 32-feature block w
+// of every step (G steps ahead, into registers) and the workgroup passes them
+// through a double-buffered LDS stage, one barrier per step. Loads past the
+// segment's end (never used) read its last step again. Waves whose 64 rows
+// lie past R compute on row block 0 and write nothing (every wave takes part
+// in the barriers).
+// workgroups of hub_spmm_kernel<CB, ...> per CU (its registers admit no more)
+constexpr int spmm_wg_per_cu(int CB) { return CB == 1 ? 3 : 2; }
 template <int CB, int RA>
-__global__ __launch_bounds__(kThreads, 2) void hub_spmm_kernel(HubSpmmArgs a) {
+__global__ __launch_bounds__(kThreads, spmm_wg_per_cu(CB)) void hub_spmm_kernel(HubSpmmArgs a) {
   constexpr int G = 4;                               // B steps in flight per wave
   constexpr int U = RA > G ? RA : G;                 // steps per loop iteration
   static_assert(U % RA == 0 && U % G == 0 && U % 2 == 0, "ring sizes must divide the unroll");
-  static_assert(kDenseAlign % (8 * U) == 0, "chunks must hold whole iterations");
+  static_assert(kDenseAlign % (8 * U) == 0, "a panel's columns must hold whole iterations");
   __shared__ float4 bs[2][CB][kWave];
-  const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, a.chunk_log2);
-  const int panel = int(blk % uint32_t(a.panels)), chunk = int(blk / uint32_t(a.panels));
   const int wave = threadIdx.x / kWave, lane = lane_id(), g = lane >> 5, l32 = lane & 31;
-  const int m0 = panel * kSpRows + wave * 64;
-  const int k0 = chunk * a.kc;
-  const int k1 = k0 + a.kc < a.ld ? k0 + a.kc : a.ld;
-  if (panel * kSpRows >= a.R || k0 >= k1) return;  // uniform over the workgroup
-  const bool active = m0 < a.R;
   const size_t steps = size_t(a.ld / 8);
-  const float* arow[2];
+  const uint32_t ipp = uint32_t(a.ld / (8 * U));  // loop iterations per panel
+  const uint64_t total = uint64_t(a.panels) * ipp;
+  uint32_t it = uint32_t(total * blockIdx.x / gridDim.x);
+  const uint32_t it1 = uint32_t(total * (blockIdx.x + 1) / gridDim.x);
+  while (it < it1) {  // uniform over the workgroup
+    const int panel = int(it / ipp);
+    const uint32_t seg_end = it1 < uint32_t(panel + 1) * ipp ? it1 : uint32_t(panel + 1) * ipp;
+    const int k0 = int(it - uint32_t(panel) * ipp) * 8 * U;
+    const int k1 = int(seg_end - uint32_t(panel) * ipp) * 8 * U;
+    it = seg_end;
+    const int m0 = panel * kSpRows + wave * 64;
+    const bool active = m0 < a.R;
+    const float* arow[2];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-    arow[rb] = a.dense + size_t((active ? m0 / 32 : 0) + rb) * steps * 256 + lane * 4;
-  const bool loader = wave < CB;  // loads B block `wave` of every step
-  const float* bsrc = a.Bt + size_t(loader ? wave : 0) * steps * 256 + lane * 4;
-  const int klast = k1 - 8;
-  auto kclamp = [klast](int k) { return k < klast ? k : klast; };
+    for (int rb = 0; rb < 2; ++rb)
+      arow[rb] = a.dense + size_t((active ? m0 / 32 : 0) + rb) * steps * 256 + lane * 4;
+    const bool loader = wave < CB;  // loads B block `wave` of every step
+    const float* bsrc = a.Bt + size_t(loader ? wave : 0) * steps * 256 + lane * 4;
+    const int klast = k1 - 8;
+    auto kclamp = [klast](int k) { return k < klast ? k : klast; };
 
-  v16f acc[2][CB];
+    v16f acc[2][CB];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = v16f{};
-  float4 A[RA][2], breg[G];
-  // B(0) into LDS slot 0, B(1 .. G) into the register ring (step t in slot t % G)
-  if (loader) {
-    bs[0][wave][lane] = load4(bsrc + size_t(k0) * 32);
+      for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = v16f{};
+    float4 A[RA][2], breg[G];
+    // B(0) into LDS slot 0, B(1 .. G) into the register ring (step t in slot t % G)
+    if (loader) {
+      bs[0][wave][lane] = load4(bsrc + size_t(k0) * 32);
 #pragma unroll
-    for (int j = 1; j <= G; ++j) breg[j % G] = load4(bsrc + size_t(kclamp(k0 + 8 * j)) * 32);
-  }
-#pragma unroll
-  for (int j = 0; j < RA - 1; ++j)
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) A[j][rb] = load4(arow[rb] + size_t(kclamp(k0 + 8 * j)) * 32);
-  __syncthreads();
-  for (int h = k0; h < k1; h += 8 * U) {
-#pragma unroll
-    for (int s = 0; s < U; ++s) {
-      const int k = h + 8 * s;  // this step's first hot column
-      float4 bf[CB];
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) bf[cb] = bs[s % 2][cb][lane];
-      if (loader) {
-        bs[(s + 1) % 2][wave][lane] = breg[(s + 1) % G];  // B(t + 1), read after the barrier
-        breg[(s + 1) % G] = load4(bsrc + size_t(kclamp(k + 8 * (G + 1))) * 32);
-      }
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-        A[(s + RA - 1) % RA][rb] = load4(arow[rb] + size_t(kclamp(k + 8 * (RA - 1))) * 32);
-      float4 as[2] = {A[s % RA][0], A[s % RA][1]};
-      mfma_step<2, CB>(acc, as, bf);
-      __syncthreads();
+      for (int j = 1; j <= G; ++j) breg[j % G] = load4(bsrc + size_t(kclamp(k0 + 8 * j)) * 32);
     }
-  }
-  if (!active) return;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int mb = m0 + rb * 32;
-    const int hr = a.hub_rows[mb + l32 < a.R ? mb + l32 : a.R - 1];
+    for (int j = 0; j < RA - 1; ++j)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int lr = 8 * (r / 4) + 4 * g + (r % 4);
-      const int dst = __shfl(hr, lr);
-      if (mb + lr < a.R) {
-        float* crow = a.C + size_t(dst) * size_t(a.N) + size_t(a.f0 + l32);
+      for (int rb = 0; rb < 2; ++rb) A[j][rb] = load4(arow[rb] + size_t(kclamp(k0 + 8 * j)) * 32);
+    __syncthreads();
+    for (int h = k0; h < k1; h += 8 * U) {
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) unsafeAtomicAdd(crow + cb * 32, acc[rb][cb][r]);
+      for (int s = 0; s < U; ++s) {
+        const int k = h + 8 * s;  // this step's first hot column
+        float4 bf[CB];
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) bf[cb] = bs[s % 2][cb][lane];
+        if (loader) {
+          bs[(s + 1) % 2][wave][lane] = breg[(s + 1) % G];  // B(t + 1), read after the barrier
+          breg[(s + 1) % G] = load4(bsrc + size_t(kclamp(k + 8 * (G + 1))) * 32);
+        }
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+          A[(s + RA - 1) % RA][rb] = load4(arow[rb] + size_t(kclamp(k + 8 * (RA - 1))) * 32);
+        float4 as[2] = {A[s % RA][0], A[s % RA][1]};
+        mfma_step<2, CB>(acc, as, bf);
+        __syncthreads();
+      }
+    }
+    // (the last step's barrier has passed: the next segment may refill bs)
+    if (active) {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const int mb = m0 + rb * 32;
+        const int hr = a.hub_rows[mb + l32 < a.R ? mb + l32 : a.R - 1];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int lr = 8 * (r / 4) + 4 * g + (r % 4);
+          const int dst = __shfl(hr, lr);
+          if (mb + lr < a.R) {
+            float* crow = a.C + size_t(dst) * size_t(a.N) + size_t(a.f0 + l32);
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) unsafeAtomicAdd(crow + cb * 32, acc[rb][cb][r]);
+          }
+        }
       }
     }
   }
@@ -910,17 +919,12 @@ uint32_t sddmm_tiles_c(const ps_hub_block* hb) { return uint32_t((hb->cols + kSd
 // CU; measured on C3 against 512, 1024 and 2048: fewer chunks add fewer
 // partial rows into C), at least 256 columns per chunk, a multiple of
 // kDenseAlign.
-int spmm_chunk(int rows, int ld) {
-  const int panels = (rows + kSpRows - 1) / kSpRows;
-  int chunks = (768 + panels - 1) / panels;
-  if (chunks > ld / 256) chunks = ld / 256;
-  if (chunks < 1) chunks = 1;
-  const int kc = (ld + chunks - 1) / chunks;
-  return (kc + kDenseAlign - 1) & ~(kDenseAlign - 1);
-}
-
 template <int CB>
-void spmm_launch_cb(const HubSpmmArgs& a, unsigned grid, hipStream_t st) {
+void spmm_launch_cb(const HubSpmmArgs& a, int cus, uint64_t iterations, hipStream_t st) {
+  // as many workgroups as the CUs hold at once, each over an even share of
+  // the loop iterations (at least one each)
+  const uint64_t slots = uint64_t(cus > 0 ? cus : 1) * spmm_wg_per_cu(CB);
+  const unsigned grid = unsigned(iterations < slots ? iterations : slots);
   // a deeper A ring for a single feature block (fewer MFMAs per A load)
   hub_spmm_kernel<CB, (CB == 1 ? 8 : 4)><<<grid, kThreads, 0, st>>>(a);
 }
@@ -1074,13 +1078,17 @@ int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, 
   a.R = hb->rows;
   a.N = N;
   a.ld = ld;
-  a.kc = ps::spmm_chunk(hb->rows, ld);
   a.panels = (hb->rows + ps::kSpRows - 1) / ps::kSpRows;
-  const int chunks = (ld + a.kc - 1) / a.kc;
-  const uint64_t grid = uint64_t(a.panels) * uint64_t(chunks);
-  PS_CHECK_ARG(grid < (1ull << 31), "ps_hub_spmm_launch: block too large");
-  // runs of the chunk's row panels on one XCD (up to 64 workgroups)
-  a.chunk_log2 = uint32_t(ps::task_chunk_log2(PS_TASK_CHUNK_AUTO, grid, 64));
+  int cus = 0;
+  {
+    int dev = 0;
+    PS_HIP(hipGetDevice(&dev));
+    PS_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  }
+  // loop iterations of the coarsest kernel (64 hot columns; the others take 32)
+  const uint64_t iterations = uint64_t(a.panels) * uint64_t(ld / 64);
+  PS_CHECK_ARG(uint64_t(a.panels) * uint64_t(ld / 32) < (1ull << 32),
+               "ps_hub_spmm_launch: block too large");
   for (int f0 = 0; f0 < N; f0 += ps::kSpSlice) {
     const int width = N - f0 < ps::kSpSlice ? N - f0 : ps::kSpSlice;
     ps::gather_hot_kernel<<<ps::grid_for(size_t(width / 32) * size_t(ld / 8) * 64, ps::kThreads),
@@ -1089,10 +1097,10 @@ int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, 
     PS_LAUNCHED();
     a.f0 = f0;
     switch (width / 32) {
-      case 1: ps::spmm_launch_cb<1>(a, unsigned(grid), st); break;
-      case 2: ps::spmm_launch_cb<2>(a, unsigned(grid), st); break;
-      case 3: ps::spmm_launch_cb<3>(a, unsigned(grid), st); break;
-      default: ps::spmm_launch_cb<4>(a, unsigned(grid), st); break;
+      case 1: ps::spmm_launch_cb<1>(a, cus, iterations, st); break;
+      case 2: ps::spmm_launch_cb<2>(a, cus, iterations, st); break;
+      case 3: ps::spmm_launch_cb<3>(a, cus, iterations, st); break;
+      default: ps::spmm_launch_cb<4>(a, cus, iterations, st); break;
     }
     PS_LAUNCHED();
   }
