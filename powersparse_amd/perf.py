@@ -188,6 +188,148 @@ def csr_order(args):
         print(f"| {name} | {ms:.3f} |")
 
 
+# ------------------------------------------------ per-class traffic split
+
+def _class_worksets(m, keep=None):
+    """ps_workset array of m's public worksets; with `keep`, every other
+    workset emptied (group_num 0), so that a launch runs that class alone."""
+    from powersparse_amd import _native
+
+    S = m.GroupTypeNum()
+    arr = (_native.Workset * S)()
+    cps, vps, dps, gn = m.WorksetColInd(), m.WorksetSpData(), m.GroupDestination(), m.GroupNum()
+    for s in range(S):
+        g = gn[s] if keep is None or keep == s else 0
+        arr[s] = _native.Workset(cps[s], vps[s], dps[s], g, 0 if s == 0 else 32 << (s - 1), None)
+    return arr
+
+
+def classes(args):
+    """The sparse kernels one workset class at a time: SDDMM N = args.n on the
+    public partition in the locality run order, SpMM N = args.n on the tuned
+    partition (3 worksets, signature order), each first with every class and
+    then with one class kept (the others emptied), `args.reps` launches each,
+    on the matrix without the dense hub block. Prints one manifest line per
+    launch group (JSON) for `classes-summarize`."""
+    import ctypes
+    import json
+
+    import powersparse_amd as ps
+    from powersparse_amd import _native
+
+    ps.set_device(0)
+    src = ps.DeviceBuffer(CALIB_BYTES)
+    dst = ps.DeviceBuffer(CALIB_BYTES)
+    ps.fill_random(src, CALIB_BYTES // 4, 7, 0.0, 1.0)
+    for _ in range(2):
+        copy_f32(dst, src, CALIB_BYTES // 4)
+    ps.synchronize()
+    cfg, n, reps = args.config, args.n, args.reps
+    csr = ps.synth(cfg, seed=1)
+    rows, cols = csr.rows, csr.cols
+    hip = _native.hip()
+
+    def nnz_of(m, s):
+        if s != 0:
+            return int(m.GroupNum()[s]) * (32 << (s - 1))
+        return int(csr.nnz) - sum(int(m.GroupNum()[k]) * (32 << (k - 1))
+                                  for k in range(1, m.GroupTypeNum()))
+
+    def groups(m, op):
+        out = [("all", None, int(csr.nnz))]
+        for s in range(m.GroupTypeNum() - 1, -1, -1):
+            if m.GroupNum()[s]:
+                label = "residue" if s == 0 else f"groups of {32 << (s - 1)}"
+                out.append((label, s, nnz_of(m, s)))
+        return out
+
+    # SDDMM: public partition, locality run order (the product's order)
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, hub_block="off")
+    S = m.GroupTypeNum()
+    X = ps.DeviceBuffer(rows * n * 4)
+    Y = ps.DeviceBuffer(cols * n * 4)
+    fill_operand(X, rows * n, 12, cfg, "sddmm")
+    fill_operand(Y, cols * n, 13, cfg, "sddmm")
+    outs = [ps.DeviceBuffer(max(k, 1) * 4) for k in m.sddmm_output_sizes()]
+    oa = (ctypes.c_void_p * S)(*[o.ptr for o in outs])
+    for label, keep, nnz in groups(m, "sddmm"):
+        arr = _class_worksets(m, keep)
+        count = ctypes.c_uint32()
+        ps._hip_call(hip.ps_task_count(_native.PS_OP_SDDMM, n, S, arr, ctypes.byref(count)))
+        order = ps.DeviceBuffer(max(count.value, 1) * 4)
+        ps._hip_call(hip.ps_task_order_build(_native.PS_OP_SDDMM, n, S, arr, order.ptr,
+                                             count.value, None))
+        for _ in range(reps):
+            ps._hip_call(hip.ps_sddmm_launch_ordered(
+                S, arr, m.ResidueOffset(), rows, cols, n, X.ptr, Y.ptr, oa,
+                _native.PS_TASK_CHUNK_AUTO, order.ptr, count.value, None))
+        ps.synchronize()
+        print(json.dumps({"op": "sddmm", "N": n, "class": label, "nnz": nnz,
+                          "tasks": count.value, "launches": reps}), flush=True)
+    del outs, X, Y
+    m.close()
+    # SpMM: the tuned partition as the product builds it without a hub block
+    m = ps.PowerSparseMatrixGPU.from_csr(csr, hub_block="off", max_group_types=3,
+                                         spmm_partition="parity", run_order=False,
+                                         task_order="signature")
+    S = m.GroupTypeNum()
+    B = ps.DeviceBuffer(cols * n * 4)
+    fill_operand(B, cols * n, 11, cfg, "spmm")
+    C = ps.DeviceBuffer(rows * n * 4)
+    C.zero()
+    for label, keep, nnz in groups(m, "spmm"):
+        arr = _class_worksets(m, keep)
+        count = ctypes.c_uint32()
+        ps._hip_call(hip.ps_task_count(_native.PS_OP_SPMM, n, S, arr, ctypes.byref(count)))
+        for _ in range(reps):
+            ps._hip_call(hip.ps_spmm_launch(S, arr, m.ResidueOffset(), m.ResidueAtomic(), rows,
+                                            cols, n, B.ptr, C.ptr, _native.PS_TASK_CHUNK_AUTO,
+                                            None))
+        ps.synchronize()
+        print(json.dumps({"op": "spmm", "N": n, "class": label, "nnz": nnz,
+                          "tasks": count.value, "launches": reps}), flush=True)
+    m.close()
+    print(f"classes {cfg}: nnz={csr.nnz} done", flush=True)
+
+
+def classes_summarize(args):
+    """Markdown table of the `classes` launches: per class its nonzeros, mean
+    launch time (kernel trace) and calibrated FETCH_SIZE + WRITE_SIZE (bytes
+    per launch and per nonzero); the operator-kernel dispatches are matched to
+    the manifest lines in order."""
+    import json
+
+    manifest = [json.loads(line) for line in open(args.manifest)
+                if line.startswith("{") and '"class"' in line]
+    durs = [d for k, _, d in read_dispatches(args.trace) if kernel_op(k) is not None]
+    fetch = read_counters(args.fetch, "FETCH_SIZE")
+    write = read_counters(args.write, "WRITE_SIZE")
+    fscale, wscale = calibration(fetch), calibration(write)
+    fv = [v for k, _, v in fetch if kernel_op(k) is not None]
+    wv = [v for k, _, v in write if kernel_op(k) is not None]
+    need = sum(e["launches"] for e in manifest)
+    if not (len(durs) == len(fv) == len(wv) == need):
+        raise SystemExit(f"dispatch counts differ: trace {len(durs)}, FETCH {len(fv)}, "
+                         f"WRITE {len(wv)}, manifest {need}")
+    lines = ["| operator | class | nonzeros (M) | tasks | us per launch | fabric MB per launch "
+             "(FETCH + WRITE) | bytes per nonzero | share of the all-class bytes |",
+             "|---|---|---|---|---|---|---|---|"]
+    i, total = 0, {}
+    for e in manifest:
+        k = e["launches"]
+        us = sum(durs[i:i + k]) / k
+        mb = (sum(fv[i:i + k]) * 1024 * fscale + sum(wv[i:i + k]) * 1024 * wscale) / k / 1e6
+        i += k
+        key = (e["op"], e["N"])
+        if e["class"] == "all":
+            total[key] = mb
+        share = f"{100 * mb / total[key]:.1f}%" if key in total and e["class"] != "all" else ""
+        lines.append(f"| {e['op']} N={e['N']} | {e['class']} | {e['nnz'] / 1e6:.1f} | "
+                     f"{e['tasks']} | {us:.1f} | {mb:.1f} | {mb * 1e6 / max(e['nnz'], 1):.1f} | "
+                     f"{share} |")
+    print("\n".join(lines))
+
+
 # The dense hub block's kernels of an operator call (they follow the sparse
 # launch on its stream).
 HUB_KERNEL = re.compile(r"(?:^|::)(hub_spmm_kernel|hub_sddmm_kernel|gather_hot_kernel|"
@@ -391,6 +533,15 @@ def main(argv=None):
     c = sub.add_parser("csr")
     c.add_argument("--config", default="C1", choices=sorted(CONFIG_OPS))
     c.add_argument("--n", type=int, default=128)
+    k = sub.add_parser("classes")
+    k.add_argument("--config", default="C3", choices=sorted(CONFIG_OPS))
+    k.add_argument("--n", type=int, default=128)
+    k.add_argument("--reps", type=int, default=3)
+    ks = sub.add_parser("classes-summarize")
+    ks.add_argument("--manifest", required=True)
+    ks.add_argument("--trace", required=True)
+    ks.add_argument("--fetch", required=True)
+    ks.add_argument("--write", required=True)
     s = sub.add_parser("summarize")
     s.add_argument("--trace", required=True)
     s.add_argument("--fetch")
@@ -404,6 +555,10 @@ def main(argv=None):
         workload(args)
     elif args.cmd == "csr":
         csr_order(args)
+    elif args.cmd == "classes":
+        classes(args)
+    elif args.cmd == "classes-summarize":
+        classes_summarize(args)
     else:
         summarize(args)
     return 0

@@ -170,3 +170,45 @@ def test_operator_calls_take_the_hub_kernels_that_follow():
     got = perf.operator_calls(seq, [("spmm", 32), ("spmm", 128), ("sddmm", 128)])
     assert got == {"spmm_N32": (3, 3, 1500.0), "spmm_N128": (3, 2, 5440.0),
                    "sddmm_N128": (3, 3, 6270.0)}
+
+
+def test_class_split_summary(tmp_path, capsys):
+    """`classes-summarize`: operator dispatches matched to the manifest in
+    order (2 launches per class), durations averaged, FETCH / WRITE scaled by
+    the calibration copy, bytes per nonzero and the share of the all-class
+    launch; a dispatch count that disagrees with the manifest is refused."""
+    manifest = tmp_path / "m.txt"
+    entries = [{"op": "sddmm", "N": 128, "class": "all", "nnz": 1000, "tasks": 10, "launches": 2},
+               {"op": "sddmm", "N": 128, "class": "residue", "nnz": 250, "tasks": 4,
+                "launches": 2}]
+    manifest.write_text("noise\n" + "\n".join(json.dumps(e) for e in entries) + "\ndone\n")
+    trace = tmp_path / "kt.db"
+    con = sqlite3.connect(trace)
+    con.execute("create table kernels (name text, grid_x integer, grid_y integer, "
+                "grid_z integer, duration real, start integer)")
+    rows = [(COPY, 1 << 20, 1e6), (SDDMM128, 3000, 100e3), (SDDMM128, 3000, 300e3),
+            (PRE, 64, 5e3), (SDDMM128, 1000, 40e3), (SDDMM128, 1000, 60e3)]
+    con.executemany("insert into kernels values (?, ?, 1, 1, ?, ?)",
+                    [(k, g, d, i) for i, (k, g, d) in enumerate(rows)])
+    con.commit()
+    con.close()
+    # FETCH reads the 1 GiB copy as 2 GiB (factor 0.5), WRITE as 1 GiB
+    fetch = counter_db(tmp_path / "f.db", "FETCH_SIZE",
+                       [(COPY, 1 << 20, 2 * (1 << 30) / KIB), (SDDMM128, 3000, 2e6 / KIB),
+                        (SDDMM128, 3000, 2e6 / KIB), (SDDMM128, 1000, 1e6 / KIB),
+                        (SDDMM128, 1000, 1e6 / KIB)])
+    write = counter_db(tmp_path / "w.db", "WRITE_SIZE",
+                       [(COPY, 1 << 20, (1 << 30) / KIB), (SDDMM128, 3000, 1e6 / KIB),
+                        (SDDMM128, 3000, 1e6 / KIB), (SDDMM128, 1000, 0.0),
+                        (SDDMM128, 1000, 0.0)])
+    args = ["classes-summarize", "--manifest", str(manifest), "--trace", str(trace),
+            "--fetch", fetch, "--write", write]
+    assert perf.main(args) == 0
+    out = capsys.readouterr().out.splitlines()
+    # all: 200 us, 1 + 1 = 2 MB, 2000 B per nonzero; residue: 50 us, 0.5 MB, 25 %
+    assert out[2] == "| sddmm N=128 | all | 0.0 | 10 | 200.0 | 2.0 | 2000.0 |  |"
+    assert out[3] == "| sddmm N=128 | residue | 0.0 | 4 | 50.0 | 0.5 | 2000.0 | 25.0% |"
+    entries[1]["launches"] = 3
+    manifest.write_text("\n".join(json.dumps(e) for e in entries) + "\n")
+    with pytest.raises(SystemExit, match="dispatch counts differ"):
+        perf.main(args)
