@@ -12,9 +12,9 @@
 //          fragment order). A pre-pass gathers B's hot rows into the B
 //          operand's fragment order (one feature slice of up to 128 at a
 //          time) with non-finite elements replaced by 0; the MFMA kernel
-//          splits the hot columns into chunks, and each workgroup adds its
-//          partial rows into C with float atomics (whole 128-byte row
-//          stretches per instruction). A fix-up adds a * b for every stored
+//          splits the row panels' hot columns evenly over its workgroups,
+//          and each adds its partial rows into C with float atomics (whole
+//          128-byte row stretches per instruction). A fix-up adds a * b for every stored
 //          block entry whose b is not finite, so Inf and NaN reach exactly
 //          the rows that store that column, as in the reference's
 //          per-nonzero products.
@@ -24,8 +24,8 @@
 //          fall in. Pre-passes gather X[hub_rows] and Y[hot_cols] into
 //          fragment order; the MFMA kernel computes each dense tile of
 //          D = X[hub_rows] * Y[hot_cols]^T in registers, stages it in LDS and
-//          writes sp_data[p] * D[i][h] to every planned output of the tile:
-//          D never reaches memory.
+//          writes sp_data[p] * D[i][h] to every planned output of the tile
+//          while it computes the next tile: D never reaches memory.
 //
 // MFMA operand layout: for v_mfma_f32_32x32x2f32, lane l supplies A[l % 32][k]
 // and B[k][l % 32] for k = l / 32; the 32 x 32 result leaves D[8 j + 4 (l / 32)
@@ -915,10 +915,9 @@ int worksets_of(int workset_count, const ps_workset* worksets, Worksets* a) {
 uint32_t sddmm_tiles_r(const ps_hub_block* hb) { return uint32_t((hb->rows + kSdRows - 1) / kSdRows); }
 uint32_t sddmm_tiles_c(const ps_hub_block* hb) { return uint32_t((hb->cols + kSdCols - 1) / kSdCols); }
 
-// Hot columns per SpMM chunk: about 768 workgroups per feature slice (3 per
-// CU; measured on C3 against 512, 1024 and 2048: fewer chunks add fewer
-// partial rows into C), at least 256 columns per chunk, a multiple of
-// kDenseAlign.
+// One SpMM feature slice of 32 CB features: the grid holds as many
+// workgroups as the CUs run at once (more rounds of shorter shares add more
+// partial rows into C and measured slower on C3).
 template <int CB>
 void spmm_launch_cb(const HubSpmmArgs& a, int cus, uint64_t iterations, hipStream_t st) {
   // as many workgroups as the CUs hold at once, each over an even share of
