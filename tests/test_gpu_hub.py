@@ -146,7 +146,7 @@ def test_hub_sddmm_tile_past_the_pipeline_capacity():
         pass
     g = G()
     g.rows, g.cols, g.nnz = rows, cols, int(ci.size)
-    for N in (32, 64, 96, 128, 160):
+    for N in (32, 64, 96, 128, 160, 512):
         B, X, Y = (gd.dense(cols, N, gd.SALT_B), gd.dense(rows, N, gd.SALT_X),
                    gd.dense(cols, N, gd.SALT_Y))
         a = run_ops(on, g, N, B, X, Y)
