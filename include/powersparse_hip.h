@@ -361,7 +361,8 @@ int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, 
  * block, are left out of the plan. The plan (ps_hub_sddmm_plan_bytes bytes of
  * device memory) groups the listed nonzeros by the dense tile (64 hub rows x
  * 128 hot columns) they fall in, each with its output position and sp_data;
- * ps_hub_sddmm_plan allocates temporaries and synchronises the stream. */
+ * tile_count * 64 must stay below 2^31. ps_hub_sddmm_plan allocates
+ * temporaries and synchronises the stream. */
 size_t ps_hub_sddmm_plan_bytes(const ps_hub_block* hb, uint32_t tile_count);
 int ps_hub_sddmm_plan(const ps_hub_block* hb, int workset_count, const ps_workset* worksets,
                       const uint32_t* tiles, uint32_t tile_count, void* plan, size_t plan_bytes,

@@ -855,8 +855,9 @@ __global__ __launch_bounds__(kThreads, kSdWgPerCu) void hub_sddmm_kernel(HubSddm
   // entries past a tile's cap: the dot products taken one entry per thread
   // from the fragment-order operands
   for (uint32_t t = t0; t < t1; ++t) {
-    const uint32_t e1 = tb[t + 1];
-    for (uint32_t e = tb[t] + cap + uint32_t(tid); e < e1; e += kThreads) {
+    const uint32_t e0 = tb[t], count = tb[t + 1] - e0;
+    for (uint32_t k = cap + uint32_t(tid); k < count; k += kThreads) {
+      const uint32_t e = e0 + k;
       const uint64_t code = a.entries[e];
       const uint32_t local = uint32_t(code >> (kPosBits + kWsBits));
       const size_t i = size_t(t / tc) * kSdRows + local / kSdLd;
@@ -1127,7 +1128,8 @@ int ps_hub_sddmm_plan(const ps_hub_block* hb, int workset_count, const ps_workse
   PS_CHECK_ARG(tile_count == 0 || tiles, "hub block: missing tile list");
   PS_CHECK_ARG(plan && plan_bytes >= ps_hub_sddmm_plan_bytes(hb, tile_count),
                "ps_hub_sddmm_plan: plan buffer too small");
-  PS_CHECK_ARG(uint64_t(tile_count) * 64 < (1ull << 32), "ps_hub_sddmm_plan: too many tiles");
+  // (entry indices, and the kernel's chunk and tail offsets past them, stay in 32 bits)
+  PS_CHECK_ARG(uint64_t(tile_count) * 64 < (1ull << 31), "ps_hub_sddmm_plan: too many tiles");
   const uint32_t tiles_c = ps::sddmm_tiles_c(hb);
   const uint64_t T64 = uint64_t(ps::sddmm_tiles_r(hb)) * tiles_c;
   PS_CHECK_ARG(T64 < (1ull << 31), "ps_hub_sddmm_plan: too many dense tiles");
@@ -1215,6 +1217,7 @@ int ps_hub_sddmm_launch(const ps_hub_block* hb, int workset_count, const ps_work
   PS_CHECK_ARG(int64_t(hb->matrix_rows) * N <= INT32_MAX && int64_t(hb->matrix_cols) * N <= INT32_MAX,
                "Dense dimensions exceed the 32-bit kernel indexing range");
   if (tile_count == 0) return PS_OK;
+  PS_CHECK_ARG(uint64_t(tile_count) * 64 < (1ull << 31), "ps_hub_sddmm_launch: too many tiles");
   PS_CHECK_ARG(workspace && ps::aligned16(workspace) &&
                    workspace_bytes >= ps_hub_workspace_bytes(hb, PS_OP_SDDMM, N),
                "ps_hub_sddmm_launch: workspace too small");

@@ -126,5 +126,11 @@ def test_sddmm_plan_rejects():
     assert rc == _native.PS_ERR_INVALID and "invalid worksets" in last_error()
     rc = lib.ps_hub_sddmm_plan(None, 2, w, FAKE, 1, FAKE, need, None)
     assert rc == _native.PS_ERR_INVALID and "null descriptor" in last_error()
+    # 2^25 tiles of 64 entries reach 2^31: refused by the plan and the launch
+    big = 1 << 25
+    rc = lib.ps_hub_sddmm_plan(ctypes.byref(hb), 2, w, FAKE, big, FAKE, 1 << 40, None)
+    assert rc == _native.PS_ERR_INVALID and "too many tiles" in last_error()
+    assert sddmm(hb, count=big) == _native.PS_ERR_INVALID and "too many tiles" in last_error()
+    assert lib.ps_hub_sddmm_plan_bytes(ctypes.byref(hb), big - 1) > 0
     # an empty list needs no plan work on the device beyond its empty tile table
     assert sddmm(hb, plan=None, count=0) == _native.PS_OK
