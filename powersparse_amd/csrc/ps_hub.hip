@@ -856,16 +856,16 @@ __global__ __launch_bounds__(kThreads, kSdWgPerCu) void hub_sddmm_kernel(HubSddm
   // from the fragment-order operands
   for (uint32_t t = t0; t < t1; ++t) {
     const uint32_t e0 = tb[t], count = tb[t + 1] - e0;
-    for (uint32_t k = cap + uint32_t(tid); k < count; k += kThreads) {
-      const uint32_t e = e0 + k;
+    for (uint32_t j = cap + uint32_t(tid); j < count; j += kThreads) {
+      const uint32_t e = e0 + j;
       const uint64_t code = a.entries[e];
       const uint32_t local = uint32_t(code >> (kPosBits + kWsBits));
-      const size_t i = size_t(t / tc) * kSdRows + local / kSdLd;
-      const size_t h = size_t(t % tc) * kSdCols + local % kSdLd;
+      const size_t hr = size_t(t / tc) * kSdRows + local / kSdLd;  // block row
+      const size_t hc = size_t(t % tc) * kSdCols + local % kSdLd;  // block column
       float dot = 0.f;
-      for (int k = 0; k < a.K; k += 4) {
-        const float4 x = load4(a.Xf + frag_offset(i, size_t(k), size_t(a.K)));
-        const float4 y = load4(a.Yf + frag_offset(h, size_t(k), size_t(a.K)));
+      for (int f = 0; f < a.K; f += 4) {
+        const float4 x = load4(a.Xf + frag_offset(hr, size_t(f), size_t(a.K)));
+        const float4 y = load4(a.Yf + frag_offset(hc, size_t(f), size_t(a.K)));
         dot = fmaf(x.x, y.x, dot);
         dot = fmaf(x.y, y.y, dot);
         dot = fmaf(x.z, y.z, dot);
