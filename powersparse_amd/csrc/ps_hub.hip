@@ -12,9 +12,10 @@
 //          fragment order). A pre-pass gathers B's hot rows into the B
 //          operand's fragment order (one feature slice of up to 128 at a
 //          time) with non-finite elements replaced by 0; the MFMA kernel
-//          splits the row panels' hot columns evenly over its workgroups,
-//          and each adds its partial rows into C with float atomics (whole
-//          128-byte row stretches per instruction). A fix-up adds a * b for every stored
+//          splits the row panels' hot columns evenly over its workgroups
+//          (up to 64 features each), sums each 32- or 64-column iteration
+//          apart before adding it to running sums, and adds those into C
+//          with float atomics (whole 128-byte row stretches per instruction). A fix-up adds a * b for every stored
 //          block entry whose b is not finite, so Inf and NaN reach exactly
 //          the rows that store that column, as in the reference's
 //          per-nonzero products.
@@ -345,23 +346,31 @@ struct HubSpmmArgs {
   int R, N, ld;
   int f0;        // first feature of this slice
   int panels;    // row panels of kSpRows rows
+  int fgroups;   // feature groups of 32 CB features in the slice
 };
 
-// The slice's 32 CB features of the hub rows, split evenly over the grid
-// (one workgroup per slot the CUs hold at once): the row panels' hot columns
+// One feature group (32 CB of the slice's features) of the hub rows per
+// workgroup, each group's work split evenly over its workgroups (the grid is
+// one workgroup per slot the CUs hold at once): the row panels' hot columns
 // in loop iterations of 8 U columns, panel-major, each workgroup an equal run
 // of them, taken as segments of at most one panel each. A segment: kSpRows
-// hub rows (64 per wave: 2 MFMA row blocks) over its hot columns; the partial
-// rows are added into C with atomics. A (dense) streams from memory once,
+// hub rows (64 per wave: 2 MFMA row blocks) over its hot columns. Each loop
+// iteration's products are summed in fresh accumulators and then added to
+// running sums, so an output's FP32 sum is a chain of 4 U MFMA accumulations
+// per iteration plus one addition per iteration (not one chain over the whole
+// segment); the running sums are added into C with atomics. The feature
+// groups' workgroups for one share run one after another on one XCD, so A
+// comes from its L2 for all but the first. A (dense) streams from memory
 // through a per-wave ring of RA 8-column steps loaded RA - 1 steps ahead. The
-// 4 waves share the slice's B fragments: wave w < CB loads 32-feature block w
-// of every step (G steps ahead, into registers) and the workgroup passes them
-// through a double-buffered LDS stage, one barrier per step. Loads past the
+// 4 waves share the group's B fragments: wave w < CB loads the group's
+// 32-feature block w of every step (G steps ahead, into registers) and the
+// workgroup passes them through a double-buffered LDS stage, one barrier per
+// step. Loads past the
 // segment's end (never used) read its last step again. Waves whose 64 rows
 // lie past R compute on row block 0 and write nothing (every wave takes part
 // in the barriers).
-// workgroups of hub_spmm_kernel<CB, ...> per CU (its registers admit no more)
-constexpr int spmm_wg_per_cu(int CB) { return CB == 1 ? 3 : 2; }
+// workgroups of hub_spmm_kernel per CU (its registers admit no more)
+constexpr int spmm_wg_per_cu(int) { return 2; }
 template <int CB, int RA>
 __global__ __launch_bounds__(kThreads, spmm_wg_per_cu(CB)) void hub_spmm_kernel(HubSpmmArgs a) {
   constexpr int G = 4;                               // B steps in flight per wave
@@ -371,10 +380,23 @@ __global__ __launch_bounds__(kThreads, spmm_wg_per_cu(CB)) void hub_spmm_kernel(
   __shared__ float4 bs[2][CB][kWave];
   const int wave = threadIdx.x / kWave, lane = lane_id(), g = lane >> 5, l32 = lane & 31;
   const size_t steps = size_t(a.ld / 8);
+  // the workgroup's feature group fg and its place wi among that group's wn
+  // workgroups; with the grid a multiple of kXcd * fgroups, the groups'
+  // workgroups for one share run on one XCD one after another (A shared in L2)
+  const uint32_t fgs = uint32_t(a.fgroups), wn = gridDim.x / fgs;
+  uint32_t fg, wi;
+  if (gridDim.x % (kXcd * fgs) == 0) {
+    const uint32_t r = blockIdx.x / kXcd;
+    fg = r % fgs;
+    wi = (r / fgs) * kXcd + blockIdx.x % kXcd;
+  } else {
+    fg = blockIdx.x % fgs;
+    wi = blockIdx.x / fgs;
+  }
   const uint32_t ipp = uint32_t(a.ld / (8 * U));  // loop iterations per panel
   const uint64_t total = uint64_t(a.panels) * ipp;
-  uint32_t it = uint32_t(total * blockIdx.x / gridDim.x);
-  const uint32_t it1 = uint32_t(total * (blockIdx.x + 1) / gridDim.x);
+  uint32_t it = uint32_t(total * wi / wn);
+  const uint32_t it1 = uint32_t(total * (wi + 1) / wn);
   while (it < it1) {  // uniform over the workgroup
     const int panel = int(it / ipp);
     const uint32_t seg_end = it1 < uint32_t(panel + 1) * ipp ? it1 : uint32_t(panel + 1) * ipp;
@@ -388,15 +410,18 @@ __global__ __launch_bounds__(kThreads, spmm_wg_per_cu(CB)) void hub_spmm_kernel(
     for (int rb = 0; rb < 2; ++rb)
       arow[rb] = a.dense + size_t((active ? m0 / 32 : 0) + rb) * steps * 256 + lane * 4;
     const bool loader = wave < CB;  // loads B block `wave` of every step
-    const float* bsrc = a.Bt + size_t(loader ? wave : 0) * steps * 256 + lane * 4;
+    const float* bsrc = a.Bt + size_t(fg * CB + (loader ? wave : 0)) * steps * 256 + lane * 4;
     const int klast = k1 - 8;
     auto kclamp = [klast](int k) { return k < klast ? k : klast; };
 
-    v16f acc[2][CB];
+    v16f acc[2][CB], sum[2][CB];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = v16f{};
+      for (int cb = 0; cb < CB; ++cb) {
+        acc[rb][cb] = v16f{};
+        sum[rb][cb] = v16f{};
+      }
     float4 A[RA][2], breg[G];
     // B(0) into LDS slot 0, B(1 .. G) into the register ring (step t in slot t % G)
     if (loader) {
@@ -427,6 +452,14 @@ __global__ __launch_bounds__(kThreads, spmm_wg_per_cu(CB)) void hub_spmm_kernel(
         mfma_step<2, CB>(acc, as, bf);
         __syncthreads();
       }
+      // the iteration's partial sums into the running sums
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          sum[rb][cb] += acc[rb][cb];
+          acc[rb][cb] = v16f{};
+        }
     }
     // (the last step's barrier has passed: the next segment may refill bs)
     if (active) {
@@ -439,9 +472,9 @@ __global__ __launch_bounds__(kThreads, spmm_wg_per_cu(CB)) void hub_spmm_kernel(
           const int lr = 8 * (r / 4) + 4 * g + (r % 4);
           const int dst = __shfl(hr, lr);
           if (mb + lr < a.R) {
-            float* crow = a.C + size_t(dst) * size_t(a.N) + size_t(a.f0 + l32);
+            float* crow = a.C + size_t(dst) * size_t(a.N) + size_t(a.f0 + fg * CB * 32 + l32);
 #pragma unroll
-            for (int cb = 0; cb < CB; ++cb) unsafeAtomicAdd(crow + cb * 32, acc[rb][cb][r]);
+            for (int cb = 0; cb < CB; ++cb) unsafeAtomicAdd(crow + cb * 32, sum[rb][cb][r]);
           }
         }
       }
@@ -916,15 +949,17 @@ int worksets_of(int workset_count, const ps_workset* worksets, Worksets* a) {
 uint32_t sddmm_tiles_r(const ps_hub_block* hb) { return uint32_t((hb->rows + kSdRows - 1) / kSdRows); }
 uint32_t sddmm_tiles_c(const ps_hub_block* hb) { return uint32_t((hb->cols + kSdCols - 1) / kSdCols); }
 
-// One SpMM feature slice of 32 CB features: the grid holds as many
-// workgroups as the CUs run at once (more rounds of shorter shares add more
-// partial rows into C and measured slower on C3).
+// One SpMM feature slice in a.fgroups groups of 32 CB features: the grid
+// holds as many workgroups as the CUs run at once (more rounds of shorter
+// shares add more partial rows into C and measured slower on C3).
 template <int CB>
 void spmm_launch_cb(const HubSpmmArgs& a, int cus, uint64_t iterations, hipStream_t st) {
-  // as many workgroups as the CUs hold at once, each over an even share of
-  // the loop iterations (at least one each)
-  const uint64_t slots = uint64_t(cus > 0 ? cus : 1) * spmm_wg_per_cu(CB);
-  const unsigned grid = unsigned(iterations < slots ? iterations : slots);
+  // as many workgroups as the CUs hold at once, a multiple of the feature
+  // groups, each group's over an even share of the loop iterations (at least
+  // one each)
+  const uint64_t fgs = uint64_t(a.fgroups);
+  const uint64_t slots = uint64_t(cus > 0 ? cus : 1) * spmm_wg_per_cu(CB) / fgs;
+  const unsigned grid = unsigned((iterations < slots ? iterations : slots) * fgs);
   // a deeper A ring for a single feature block (fewer MFMAs per A load)
   hub_spmm_kernel<CB, (CB == 1 ? 8 : 4)><<<grid, kThreads, 0, st>>>(a);
 }
@@ -1097,10 +1132,12 @@ int ps_hub_spmm_launch(const ps_hub_block* hb, int N, const float* B, float* C, 
     PS_LAUNCHED();
     a.f0 = f0;
     switch (width / 32) {
-      case 1: ps::spmm_launch_cb<1>(a, cus, iterations, st); break;
-      case 2: ps::spmm_launch_cb<2>(a, cus, iterations, st); break;
-      case 3: ps::spmm_launch_cb<3>(a, cus, iterations, st); break;
-      default: ps::spmm_launch_cb<4>(a, cus, iterations, st); break;
+      // 64 features per workgroup at most (its partial and running sums
+      // both in registers): 128 features as two groups, 96 as three of 32
+      case 1: a.fgroups = 1; ps::spmm_launch_cb<1>(a, cus, iterations, st); break;
+      case 2: a.fgroups = 1; ps::spmm_launch_cb<2>(a, cus, iterations, st); break;
+      case 3: a.fgroups = 3; ps::spmm_launch_cb<1>(a, cus, iterations, st); break;
+      default: a.fgroups = 2; ps::spmm_launch_cb<2>(a, cus, iterations, st); break;
     }
     PS_LAUNCHED();
   }
