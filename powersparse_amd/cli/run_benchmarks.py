@@ -20,6 +20,10 @@ Contract of the reference's scripts/run_benchmarks.sh:1-64, kept:
 Differences, following this build's binaries: N = 64 is accepted besides 32
 and 128; the default selection also takes *.pscsr binary CSRs; a manifest
 entry `synth:NAME[:SEED[:SCALE]]` names a generated graph and is passed through.
+With PS_BENCH_LAUNCHER=python every run goes through the same harness from a
+Python process instead (`python -m powersparse_amd.cli OP ...`, the package
+being BUILD_DIR, which must hold lib/libpowersparse_bench.so), with the same
+arguments, output and exit codes.
 """
 import os
 import re
@@ -99,10 +103,29 @@ def select_inputs(root, manifest):
     return inputs
 
 
-def run(cfg, manifest):
-    binary = os.path.join(cfg["build_dir"], "bin", f"powersparse_{cfg['op']}")
+def launcher(cfg, kind):
+    """(command prefix, environment) that runs one benchmark call."""
+    op = cfg["op"]
+    if kind == "python":
+        package = os.path.abspath(cfg["build_dir"])
+        lib = os.path.join(package, "lib", "libpowersparse_bench.so")
+        if not os.path.isfile(lib):
+            raise Stop(1, f"Missing library: {lib}")
+        env = dict(os.environ)
+        parent = os.path.dirname(package)
+        env["PYTHONPATH"] = os.pathsep.join(
+            p for p in (parent, env.get("PYTHONPATH", "")) if p)
+        return [sys.executable, "-m", f"{os.path.basename(package)}.cli", op], env
+    if kind not in ("", "binary"):
+        raise Stop(2, f"Unknown PS_BENCH_LAUNCHER: {kind} (use binary or python)")
+    binary = os.path.join(cfg["build_dir"], "bin", f"powersparse_{op}")
     if not (os.path.isfile(binary) and os.access(binary, os.X_OK)):
         raise Stop(1, f"Missing executable: {binary}")
+    return [binary], None
+
+
+def run(cfg, manifest, kind=""):
+    command, env = launcher(cfg, kind)
     inputs = select_inputs(cfg["root"], manifest)
     output = cfg["output"]
     partial = output + ".partial"
@@ -118,14 +141,14 @@ def run(cfg, manifest):
         raise Stop(1, f"Output already exists: {output} (or .partial)") from None
     with os.fdopen(fd, "w") as fh:
         fh.flush()
-        status = subprocess.call([binary, "--header"], stdout=fh)
+        status = subprocess.call(command + ["--header"], stdout=fh, env=env)
         if status != 0:
             raise Stop(status)
         for path in inputs:
             for n in cfg["widths"]:
                 fh.flush()
-                status = subprocess.call([binary, path, str(n), cfg["device"], cfg["check"],
-                                          cfg["repeats"]], stdout=fh)
+                status = subprocess.call(command + [path, str(n), cfg["device"], cfg["check"],
+                                                    cfg["repeats"]], stdout=fh, env=env)
                 if status != 0:
                     raise Stop(status)
     os.replace(partial, output)
@@ -135,7 +158,8 @@ def run(cfg, manifest):
 def main(argv=None):
     argv = sys.argv[1:] if argv is None else argv
     try:
-        run(parse(argv), os.environ.get("DATASET_LIST", ""))
+        run(parse(argv), os.environ.get("DATASET_LIST", ""),
+            os.environ.get("PS_BENCH_LAUNCHER", ""))
     except Stop as stop:
         if stop.message:
             print(stop.message, file=sys.stderr)

@@ -51,3 +51,28 @@ def test_unselected_width(op, name):
 def test_argument_errors(args, message):
     r = run("spmm", *args)
     assert r.returncode == 1 and r.stderr.strip() == message
+
+
+def run_python(*args):
+    """The same harness through the Python launcher (python -m powersparse_amd.cli)."""
+    if not os.path.exists(os.path.join(ROOT, "powersparse_amd", "lib", "libpowersparse_bench.so")):
+        pytest.skip("harness library not built")
+    return subprocess.run(["python", "-m", "powersparse_amd.cli"] + [str(a) for a in args],
+                          capture_output=True, text=True, timeout=120, cwd=ROOT)
+
+
+@pytest.mark.parametrize("op,name", [("spmm", "SpMM"), ("sddmm", "SDDMM")])
+def test_python_launcher_contract(op, name):
+    r = run_python(op, "--header")
+    assert r.returncode == 0 and r.stdout.strip() == HEADER
+    r = run_python(op)
+    assert r.returncode == 2 and r.stderr.startswith("Usage: powersparse_")
+    r = run_python(op, "synth:C0", 48, 0, 0, 1)
+    assert r.returncode == 2
+    assert r.stderr.strip() == (f"{name} benchmark: N=48 was not selected in main; "
+                                "please use N=32, 64 or 128.")
+    r = run_python(op, "synth:C0", 32, 0, 2, 1)
+    assert r.returncode == 1 and r.stderr.strip() == (
+        "Error: DEVICE must be nonnegative, CHECK 0 or 1, and REPEATS positive")
+    r = run_python("gemm")
+    assert r.returncode == 2 and "python -m powersparse_amd.cli {spmm|sddmm}" in r.stderr

@@ -9,6 +9,8 @@ import csv
 import ctypes
 import io
 import os
+import subprocess
+import sys
 import tempfile
 
 import pytest
@@ -118,3 +120,52 @@ def test_harness_on_the_runner_matrices(tmp_path):
     assert all(r["check"] == "passed" and r["operator"] == "SDDMM" for r in rows)
     rc, out, _ = harness("spmm", tmp_path / "small.mtx", 32, 0, 1, 2)
     assert rc == 0 and row_of(out)["check"] == "passed" and int(row_of(out)["rows"]) == 6
+
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def child(args, env=None):
+    """A child process's (exit code, stdout, stderr), its stderr logged in full."""
+    say("$", " ".join(str(a) for a in args))
+    r = subprocess.run([str(a) for a in args], capture_output=True, text=True, timeout=240,
+                       cwd=ROOT, env=env)
+    say(f"exit status {r.returncode}")
+    say(r.stderr.strip())
+    return r.returncode, r.stdout, r.stderr
+
+
+@pytest.mark.parametrize("op,N", [("spmm", 32), ("sddmm", 128)])
+def test_python_launcher_synth_check(op, N):
+    """The harness from its own Python process (python -m powersparse_amd.cli):
+    the CSV row, the check path and exit code 0 through the process's exit."""
+    rc, out, err = child([sys.executable, "-m", "powersparse_amd.cli", op, "synth:C0:5", N, 0,
+                          1, 3])
+    assert rc == 0
+    row = row_of(out)
+    assert row["check"] == "passed" and int(row["N"]) == N and int(row["nnz"]) == 64975
+    assert float(row["ms"]) > 0 and "checks passed" in err
+
+
+def test_runner_end_to_end_python_launcher(tmp_path):
+    """The batch runner (scripts/run_benchmarks.sh:1-64 contract) over two
+    MatrixMarket files and a generated graph at two widths, each run a child
+    process of the harness through PS_BENCH_LAUNCHER=python."""
+    data = tmp_path / "data"
+    data.mkdir()
+    (data / "small.mtx").write_text(SMALL_MTX)
+    (data / "rows40.mtx").write_text(dense_mtx(80, 300, 40))
+    manifest = tmp_path / "list.txt"
+    manifest.write_text("# two files and a generated graph\nsmall.mtx\nrows40.mtx\nsynth:C4:2:64\n")
+    out = tmp_path / "out" / "sddmm.csv"
+    env = dict(os.environ, DATASET_LIST=str(manifest), PS_BENCH_LAUNCHER="python")
+    rc, _, err = child([sys.executable, "-m", "powersparse_amd.cli.run_benchmarks",
+                        os.path.join(ROOT, "powersparse_amd"), data, "sddmm", 0, out, "32,64", 2,
+                        1], env=env)
+    assert rc == 0 and "Results saved to" in err
+    table = list(csv.DictReader(io.StringIO(out.read_text())))
+    assert [(os.path.basename(t["matrix"]), int(t["N"])) for t in table] == [
+        ("small.mtx", 32), ("small.mtx", 64), ("rows40.mtx", 32), ("rows40.mtx", 64),
+        ("synth:C4:2:64", 32), ("synth:C4:2:64", 64)]
+    assert all(t["check"] == "passed" and t["operator"] == "SDDMM" for t in table)
+    assert [int(t["nnz"]) for t in table[:4]] == [9, 9, 3200, 3200]

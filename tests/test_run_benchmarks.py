@@ -167,3 +167,35 @@ def test_module_entry_point(build, data, tmp_path):
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
     assert len(rows(out)) == 4
+
+
+def test_python_launcher(data, tmp_path, capsys):
+    """PS_BENCH_LAUNCHER=python: the in-tree harness library through
+    `python -m powersparse_amd.cli`; here (no GPU) the header is written and the
+    first run stops at opening the device, so the file stays partial and the
+    harness's exit status 1 is returned."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    package = os.path.join(root, "powersparse_amd")
+    if not os.path.exists(os.path.join(package, "lib", "libpowersparse_bench.so")):
+        pytest.skip("harness library not built")
+    out = tmp_path / "o.csv"
+    env = {"PS_BENCH_LAUNCHER": "python"}
+    try:
+        status = run([package, data, "spmm", "0", out, "32"], env=env)
+    finally:
+        os.environ.pop("PS_BENCH_LAUNCHER", None)
+    assert status == 1
+    assert not out.exists()
+    assert rows(tmp_path / "o.csv.partial")[0].startswith("algorithm,operator,matrix,")
+
+
+def test_launcher_errors(build, data, tmp_path, capsys):
+    try:
+        assert run([build, data, "spmm", "0", tmp_path / "o.csv"],
+                   env={"PS_BENCH_LAUNCHER": "python"}) == 1
+        assert "Missing library:" in capsys.readouterr().err
+        assert run([build, data, "spmm", "0", tmp_path / "o.csv"],
+                   env={"PS_BENCH_LAUNCHER": "shell"}) == 2
+        assert "Unknown PS_BENCH_LAUNCHER: shell" in capsys.readouterr().err
+    finally:
+        os.environ.pop("PS_BENCH_LAUNCHER", None)
