@@ -5,7 +5,7 @@
 //     groups of 32 when GS == 32);
 //   residue workset: 8 groups per wave, one slot per group, as stored or in
 //     the workset's run order (ps_workset.order); a slot loads its group's X
-//     row once, stages the group's columns in LDS and walks it 8 nonzeros at a
+//     row once, stages the group's columns and values in LDS and walks it 8 nonzeros at a
 //     time; in stored order the task's results (one contiguous output range)
 //     are collected in LDS and added with whole-wave atomics at the end.
 // Lanes form slots of 8; slot q owns 8 consecutive nonzeros and each lane of the
@@ -38,7 +38,7 @@ namespace ps {
 namespace {
 
 constexpr int kWavesPerBlock = 4;
-constexpr int kStage = 32;  // residue columns staged in LDS per slot
+constexpr int kStage = 32;  // residue columns (and values) staged in LDS per slot
 constexpr int kTaskOut = 256;  // residue results of one task collected in LDS
 // Longest XCD run of PS_TASK_CHUNK_AUTO (measured in the locality run order,
 // C3 N = 128: runs of 256 workgroups 1.4% faster than the round robin, 1024
@@ -127,6 +127,9 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
   constexpr int K = 32 * KQ;
   __shared__ __attribute__((aligned(16))) int stage[kWavesPerBlock][8 * kStage];
   __shared__ float task_out[kWavesPerBlock][kTaskOut];  // residue results of a task
+  // residue values staged with their columns (no dependent value load after
+  // each step's dots: C3 SDDMM N=128 6.303 -> 6.292 ms)
+  __shared__ __attribute__((aligned(16))) float stage_val[kWavesPerBlock][8 * kStage];
   const uint32_t blk = balanced_block(blockIdx.x, gridDim.x, args.chunk_log2);
   uint32_t task = __builtin_amdgcn_readfirstlane(blk * kWavesPerBlock + threadIdx.x / kWave);
   if (task >= args.launch_tasks) return;
@@ -159,6 +162,19 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     const int g = valid ? p0 >> gs_shift : 0;
     const int row = valid ? ws.group_des[g] : 0;
     int4 c0 = make_int4(0, 0, 0, 0), c1 = make_int4(0, 0, 0, 0);
+    // the lane's value, loaded with the column ids rather than after the dots
+    // (no dependent load at the end of the task: C3 SDDMM N=128 6.346 ->
+    // 6.297 ms)
+    const int pos = local * 64 + lane;
+    const float a_val = valid ? __builtin_nontemporal_load(ws.sp_data + pos) : 0.f;
+    // the output's index, also loaded up front in the mapped modes
+    int dst = pos;
+    if constexpr (kMode == 1) {
+      if (valid) dst = out_pos[pos];
+    } else if constexpr (kMode == 2) {
+      const int gl = pos >> gs_shift;
+      if (valid) dst = out_pos[gl] + (pos - gl * ws.group_size);
+    }
     if (valid) {
       // column ids and values are read once per launch: non-temporal, so that
       // they displace fewer of the L2's Y rows (C3 SDDMM N=128 6.71 -> 6.69 ms)
@@ -174,17 +190,11 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     for (int j = 0; j < 8; ++j) yoff[j] = Off(uint32_t(c[j])) * row_bytes + piece;
     slot_dots<KQ, kBuf>(Y, yoff, x, p);
     const float dot = slot_transpose_sum(p, sub);
-    const int pos = local * 64 + lane;
     if (valid) {
-      const float v = dot * __builtin_nontemporal_load(ws.sp_data + pos);
-      if constexpr (kMode == 1) {
-        out[out_pos[pos]] = v;
-      } else if constexpr (kMode == 2) {
-        const int gl = pos >> gs_shift;
-        out[out_pos[gl] + (pos - gl * ws.group_size)] = v;
-      } else {
-        out[pos] = v;
-      }
+      // every output is written once and not read back by the launch:
+      // non-temporal stores keep them from displacing Y rows in the L2 (C3
+      // SDDMM N=128 6.374 -> 6.348 ms)
+      __builtin_nontemporal_store(dot * a_val, out + dst);
     }
   } else {
     // One slot per group (the run order's entry local * 8 + slot: order[]
@@ -217,14 +227,18 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     for (int qq = 0; qq < KQ; ++qq)
       x[qq] = X.load(Off(uint32_t(row)) * row_bytes + piece + 128u * qq);
     // Groups of up to kStage nonzeros (all the preprocessing builds) have their
-    // columns staged in LDS, positions past the end holding the last column;
+    // columns and values staged in LDS, positions past the end holding the last;
     // longer groups read theirs directly.
     int* const cols_lds = stage[threadIdx.x / kWave] + slot * kStage;
+    float* const vals_lds = stage_val[threadIdx.x / kWave] + slot * kStage;
     const bool staged = len <= kStage;
     if (staged && len > 0) {
 #pragma unroll
-      for (int j = sub; j < kStage; j += 8)
-        cols_lds[j] = ws.col_ind[beg + (j < len ? j : len - 1)];
+      for (int j = sub; j < kStage; j += 8) {
+        const int at = beg + (j < len ? j : len - 1);
+        cols_lds[j] = ws.col_ind[at];
+        vals_lds[j] = ws.sp_data[at];
+      }
     }
     wave_lds_sync();
 #pragma unroll 1
@@ -250,7 +264,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
       const float dot = slot_transpose_sum(p, sub);
       const int k = c0 + sub;
       if (k < len) {
-        const float v = dot * ws.sp_data[beg + k];
+        const float v = dot * (staged ? vals_lds[k] : ws.sp_data[beg + k]);
         if constexpr (kMode == 2) {
           if (group_collect) res_lds[slot * kStage + k] = v;
           else if (args.residue_add) unsafeAtomicAdd(out + out_pos[g] + k, v);

@@ -280,7 +280,11 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs ar
       if (args.residue_atomic[g])
         atomic_row = row;
       else
-        *reinterpret_cast<float4*>(args.C + row * N + col0 + sub * 4) = acc;
+        // written once per launch: a non-temporal store keeps the row from
+        // displacing B rows in the L2 (C3 SpMM N=32 / 128: 1.594 / 5.674 ->
+        // 1.585 / 5.650 ms)
+        __builtin_nontemporal_store(fv4{acc.x, acc.y, acc.z, acc.w},
+                                    reinterpret_cast<fv4*>(args.C + row * N + col0 + sub * 4));
     }
     add_rows_atomic<LPN>(args.C, N, col0, my_lds, acc, atomic_row);
   }
