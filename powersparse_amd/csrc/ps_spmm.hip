@@ -299,6 +299,8 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs ar
 // 2.05 -> 2.03 and 2.23 -> 2.17 ms; one 128-float slice: 7.25 / 7.19 and
 // 2.13 / 2.19 ms), where in the first build's stored order the 32-float
 // slices had been faster (C1: 2.96 -> 2.53 ms against 128-float slices).
+// With the dense hub block they still win (C3 SpMM N=128: 5.65 ms against
+// 5.92 ms in 32-float slices and 5.88 ms in one 128-float slice).
 int pick_lpn(int N) { return spmm_lanes_per_row(N); }
 
 template <int LPN>
