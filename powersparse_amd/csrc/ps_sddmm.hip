@@ -122,6 +122,76 @@ __device__ __forceinline__ void slot_dots(const Rows<kBuf>& Y,
   }
 }
 
+// The full dot of nonzero `sub` of this lane's slot, whose 8 nonzeros have
+// the columns col_of(0 .. 7). Up to K = 256 the nonzeros are taken in pairs
+// (j, j + 4), P pairs per batch (the same loads in flight as slot_dots), and
+// each pair's partials pass the butterfly's first (xor 4) exchange at once, so
+// a lane keeps 4 partials instead of 8 and no row offsets (the same sums, bit
+// for bit): at K = 128 the kernel takes 69 VGPRs instead of 79, 7 waves per
+// SIMD instead of 6 (C3 SDDMM N=128 6.29 -> 6.26 ms; asked for 8 waves the
+// compiler spills 2 registers and the launch runs at 6.33 ms).
+template <int KQ, bool kBuf, typename ColOf>
+__device__ __forceinline__ float slot_dot(const Rows<kBuf>& Y, uint32_t row_bytes, uint32_t piece,
+                                          const float4 (&x)[KQ], int sub, ColOf col_of) {
+  using Off = typename Rows<kBuf>::Off;
+  if constexpr (KQ > 8) {
+    float p[8];
+    Off yoff[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) yoff[j] = Off(uint32_t(col_of(j))) * row_bytes + piece;
+    slot_dots<KQ, kBuf>(Y, yoff, x, p);
+    return slot_transpose_sum(p, sub);
+  } else {
+    constexpr int P = KQ <= 2 ? 4 : 1;  // pairs per batch: 8 KQ or 2 KQ loads in flight
+    const bool b2 = sub & 4, b1 = sub & 2, b0 = sub & 1;
+    float q[4];
+#pragma unroll
+    for (int i0 = 0; i0 < 4; i0 += P) {
+      float4 y[P][2][KQ];
+#pragma unroll
+      for (int u = 0; u < P; ++u) {
+        const Off o0 = Off(uint32_t(col_of(i0 + u))) * row_bytes + piece;
+        const Off o1 = Off(uint32_t(col_of(i0 + u + 4))) * row_bytes + piece;
+#pragma unroll
+        for (int k = 0; k < KQ; ++k) {
+          y[u][0][k] = Y.load(o0 + 128u * uint32_t(k));
+          y[u][1][k] = Y.load(o1 + 128u * uint32_t(k));
+        }
+      }
+      // keep the whole batch of loads in flight before the first use
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < P; ++u) {
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int k = 0; k < KQ; ++k) {
+          s0 = fmaf(x[k].x, y[u][0][k].x, s0);
+          s0 = fmaf(x[k].y, y[u][0][k].y, s0);
+          s0 = fmaf(x[k].z, y[u][0][k].z, s0);
+          s0 = fmaf(x[k].w, y[u][0][k].w, s0);
+          s1 = fmaf(x[k].x, y[u][1][k].x, s1);
+          s1 = fmaf(x[k].y, y[u][1][k].y, s1);
+          s1 = fmaf(x[k].z, y[u][1][k].z, s1);
+          s1 = fmaf(x[k].w, y[u][1][k].w, s1);
+        }
+        // slot_transpose_sum's first exchange for nonzeros i and i + 4
+        const float keep = b2 ? s1 : s0, send = b2 ? s0 : s1;
+        q[i0 + u] = keep + xor_shfl<4>(send);
+      }
+    }
+    float r[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const float keep = b1 ? q[i + 2] : q[i];
+      const float send = b1 ? q[i] : q[i + 2];
+      r[i] = keep + xor_shfl<2>(send);
+    }
+    const float keep = b0 ? r[1] : r[0];
+    const float send = b0 ? r[0] : r[1];
+    return keep + xor_shfl<1>(send);
+  }
+}
+
 template <int KQ, bool kBuf, int kMode>
 __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs args) {
   constexpr int K = 32 * KQ;
@@ -151,8 +221,7 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
   const uint32_t row_bytes = uint32_t(K) * 4u;
   const uint32_t piece = uint32_t(sub) * 16u;
   float4 x[KQ];
-  float p[8];
-  Off yoff[8];
+  int* const wave_stage = stage[threadIdx.x / kWave];
 
   if (ws.group_size > 0) {
     const int total = ws.group_num * ws.group_size;
@@ -161,12 +230,14 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     const int gs_shift = __builtin_ctz(unsigned(ws.group_size));  // a power of two
     const int g = valid ? p0 >> gs_shift : 0;
     const int row = valid ? ws.group_des[g] : 0;
-    int4 c0 = make_int4(0, 0, 0, 0), c1 = make_int4(0, 0, 0, 0);
-    // the lane's value, loaded with the column ids rather than after the dots
-    // (no dependent load at the end of the task: C3 SDDMM N=128 6.346 ->
-    // 6.297 ms)
+    // the lane's column id and value (one coalesced load each; the column ids
+    // go through the wave's LDS to their slots), loaded before the dots (no
+    // dependent load at the end of the task: C3 SDDMM N=128 6.346 -> 6.297 ms)
     const int pos = local * 64 + lane;
     const float a_val = valid ? __builtin_nontemporal_load(ws.sp_data + pos) : 0.f;
+    // column ids are read once per launch: non-temporal, so that they
+    // displace fewer of the L2's Y rows (C3 SDDMM N=128 6.71 -> 6.69 ms)
+    wave_stage[lane] = valid ? __builtin_nontemporal_load(ws.col_ind + pos) : 0;
     // the output's index, also loaded up front in the mapped modes
     int dst = pos;
     if constexpr (kMode == 1) {
@@ -175,21 +246,12 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
       const int gl = pos >> gs_shift;
       if (valid) dst = out_pos[gl] + (pos - gl * ws.group_size);
     }
-    if (valid) {
-      // column ids and values are read once per launch: non-temporal, so that
-      // they displace fewer of the L2's Y rows (C3 SDDMM N=128 6.71 -> 6.69 ms)
-      const iv4 x0 = __builtin_nontemporal_load(reinterpret_cast<const iv4*>(ws.col_ind + p0));
-      const iv4 x1 = __builtin_nontemporal_load(reinterpret_cast<const iv4*>(ws.col_ind + p0 + 4));
-      c0 = make_int4(x0.x, x0.y, x0.z, x0.w);
-      c1 = make_int4(x1.x, x1.y, x1.z, x1.w);
-    }
 #pragma unroll
     for (int q = 0; q < KQ; ++q) x[q] = X.load(Off(uint32_t(row)) * row_bytes + piece + 128u * q);
-    const int c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-#pragma unroll
-    for (int j = 0; j < 8; ++j) yoff[j] = Off(uint32_t(c[j])) * row_bytes + piece;
-    slot_dots<KQ, kBuf>(Y, yoff, x, p);
-    const float dot = slot_transpose_sum(p, sub);
+    wave_lds_sync();
+    const int* const slot_cols = wave_stage + slot * 8;
+    const float dot = slot_dot<KQ, kBuf>(Y, row_bytes, piece, x, sub,
+                                         [&](int j) { return slot_cols[j]; });
     if (valid) {
       // every output is written once and not read back by the launch:
       // non-temporal stores keep them from displacing Y rows in the L2 (C3
@@ -226,45 +288,32 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
 #pragma unroll
     for (int qq = 0; qq < KQ; ++qq)
       x[qq] = X.load(Off(uint32_t(row)) * row_bytes + piece + 128u * qq);
-    // Groups of up to kStage nonzeros (all the preprocessing builds) have their
-    // columns and values staged in LDS, positions past the end holding the last;
-    // longer groups read theirs directly.
+    // The group's columns and values pass through the slot's LDS area in
+    // chunks of kStage (one chunk for every group the preprocessing builds),
+    // positions past the group's end holding its last column (those
+    // nonzeros' dots are dropped); the chunk boundaries are the same for the
+    // whole wave (c0 is uniform).
     int* const cols_lds = stage[threadIdx.x / kWave] + slot * kStage;
     float* const vals_lds = stage_val[threadIdx.x / kWave] + slot * kStage;
-    const bool staged = len <= kStage;
-    if (staged && len > 0) {
-#pragma unroll
-      for (int j = sub; j < kStage; j += 8) {
-        const int at = beg + (j < len ? j : len - 1);
-        cols_lds[j] = ws.col_ind[at];
-        vals_lds[j] = ws.sp_data[at];
-      }
-    }
-    wave_lds_sync();
 #pragma unroll 1
     for (int c0 = 0; __any(c0 < len); c0 += 8) {
-      // nonzeros past the group's end re-read its last column and are dropped
-      int c[8];
-      if (staged && c0 < kStage) {
-        const int4 lo = *reinterpret_cast<const int4*>(cols_lds + c0);
-        const int4 hi = *reinterpret_cast<const int4*>(cols_lds + c0 + 4);
-        c[0] = lo.x; c[1] = lo.y; c[2] = lo.z; c[3] = lo.w;
-        c[4] = hi.x; c[5] = hi.y; c[6] = hi.z; c[7] = hi.w;
-      } else {
+      const int cs = c0 % kStage;  // place of nonzero c0 in the staged chunk
+      if (cs == 0) {
+        if (c0 > 0) wave_lds_sync();  // the previous chunk's reads come first
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = sub; j < kStage; j += 8) {
           const int k = c0 + j;
-          c[j] = len > 0 ? ws.col_ind[beg + (k < len ? k : len - 1)] : 0;
+          const int at = beg + (k < len ? k : len - 1);
+          cols_lds[j] = len > 0 ? ws.col_ind[at] : 0;
+          vals_lds[j] = len > 0 ? ws.sp_data[at] : 0.f;
         }
+        wave_lds_sync();
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        yoff[j] = len > 0 ? Off(uint32_t(c[j])) * row_bytes + piece : Off(piece);
-      slot_dots<KQ, kBuf>(Y, yoff, x, p);
-      const float dot = slot_transpose_sum(p, sub);
+      const float dot = slot_dot<KQ, kBuf>(Y, row_bytes, piece, x, sub,
+                                           [&](int j) { return cols_lds[cs + j]; });
       const int k = c0 + sub;
       if (k < len) {
-        const float v = dot * (staged ? vals_lds[k] : ws.sp_data[beg + k]);
+        const float v = dot * vals_lds[cs + sub];
         if constexpr (kMode == 2) {
           if (group_collect) res_lds[slot * kStage + k] = v;
           else if (args.residue_add) unsafeAtomicAdd(out + out_pos[g] + k, v);
