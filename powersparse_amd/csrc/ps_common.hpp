@@ -158,6 +158,8 @@ inline int task_chunk_log2(int task_chunk, uint64_t grid, int auto_max) {
   return l;
 }
 
+// cache-policy operand of the buffer loads: the non-temporal (slc) bit
+constexpr int kNonTemporal = 2;
 // 128-bit loads at byte offsets from a base: through a buffer resource with
 // 32-bit offsets when the whole array fits 4 GiB (Off = uint32_t), plain
 // global loads with 64-bit offsets otherwise (Off = uint64_t).
@@ -170,6 +172,14 @@ struct Rows {
     if constexpr (kBuf)
       rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(m), (short)0, int(bytes),
                                                0x00020000);
+  }
+  // the same load with the non-temporal hint: for rows read once, so that
+  // they displace fewer of the L2's reused lines
+  __device__ __forceinline__ float4 load_nt(Off off) const {
+    if constexpr (kBuf)
+      return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, kNonTemporal));
+    else
+      return __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const fv4*>(base + off)));
   }
   __device__ __forceinline__ float4 load(Off off) const {
     if constexpr (kBuf)

@@ -285,9 +285,13 @@ __global__ __launch_bounds__(kWave* kWavesPerBlock) void sddmm_kernel(SddmmArgs 
     // row-order copy (mode 2) adding its results: a group of up to kStage
     // results is collected in LDS and added with 32 lanes on its output range
     const bool group_collect = kMode == 2 && args.residue_add && len <= kStage;
+    // a residue group's X row is read by this task alone in the launch's
+    // order (the row's block tiles run long before): non-temporal (C3 SDDMM
+    // N=128 6.271 -> 6.254 ms, C4 N=64 1.358 -> 1.348 ms; the block tiles' X
+    // rows, shared by a hub row's tiles, measured 2% slower so)
 #pragma unroll
     for (int qq = 0; qq < KQ; ++qq)
-      x[qq] = X.load(Off(uint32_t(row)) * row_bytes + piece + 128u * qq);
+      x[qq] = X.load_nt(Off(uint32_t(row)) * row_bytes + piece + 128u * qq);
     // The group's columns and values pass through the slot's LDS area in
     // chunks of kStage (one chunk for every group the preprocessing builds),
     // positions past the group's end holding its last column (those
