@@ -5,16 +5,18 @@
 //     groups of 32 when GS == 32);
 //   residue workset: 8 groups per wave, one slot per group, as stored or in
 //     the workset's run order (ps_workset.order); a slot loads its group's X
-//     row once, stages the group's columns and values in LDS and walks it 8 nonzeros at a
-//     time; in stored order the task's results (one contiguous output range)
-//     are collected in LDS and added with whole-wave atomics at the end.
+//     row once, stages the group's columns and values in LDS and walks it 8
+//     nonzeros at a time; in stored order the task's results (one contiguous
+//     output range) are collected in LDS and added with whole-wave atomics
+//     at the end.
 // Lanes form slots of 8; slot q owns 8 consecutive nonzeros and each lane of the
 // slot holds K / 8 features of X (float4 pieces 32 floats apart, so a slot reads
-// a 128-byte line per piece). After the 8 partial dots per lane the slot does a
-// transposing butterfly (xor 4, 2, 1 via swizzle / DPP): each exchange halves the
-// number of partials a lane keeps, and at the end lane `sub` of slot `q` holds
-// the full dot of nonzero 8q + sub, so the wave's 64 results are stored with
-// one coalesced write.
+// a 128-byte line per piece). Each lane's 8 partial dots go through a
+// transposing butterfly (xor 4, 2, 1 via swizzle / DPP; the xor-4 exchange per
+// pair of nonzeros j, j + 4 as soon as their partials are summed): each
+// exchange halves the number of partials a lane keeps, and at the end lane
+// `sub` of slot `q` holds the full dot of nonzero 8q + sub, so the wave's 64
+// results are stored with one coalesced write.
 //
 // Reference behaviour kept (PowerSparse_SDDMM/sddmm_solution.cu:7-50,
 // sddmm_kernel_block.cu:155-164, sddmm_kernel_residue.cu:295-305): block
