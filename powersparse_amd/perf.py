@@ -67,9 +67,20 @@ def host_operand(rng, shape, config, op):
     return rng.uniform(a, b, shape).astype(np.float32)
 
 
+def code_text(source):
+    """The code of a C / C++ / HIP source: comments and blank lines removed and
+    runs of whitespace folded (the sources hold no comment markers inside
+    string literals)."""
+    source = re.sub(r"/\*.*?\*/", " ", source, flags=re.S)
+    source = re.sub(r"//[^\n]*", "", source)
+    lines = (" ".join(line.split()) for line in source.split("\n"))
+    return "\n".join(line for line in lines if line)
+
+
 def sources_digest(root=None):
-    """SHA-256 over the kernel sources and the C ABI header: ties a committed
-    profile summary to the kernels it measured."""
+    """SHA-256 over the code of the kernel sources and the C ABI header (their
+    comments left out): ties a committed profile summary to the kernels it
+    measured."""
     import glob
     import hashlib
     import os
@@ -81,8 +92,8 @@ def sources_digest(root=None):
     h = hashlib.sha256()
     for f in files:
         h.update(os.path.basename(f).encode())
-        with open(f, "rb") as fh:
-            h.update(fh.read())
+        with open(f, encoding="utf-8") as fh:
+            h.update(code_text(fh.read()).encode())
     return h.hexdigest()[:16]
 
 

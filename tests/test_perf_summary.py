@@ -212,3 +212,20 @@ def test_class_split_summary(tmp_path, capsys):
     manifest.write_text("\n".join(json.dumps(e) for e in entries) + "\n")
     with pytest.raises(SystemExit, match="dispatch counts differ"):
         perf.main(args)
+
+
+def test_sources_digest_follows_code_not_comments(tmp_path):
+    """The digest tying a profile summary to its kernel sources changes with
+    the code and not with comments, blank lines or indentation."""
+    def tree(text):
+        root = tmp_path / str(abs(hash(text)))
+        (root / "powersparse_amd" / "csrc").mkdir(parents=True)
+        (root / "include").mkdir()
+        (root / "powersparse_amd" / "csrc" / "k.hip").write_text(text)
+        (root / "include" / "powersparse_hip.h").write_text("int f(int);\n")
+        return perf.sources_digest(str(root))
+
+    base = tree("__global__ void k(float* p) {\n  p[0] = 1.f;  // one\n}\n")
+    assert tree("/* a kernel */\n__global__ void k(float* p) {\n\n    p[0] = 1.f;\n}\n") == base
+    assert tree("__global__ void k(float* p) {\n  p[0] = 2.f;  // one\n}\n") != base
+    assert perf.code_text("a; // b\n/* c\n d */ e  f;\n") == "a;\ne f;"
