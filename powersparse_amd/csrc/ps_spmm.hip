@@ -48,7 +48,10 @@
 namespace ps {
 namespace {
 
-constexpr int kWavesPerBlock = 4;
+// Waves per workgroup: 2 for 8-lane slots (32-float slices: C3 SpMM N=32
+// 1.586 -> 1.573 ms, C1 0.502 -> 0.497 ms against 4; 64-float slices run
+// best at 4: C3 N=128 5.654 ms against 5.711 at 2 and 5.734 at 8).
+constexpr int waves_per_block(int lpn) { return lpn == 8 ? 2 : 4; }
 constexpr int kPer = 32;          // nonzeros per slot per block tile
 constexpr int kSlotWords = 2 * kPer + 4;  // LDS words per slot (pairs + pad)
 // Longest XCD run of PS_TASK_CHUNK_AUTO (measured on the tuned SpMM partition,
@@ -128,7 +131,8 @@ __device__ __forceinline__ float group_sum(float v, int spg) {
 }
 
 template <int LPN, bool kBuf>
-__global__ __launch_bounds__(kWave* kWavesPerBlock) void spmm_kernel(SpmmArgs args) {
+__global__ __launch_bounds__(kWave* waves_per_block(LPN)) void spmm_kernel(SpmmArgs args) {
+  constexpr int kWavesPerBlock = waves_per_block(LPN);
   // the tile of kPer * SL nonzeros and the SL residue groups of a task are
   // spmm_task_shape(N)
   constexpr int SL = 64 / LPN;
@@ -305,7 +309,7 @@ int pick_lpn(int N) { return spmm_lanes_per_row(N); }
 
 template <int LPN>
 void launch_lpn(const SpmmArgs& a, bool buf, unsigned grid, hipStream_t stream) {
-  const dim3 block(kWave * kWavesPerBlock);
+  const dim3 block(kWave * waves_per_block(LPN));
   if (buf) spmm_kernel<LPN, true><<<grid, block, 0, stream>>>(a);
   else spmm_kernel<LPN, false><<<grid, block, 0, stream>>>(a);
 }
@@ -370,7 +374,8 @@ int launch(int count, const int* order, const ps_workset* worksets, const int* r
   tasks *= uint64_t(a.slices);
   PS_CHECK_ARG(tasks < (1ull << 31), "SpMM task count exceeds the launch range");
   a.total_tasks = uint32_t(tasks);
-  const unsigned grid = unsigned((tasks + kWavesPerBlock - 1) / kWavesPerBlock);
+  const unsigned wpb = unsigned(waves_per_block(lpn));
+  const unsigned grid = unsigned((tasks + wpb - 1) / wpb);
   a.chunk_log2 = uint32_t(task_chunk_log2(task_chunk, grid, kAutoChunkMax));
   switch (lpn) {
     case 8: launch_lpn<8>(a, buf, grid, stream); break;
