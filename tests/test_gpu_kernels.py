@@ -191,7 +191,8 @@ def test_long_residue_groups(kind):
     d_off = ps.DeviceBuffer(host=offsets)
     d_atomic = ps.DeviceBuffer.zeros(rows)
     say(f"long residue groups order={kind} rows={rows} nnz={nnz} max={lens.max()}")
-    for N in (32, 64, 96):
+    # the SDDMM kernel's paired dots (K up to 256) and its unpaired form (K = 320)
+    for N in (32, 64, 96, 128, 320):
         B = rng.uniform(-1, 1, (cols, N)).astype(np.float32)
         dB = ps.DeviceBuffer(host=B)
         dC = ps.DeviceBuffer.zeros(rows * N * 4)
