@@ -126,12 +126,11 @@ __device__ __forceinline__ void slot_dots(const Rows<kBuf>& Y,
 
 // The full dot of nonzero `sub` of this lane's slot, whose 8 nonzeros have
 // the columns col_of(0 .. 7). Up to K = 256 the nonzeros are taken in pairs
-// (j, j + 4), P pairs per batch (the same loads in flight as slot_dots), and
-// each pair's partials pass the butterfly's first (xor 4) exchange at once, so
-// a lane keeps 4 partials instead of 8 and no row offsets (the same sums, bit
-// for bit): at K = 128 the kernel takes 69 VGPRs instead of 79, 7 waves per
-// SIMD instead of 6 (C3 SDDMM N=128 6.29 -> 6.26 ms; asked for 8 waves the
-// compiler spills 2 registers and the launch runs at 6.33 ms).
+// (j, j + 4), P pairs per batch, and each pair's partials pass the
+// butterfly's first (xor 4) exchange at once, so a lane keeps 4 partials
+// instead of 8 and no row offsets (the same sums, bit for bit; with one pair
+// per batch the K = 128 kernel took 69 VGPRs instead of 79 and ran C3 SDDMM
+// N=128 in 6.26 instead of 6.29 ms).
 template <int KQ, bool kBuf, typename ColOf>
 __device__ __forceinline__ float slot_dot(const Rows<kBuf>& Y, uint32_t row_bytes, uint32_t piece,
                                           const float4 (&x)[KQ], int sub, ColOf col_of) {
@@ -144,7 +143,12 @@ __device__ __forceinline__ float slot_dot(const Rows<kBuf>& Y, uint32_t row_byte
     slot_dots<KQ, kBuf>(Y, yoff, x, p);
     return slot_transpose_sum(p, sub);
   } else {
-    constexpr int P = KQ <= 2 ? 4 : 1;  // pairs per batch: 8 KQ or 2 KQ loads in flight
+    // pairs per batch: 8 KQ loads in flight up to K = 64, 16 at K = 128
+    // (C3 SDDMM N=128 6.234 -> 6.195 ms, C1 2.250 -> 2.230 ms against 8
+    // loads, although the kernel then holds 100 VGPRs, 4 waves per SIMD; 32
+    // loads: 6.494 ms; K = 64 with 8 loads instead of 16: C4 1.347 -> 1.372
+    // ms), 2 KQ otherwise
+    constexpr int P = KQ <= 2 ? 4 : (KQ == 4 ? 2 : 1);
     const bool b2 = sub & 4, b1 = sub & 2, b0 = sub & 1;
     float q[4];
 #pragma unroll
